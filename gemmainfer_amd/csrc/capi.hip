@@ -1,0 +1,208 @@
+// extern "C" entry points declared in include/gemmainfer_amd.h: argument
+// checks, dtype dispatch and error reporting around the gfx950 kernels.
+
+#include <string>
+
+#include "../../include/gemmainfer_amd.h"
+#include "gi_internal.h"
+
+namespace gi {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  g_last_error = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
+  return GI_ERR_HIP;
+}
+
+int device_cu_count() {
+  static int cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+}  // namespace gi
+
+using gi::fail;
+
+namespace {
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+int check_idx_dtype(int dt) {
+  if (dt != GI_DTYPE_INT32 && dt != GI_DTYPE_INT64)
+    return fail(GI_ERR_UNSUPPORTED, "expert ids must be int32 or int64");
+  return GI_OK;
+}
+
+int check_bf16_x(int dt, const char* who) {
+  if (dt != GI_DTYPE_BF16)
+    return fail(GI_ERR_UNSUPPORTED,
+                std::string(who) + ": only bf16 activations/scales are implemented on gfx950");
+  return GI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gi_last_error(void) { return gi::g_last_error.c_str(); }
+
+int gi_abi_version(void) { return 1; }
+
+int gi_moe_route_topk_softmax(const void* logits, int logits_dtype, const float* expert_scale,
+                              int M, int E, int top_k, int32_t* out_idx, void* out_w,
+                              int w_dtype, void* stream) {
+  return gi::launch_route(logits, logits_dtype, expert_scale, M, E, top_k, out_idx, out_w,
+                          w_dtype, as_stream(stream));
+}
+
+int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
+                 int32_t* unique_experts, int32_t* num_unique, int32_t* slot_to_unique,
+                 int32_t* offsets, int32_t* slots, void* stream) {
+  int st = check_idx_dtype(idx_dtype);
+  if (st != GI_OK) return st;
+  return gi::launch_moe_align(idx, idx_dtype == GI_DTYPE_INT64, M, top_k, E, unique_experts,
+                              num_unique, slot_to_unique, offsets, slots, as_stream(stream));
+}
+
+size_t gi_fused_moe_workspace_bytes(int M, int top_k, int H, int I, int E) {
+  if (top_k <= 0 || H <= 0 || I <= 0 || E <= 0) return 0;
+  return gi::moe_workspace_bytes(M, top_k, H, I, E);
+}
+
+int gi_fused_batched_moe(const void* x, int x_dtype, const int32_t* gu_packed,
+                         const void* gu_scales, int gu_groups, const int32_t* d_packed,
+                         const void* d_scales, int d_groups, const void* idx, int idx_dtype,
+                         const void* w, int w_dtype, void* out, int M, int H, int I, int E,
+                         int top_k, int group_size, void* workspace, size_t workspace_bytes,
+                         int spin_limit, void* stream) {
+  int st = check_bf16_x(x_dtype, "fused_batched_moe");
+  if (st != GI_OK) return st;
+  st = check_idx_dtype(idx_dtype);
+  if (st != GI_OK) return st;
+  if (w_dtype != GI_DTYPE_BF16 && w_dtype != GI_DTYPE_FP16 && w_dtype != GI_DTYPE_FP32)
+    return fail(GI_ERR_UNSUPPORTED, "fused_batched_moe: expert weights must be bf16, fp16 or fp32");
+  gi::MoeHostArgs a{};
+  a.x = x;
+  a.gu_packed = gu_packed;
+  a.gu_scales = gu_scales;
+  a.d_packed = d_packed;
+  a.d_scales = d_scales;
+  a.idx = idx;
+  a.idx_is64 = idx_dtype == GI_DTYPE_INT64;
+  a.w = w;
+  a.w_dtype = w_dtype;
+  a.out = out;
+  a.M = M;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.top_k = top_k;
+  a.gs = group_size;
+  a.Ggu = gu_groups;
+  a.Gd = d_groups;
+  a.overwrite = 0;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.spin_limit = spin_limit;
+  a.stream = as_stream(stream);
+  return gi::launch_fused_moe(a);
+}
+
+int gi_moe_layer_from_logits(const void* x, int x_dtype, const void* logits, int logits_dtype,
+                             const float* expert_scale, const int32_t* gu_packed,
+                             const void* gu_scales, int gu_groups, const int32_t* d_packed,
+                             const void* d_scales, int d_groups, void* out, int32_t* out_idx,
+                             void* out_w, int M, int H, int I, int E, int top_k,
+                             int group_size, void* workspace, size_t workspace_bytes,
+                             int spin_limit, void* stream) {
+  int st = check_bf16_x(x_dtype, "moe_layer_from_logits");
+  if (st != GI_OK) return st;
+  if (logits_dtype != GI_DTYPE_BF16 && logits_dtype != GI_DTYPE_FP32)
+    return fail(GI_ERR_UNSUPPORTED, "moe_layer_from_logits: logits must be bf16 or fp32");
+  if (!logits) return fail(GI_ERR_INVALID_ARG, "moe_layer_from_logits: null logits");
+  if (top_k > E) return fail(GI_ERR_INVALID_ARG, "moe_layer_from_logits: top_k > number of experts");
+  gi::MoeHostArgs a{};
+  a.x = x;
+  a.gu_packed = gu_packed;
+  a.gu_scales = gu_scales;
+  a.d_packed = d_packed;
+  a.d_scales = d_scales;
+  a.logits = logits;
+  a.logits_dtype = logits_dtype;
+  a.expert_scale = expert_scale;
+  a.out_idx = out_idx;
+  a.out_w = out_w;
+  a.out = out;
+  a.M = M;
+  a.H = H;
+  a.I = I;
+  a.E = E;
+  a.top_k = top_k;
+  a.gs = group_size;
+  a.Ggu = gu_groups;
+  a.Gd = d_groups;
+  a.overwrite = 1;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  a.spin_limit = spin_limit;
+  a.stream = as_stream(stream);
+  return gi::launch_fused_moe(a);
+}
+
+int gi_workspace_status(void* workspace, size_t workspace_bytes, int32_t* host_status,
+                        void* stream) {
+  if (workspace_bytes < sizeof(int32_t))
+    return fail(GI_ERR_WORKSPACE, "workspace_status: workspace too small");
+  return gi::read_workspace_status(workspace, host_status, as_stream(stream));
+}
+
+size_t gi_w4a16_workspace_bytes(int M, int K, int N, int group_size) {
+  return gi::w4a16_workspace_bytes(M, K, N, group_size);
+}
+
+int gi_w4a16_linear(const void* A, int a_dtype, const int32_t* B_packed, const void* scales,
+                    int n_groups, void* C, int M, int K, int N, int group_size, float softcap,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_bf16_x(a_dtype, "w4a16_linear");
+  if (st != GI_OK) return st;
+  return gi::launch_w4a16(A, B_packed, scales, n_groups, C, M, K, N, group_size, softcap,
+                          workspace, workspace_bytes, as_stream(stream));
+}
+
+int gi_softcap_inplace(void* x, int dtype, int64_t n, float cap, void* stream) {
+  return gi::launch_softcap(x, dtype, n, cap, as_stream(stream));
+}
+
+int gi_rmsnorm(const void* in, const void* weight, void* out, int dtype, int64_t rows,
+               int hidden, float eps, int add_unit_offset, void* stream) {
+  return gi::launch_rmsnorm(in, weight, out, dtype, rows, hidden, eps, add_unit_offset,
+                            as_stream(stream));
+}
+
+int gi_rope_inplace(void* q, void* k, const void* cos_t, const void* sin_t,
+                    const int64_t* position_ids, int dtype, int B, int Hq, int Hk, int S, int D,
+                    int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t k_sb, int64_t k_sh,
+                    int64_t k_ss, void* stream) {
+  const int64_t qs[3] = {q_sb, q_sh, q_ss};
+  const int64_t ks[3] = {k_sb, k_sh, k_ss};
+  return gi::launch_rope(q, k, cos_t, sin_t, position_ids, dtype, B, Hq, Hk, S, D, qs, ks,
+                         as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// Device helpers shared by the gfx950 kernels of the W4A16 MoE path.
+//
+// Conventions
+//   * bf16 values travel as uint16_t bit patterns; arithmetic is fp32.
+//   * int4 weights: nibble i of a packed int32 word holds the code q of row
+//     k = 8*pk + i; the weight is (q - 8) * scale (reference quant.py:41-43,
+//     marlin.cu:75-76).
+//   * Activations used against packed words are staged "pair-permuted": the 8
+//     bf16 values x0..x7 of one packed row are stored as the four dwords
+//     (x0|x4), (x1|x5), (x2|x6), (x3|x7) so that one v_dot2_f32_bf16 consumes
+//     the two codes that a single mask-and-or extracts from the word.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gi {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal hint: weights are read once).
+__device__ __forceinline__ uint4 load_nt_u4(const void* p) {
+  u32x4_t v = __builtin_nontemporal_load((const u32x4_t*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bit pattern (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float round_to_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+__device__ __forceinline__ float fp16_to_f32(uint16_t bits) {
+  _Float16 h = __builtin_bit_cast(_Float16, bits);
+  return (float)h;
+}
+
+// Load one routing weight of dtype code `dt` (0 bf16, 1 fp16, 2 fp32) and
+// round it to bf16, the activation dtype (the reference casts the weights to
+// x's dtype, marlin.cu:634-636).
+__device__ __forceinline__ float load_weight_as_bf16(const void* w, int dt, int i) {
+  float v;
+  if (dt == 0) v = bf16_to_f32(((const uint16_t*)w)[i]);
+  else if (dt == 1) v = fp16_to_f32(((const uint16_t*)w)[i]);
+  else v = ((const float*)w)[i];
+  return round_to_bf16(v);
+}
+
+__device__ __forceinline__ int load_expert_id(const void* idx, int is64, int i) {
+  if (is64) {
+    long long v = ((const long long*)idx)[i];
+    return (v < -2147483647LL || v > 2147483647LL) ? -1 : (int)v;
+  }
+  return ((const int*)idx)[i];
+}
+
+// Pair-permute 8 consecutive bf16 values (as 4 dwords d0..d3 = x0x1, x2x3,
+// x4x5, x6x7) into (x0|x4), (x1|x5), (x2|x6), (x3|x7).
+__device__ __forceinline__ uint4 pair_permute(uint4 d) {
+  uint4 p;
+  p.x = __builtin_amdgcn_perm(d.z, d.x, 0x05040100u);
+  p.y = __builtin_amdgcn_perm(d.z, d.x, 0x07060302u);
+  p.z = __builtin_amdgcn_perm(d.w, d.y, 0x05040100u);
+  p.w = __builtin_amdgcn_perm(d.w, d.y, 0x07060302u);
+  return p;
+}
+
+// -136 * sum of the 8 bf16 values in d: the bias that turns sum x*(128+q)
+// into sum x*(q-8) (see dot8_q4).
+__device__ __forceinline__ float neg_bias_136(uint4 d) {
+  float s = bf16_to_f32(d.x & 0xffffu) + bf16_to_f32(d.x >> 16) +
+            bf16_to_f32(d.y & 0xffffu) + bf16_to_f32(d.y >> 16) +
+            bf16_to_f32(d.z & 0xffffu) + bf16_to_f32(d.z >> 16) +
+            bf16_to_f32(d.w & 0xffffu) + bf16_to_f32(d.w >> 16);
+  return -136.0f * s;
+}
+
+__device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
+// sum_{i<8} x_i * (q_i - 8) for one packed word, given pair-permuted x and
+// bias = -136 * sum x_i.  OR-ing a code into 0x4300 (bf16 128.0, ulp 1)
+// yields the exact bf16 value 128 + q, so two codes per mask-and-or feed one
+// v_dot2_f32_bf16; the bias removes the 136 = 128 + 8 offset.
+__device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias) {
+  const uint32_t m = 0x000F000Fu, mag = 0x43004300u;
+  float d = fdot2(xp.x, (w & m) | mag, bias);
+  d = fdot2(xp.y, ((w >> 4) & m) | mag, d);
+  d = fdot2(xp.z, ((w >> 8) & m) | mag, d);
+  d = fdot2(xp.w, ((w >> 12) & m) | mag, d);
+  return d;
+}
+
+__device__ __forceinline__ float bf16lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+
+// Sum over the lanes that share (lane & (group-1)) within a wave: i.e. reduce
+// across lane bits log2(group)..5.  Every lane ends with its group's total.
+template <int kGroup>
+__device__ __forceinline__ float reduce_across_groups(float v) {
+#pragma unroll
+  for (int off = kGroup; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// ---- inter-workgroup signalling (agent scope) -----------------------------
+__device__ __forceinline__ int atomic_add_release(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int atomic_add_acq_rel(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_acquire(int* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_relaxed(int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_relaxed(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void fence_acquire_agent() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))  (reference marlin.cu:7-11)
+  float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
+  return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+}  // namespace gi

@@ -1,0 +1,71 @@
+// Host-side declarations shared between the C-ABI layer (capi.cpp) and the
+// kernel translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace gi {
+
+// Sets the thread-local error message and returns `code`.
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+// Multiprocessor count of the current device (cached per device).
+int device_cu_count();
+
+// ---- fused MoE --------------------------------------------------------------
+struct MoeHostArgs {
+  const void* x;
+  const int32_t* gu_packed;
+  const void* gu_scales;
+  const int32_t* d_packed;
+  const void* d_scales;
+  const void* idx;
+  int idx_is64;
+  const void* w;
+  int w_dtype;
+  const void* logits;       // layer mode when non-null
+  int logits_dtype;         // 0 bf16, 2 fp32
+  const float* expert_scale;
+  int32_t* out_idx;
+  void* out_w;
+  void* out;
+  int M, H, I, E, top_k, gs, Ggu, Gd;
+  int overwrite;
+  void* workspace;
+  size_t workspace_bytes;
+  int spin_limit;
+  hipStream_t stream;
+};
+
+// Largest number of token rows one fused launch handles (S = rows*top_k <= 256).
+int moe_rows_per_launch(int top_k);
+size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E);
+int launch_fused_moe(const MoeHostArgs& a);
+int launch_moe_align(const void* idx, int is64, int M, int top_k, int E, int32_t* uniq,
+                     int32_t* nuniq, int32_t* s2u, int32_t* offsets, int32_t* slots,
+                     hipStream_t stream);
+int launch_route(const void* logits, int logits_dtype, const float* expert_scale, int M,
+                 int E, int top_k, int32_t* out_idx, void* out_w, int w_dtype,
+                 hipStream_t stream);
+int read_workspace_status(void* workspace, int32_t* host_status, hipStream_t stream);
+
+// ---- W4A16 linear -------------------------------------------------------------
+size_t w4a16_workspace_bytes(int M, int K, int N, int gs);
+int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_groups, void* C,
+                 int M, int K, int N, int gs, float softcap, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream);
+
+// ---- companions -------------------------------------------------------------
+int launch_softcap(void* x, int dtype, int64_t n, float cap, hipStream_t stream);
+int launch_rmsnorm(const void* in, const void* weight, void* out, int dtype, int64_t rows,
+                   int hidden, float eps, int add_unit_offset, hipStream_t stream);
+int launch_rope(void* q, void* k, const void* cos_t, const void* sin_t,
+                const int64_t* pos, int dtype, int B, int Hq, int Hk, int S, int D,
+                const int64_t* q_strides, const int64_t* k_strides, hipStream_t stream);
+
+}  // namespace gi

@@ -1,0 +1,273 @@
+// W4A16 linear C[M, N] = A[M, K] @ dequant(B) on gfx950, with an optional
+// fused final-logit softcap epilogue (lm_head).
+//
+// Reference behaviour restated (paths relative to the GemmaInfer repo):
+//   csrc/marlin.cu:704-856 launch_marlin_w4a16 (split-K / tiled / coalesced
+//   kernels at :13-260), csrc/pybind.cpp:46-85 (CPU semantics),
+//   gemmainfer/models/gemma.py:351-357 + csrc/softcapping.cu:7-19 (epilogue).
+//
+// One kernel for every shape: a workgroup owns 64 output columns and one
+// K-slice of the packed rows.  Lane (rsub = lane>>4, colq = lane&15) loads
+// 16-byte words of 4 adjacent columns, four packed rows per wave per load, so
+// one wave instruction reads 4 rows x 256 contiguous bytes.  Weights stream
+// through registers in batches of 8 row-steps with the next batch's loads in
+// flight while the current one is reduced.  When the grid would be too small
+// to fill 256 CUs (narrow N), K is split; the slices write fp32 partials and
+// the last slice to arrive for a column tile sums them in slice order (a
+// deterministic reduction -- the reference zeroes C and adds bf16 atomics,
+// marlin.cu:201,777).  Token rows are processed NT at a time over the same
+// weight stream.
+
+#include <mutex>
+
+#include "../../include/gemmainfer_amd.h"
+#include "gi_common.h"
+#include "gi_internal.h"
+
+namespace gi {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kCols = 64;           // output columns per workgroup
+constexpr int kRowsPerStep = 16;    // packed rows per step (4 waves x 4 lane rows)
+constexpr int kBatch = 8;           // steps per register batch
+constexpr int kTargetWgs = 1024;    // split K until the grid reaches this many workgroups
+
+struct GemvArgs {
+  const uint16_t* A;     // [M, K] bf16
+  const int32_t* B;      // [K/8, N]
+  const uint16_t* S;     // [G, N] bf16
+  uint16_t* C;           // [M, N] bf16
+  float* part;           // [ks, M, N] fp32 (ks > 1)
+  int* ctr;              // [n_tiles] (ks > 1)
+  int M, K, N, gs, G;
+  int ks, rows_per_split, stage_stride;
+  float cap;             // > 0: C = cap * tanh(y / cap)
+};
+
+__device__ __forceinline__ float epilogue(float y, float cap) {
+  return cap > 0.f ? cap * tanhf(y / cap) : y;
+}
+
+template <int NT>
+__global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
+  extern __shared__ uint4 dyn[];
+  __shared__ float red[kWaves * NT * kCols];
+  __shared__ int last;
+  uint4* xs = dyn;
+  float* xb = (float*)(dyn + NT * a.stage_stride);
+
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int rsub = lane >> 4, colq = lane & 15;
+  const int tile = blockIdx.x, split = blockIdx.y;
+  const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  const int r_begin = split * a.rows_per_split;
+  const int r_end = min(Kp, r_begin + a.rows_per_split);
+  const int nrows = max(0, r_end - r_begin);
+  const int col = tile * kCols + colq * 4;
+  const bool col_ok = col < a.N;
+  const int steps = (nrows + kRowsPerStep - 1) / kRowsPerStep;
+  const int nbatch = (steps + kBatch - 1) / kBatch;
+
+  for (int t0 = 0; t0 < a.M; t0 += NT) {
+    const int nch = min(NT, a.M - t0);
+    __syncthreads();  // previous chunk's LDS readers are done
+    for (int i = tid; i < nch * nrows; i += kThreads) {
+      const int n = i / nrows, r = i - n * nrows;
+      const uint4 d = *(const uint4*)(a.A + (size_t)(t0 + n) * a.K + 8 * (r_begin + r));
+      xs[n * a.stage_stride + r] = pair_permute(d);
+      xb[n * a.stage_stride + r] = neg_bias_136(d);
+    }
+    __syncthreads();
+
+    float acc[4][NT];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
+
+    uint4 wcur[kBatch];
+    uint2 scur[kBatch];
+    auto load_batch = [&](int b, uint4* w, uint2* s) {
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int rl = (b * kBatch + j) * kRowsPerStep + wave * 4 + rsub;  // local row
+        const int r = r_begin + rl;
+        const int g = r / rpg;
+        if (col_ok && rl < nrows && g < a.G) {
+          w[j] = load_nt_u4(a.B + (size_t)r * a.N + col);
+          s[j] = *(const uint2*)(a.S + (size_t)g * a.N + col);
+        } else {
+          w[j] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+          s[j] = make_uint2(0u, 0u);
+        }
+      }
+    };
+    if (nbatch > 0) load_batch(0, wcur, scur);
+    for (int b = 0; b < nbatch; ++b) {
+      uint4 wnxt[kBatch];
+      uint2 snxt[kBatch];
+      if (b + 1 < nbatch) load_batch(b + 1, wnxt, snxt);
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        const int rl = (b * kBatch + j) * kRowsPerStep + wave * 4 + rsub;
+        if (rl < nrows) {
+          const float sv[4] = {bf16lo(scur[j].x), bf16hi(scur[j].x), bf16lo(scur[j].y),
+                               bf16hi(scur[j].y)};
+          const uint32_t wv[4] = {wcur[j].x, wcur[j].y, wcur[j].z, wcur[j].w};
+#pragma unroll
+          for (int n = 0; n < NT; ++n) {
+            if (n < nch) {
+              const uint4 xp = xs[n * a.stage_stride + rl];
+              const float bias = xb[n * a.stage_stride + rl];
+#pragma unroll
+              for (int q = 0; q < 4; ++q) acc[q][n] += sv[q] * dot8_q4(wv[q], xp, bias);
+            }
+          }
+        }
+      }
+      if (b + 1 < nbatch) {
+#pragma unroll
+        for (int j = 0; j < kBatch; ++j) {
+          wcur[j] = wnxt[j];
+          scur[j] = snxt[j];
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[q][n] = reduce_across_groups<16>(acc[q][n]);
+    if (rsub == 0) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) red[(wave * NT + n) * kCols + colq * 4 + q] = acc[q][n];
+    }
+    __syncthreads();
+    for (int i = tid; i < nch * kCols; i += kThreads) {
+      const int n = i / kCols, cc = i - n * kCols;
+      const int oc = tile * kCols + cc;
+      if (oc < a.N) {
+        float y = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) y += red[(w * NT + n) * kCols + cc];
+        const size_t o = (size_t)(t0 + n) * a.N + oc;
+        if (a.ks == 1) a.C[o] = f32_to_bf16(epilogue(y, a.cap));
+        else a.part[(size_t)split * a.M * a.N + o] = y;
+      }
+    }
+  }
+  if (a.ks == 1) return;
+
+  // Last K-slice to arrive for this column tile reduces the partials in order.
+  __syncthreads();
+  if (tid == 0) last = atomic_add_acq_rel(&a.ctr[tile], 1) == a.ks - 1;
+  __syncthreads();
+  if (!last) return;
+  for (int i = tid; i < a.M * kCols; i += kThreads) {
+    const int t = i / kCols, cc = i - t * kCols;
+    const int oc = tile * kCols + cc;
+    if (oc < a.N) {
+      const size_t o = (size_t)t * a.N + oc;
+      float y = 0.f;
+      for (int s = 0; s < a.ks; ++s) y += a.part[(size_t)s * a.M * a.N + o];
+      a.C[o] = f32_to_bf16(epilogue(y, a.cap));
+    }
+  }
+  if (tid == 0) store_relaxed(&a.ctr[tile], 0);
+}
+
+constexpr size_t kAlign = 256;
+inline size_t round_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+struct Plan {
+  int ks, rows_per_split, tiles, nt;
+  size_t ctr_off, part_off, total;
+};
+
+Plan make_plan(int M, int K, int N) {
+  Plan p;
+  const int Kp = K >> 3;
+  p.tiles = (N + kCols - 1) / kCols;
+  p.nt = M <= 1 ? 1 : (M <= 4 ? 4 : 8);
+  int ks = (kTargetWgs + p.tiles - 1) / p.tiles;
+  const int max_ks = (Kp + kRowsPerStep - 1) / kRowsPerStep;
+  if (ks > max_ks) ks = max_ks;
+  if (ks < 1) ks = 1;
+  // rows per split: a whole number of 16-row steps
+  int rps = (Kp + ks - 1) / ks;
+  rps = (rps + kRowsPerStep - 1) / kRowsPerStep * kRowsPerStep;
+  ks = (Kp + rps - 1) / rps;
+  // x staging must fit in 64 KB of LDS
+  while ((size_t)p.nt * rps * (sizeof(uint4) + sizeof(float)) > 56 * 1024 && rps > kRowsPerStep) {
+    ks *= 2;
+    rps = (Kp + ks - 1) / ks;
+    rps = (rps + kRowsPerStep - 1) / kRowsPerStep * kRowsPerStep;
+    ks = (Kp + rps - 1) / rps;
+  }
+  p.ks = ks;
+  p.rows_per_split = rps;
+  p.ctr_off = 0;
+  p.part_off = round_up((size_t)p.tiles * sizeof(int));
+  p.total = ks > 1 ? round_up(p.part_off + (size_t)ks * M * N * sizeof(float)) : 0;
+  return p;
+}
+
+}  // namespace
+
+size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
+  (void)gs;
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  return make_plan(M, K, N).total;
+}
+
+int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_groups, void* C,
+                 int M, int K, int N, int gs, float softcap, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
+  if (M < 0 || K <= 0 || N <= 0) return fail(GI_ERR_INVALID_ARG, "w4a16: K and N must be positive, M >= 0");
+  if (K % 8) return fail(GI_ERR_INVALID_ARG, "w4a16: K must be a multiple of 8 (8 codes per int32)");
+  if (N % 4) return fail(GI_ERR_UNSUPPORTED, "w4a16: N must be a multiple of 4");
+  if (gs <= 0 || gs % 8) return fail(GI_ERR_INVALID_ARG, "w4a16: group_size must be a positive multiple of 8");
+  if (n_groups <= 0) return fail(GI_ERR_INVALID_ARG, "w4a16: scales need at least one group");
+  if (!A || !B || !scales || !C) return fail(GI_ERR_INVALID_ARG, "w4a16: null tensor pointer");
+  if ((((uintptr_t)A) | ((uintptr_t)B)) % 16)
+    return fail(GI_ERR_INVALID_ARG, "w4a16: A and B_packed must be 16-byte aligned");
+  if (((uintptr_t)scales) % 8) return fail(GI_ERR_INVALID_ARG, "w4a16: scales must be 8-byte aligned");
+  if (M == 0) return GI_OK;
+  const Plan p = make_plan(M, K, N);
+  if (p.ks > 1) {
+    if (!workspace || workspace_bytes < p.total)
+      return fail(GI_ERR_WORKSPACE, "w4a16: workspace missing or smaller than gi_w4a16_workspace_bytes()");
+    if (((uintptr_t)workspace) % kAlign)
+      return fail(GI_ERR_WORKSPACE, "w4a16: workspace must be 256-byte aligned");
+  }
+  GemvArgs k{};
+  k.A = (const uint16_t*)A;
+  k.B = B;
+  k.S = (const uint16_t*)scales;
+  k.C = (uint16_t*)C;
+  k.ctr = p.ks > 1 ? (int*)((char*)workspace + p.ctr_off) : nullptr;
+  k.part = p.ks > 1 ? (float*)((char*)workspace + p.part_off) : nullptr;
+  k.M = M;
+  k.K = K;
+  k.N = N;
+  k.gs = gs;
+  k.G = n_groups;
+  k.ks = p.ks;
+  k.rows_per_split = p.rows_per_split;
+  k.stage_stride = p.rows_per_split;
+  k.cap = softcap;
+  const size_t dyn = (size_t)p.nt * p.rows_per_split * (sizeof(uint4) + sizeof(float));
+  const dim3 grid(p.tiles, p.ks);
+  if (p.nt == 1) hipLaunchKernelGGL(w4a16_kernel<1>, grid, dim3(kThreads), dyn, stream, k);
+  else if (p.nt == 4) hipLaunchKernelGGL(w4a16_kernel<4>, grid, dim3(kThreads), dyn, stream, k);
+  else hipLaunchKernelGGL(w4a16_kernel<8>, grid, dim3(kThreads), dyn, stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
+  return GI_OK;
+}
+
+}  // namespace gi

@@ -1,0 +1,170 @@
+/*
+ * gemmainfer_amd.h -- C ABI of the MI355X (gfx950) Token-Union W4A16 MoE path.
+ *
+ * Plain C: pointers, sizes and int status codes; no torch or HIP types in the
+ * signatures (a stream is passed as ``void*`` holding a hipStream_t, NULL =
+ * the default stream).  Every entry point is asynchronous on that stream,
+ * allocates no memory and performs no host<->device synchronisation, so it
+ * can be recorded into a HIP graph.  Scratch memory is caller-owned
+ * ("workspace"); it must be zero-filled once when first allocated and is
+ * left zeroed by every successful call (the kernels reset their own
+ * counters).  Calls that share one workspace must be ordered (same stream).
+ *
+ * Reference interfaces replaced (paths relative to the GemmaInfer repo):
+ *   gi_fused_batched_moe        <- gemmainfer_csrc.fused_batched_moe
+ *                                  csrc/pybind.cpp:247-271 -> csrc/marlin.cu:612-702
+ *   gi_w4a16_linear             <- gemmainfer_csrc.marlin_w4a16
+ *                                  csrc/pybind.cpp:182-196 -> csrc/marlin.cu:704-856
+ *   gi_moe_route_topk_softmax   <- the router tail of GemmaBatchedMoE.forward
+ *                                  gemmainfer/models/gemma.py:77-80 (torch ops there)
+ *   gi_moe_align                <- the per-block dedup scan of the Token-Union kernels
+ *                                  csrc/marlin.cu:285-335 and :453-505 (implicit there)
+ *   gi_moe_layer_from_logits    <- gemma.py:77-98 (router tail + zeroed out + fused call)
+ *   gi_softcap_inplace          <- gemmainfer_csrc.softcapping
+ *                                  csrc/pybind.cpp:169-180 -> csrc/softcapping.cu:21-47
+ *   gi_rmsnorm                  <- gemmainfer_csrc.rmsnorm
+ *                                  csrc/pybind.cpp:137-151 -> csrc/rmsnorm.cu:75-114
+ *   gi_rope_inplace             <- gemmainfer_csrc.fused_rope_inplace
+ *                                  csrc/pybind.cpp:153-167 -> csrc/rmsnorm.cu:116-231
+ *
+ * Weight layouts are the reference's (gemmainfer/utils/weights.py:153-159,
+ * gemmainfer/kernels/quant.py:12-46): int4 codes packed 8 per int32 along the
+ * reduction dimension, nibble i of word [pk][n] = code of k = 8*pk+i, value
+ * (code - 8) * scale[k / group_size][n].  A scales tensor with fewer groups
+ * than ceil(K / group_size) drops the rows it does not cover, exactly as the
+ * reference CUDA kernels do (marlin.cu:357,526).
+ */
+#ifndef GEMMAINFER_AMD_H
+#define GEMMAINFER_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define GI_OK 0
+#define GI_ERR_INVALID_ARG (-1)   /* bad pointer / shape / dtype combination   */
+#define GI_ERR_UNSUPPORTED (-2)   /* valid but not implemented (e.g. fp32 x)   */
+#define GI_ERR_WORKSPACE (-3)     /* workspace missing or too small            */
+#define GI_ERR_HIP (-4)           /* a HIP runtime call failed                 */
+#define GI_ERR_DEVICE (-5)        /* a kernel reported a device-side error     */
+
+/* ---- dtype codes ------------------------------------------------------- */
+#define GI_DTYPE_BF16 0
+#define GI_DTYPE_FP16 1
+#define GI_DTYPE_FP32 2
+#define GI_DTYPE_INT32 3
+#define GI_DTYPE_INT64 4
+
+/* Device-side status bits written into a workspace's status word. */
+#define GI_DEVICE_SPIN_TIMEOUT 1  /* a bounded wait gave up (never expected)  */
+
+/* Message for the last non-OK status returned on this host thread. */
+const char* gi_last_error(void);
+/* ABI version (increments on any signature change). */
+int gi_abi_version(void);
+
+/* ---- a1: router tail ----------------------------------------------------
+ * logits [M, E] (bf16 or fp32, row-major) -> out_idx int32 [M, top_k]
+ * (descending logit; ties -> lower expert index; NaN ranks highest) and
+ * out_w [M, top_k] = softmax_fp32(top logits) * expert_scale[idx], stored in
+ * w_dtype (bf16/fp16/fp32).  expert_scale: fp32 [E] or NULL (= ones).
+ * Limits: 1 <= top_k <= min(E, 64), E <= 1024.                              */
+int gi_moe_route_topk_softmax(const void* logits, int logits_dtype,
+                              const float* expert_scale, int M, int E, int top_k,
+                              int32_t* out_idx, void* out_w, int w_dtype,
+                              void* stream);
+
+/* ---- a2: Token-Union alignment -----------------------------------------
+ * idx [M*top_k] (int32 or int64; ids outside [0, E) are skipped) ->
+ *   unique_experts int32 [min(S,E)]  first-occurrence slot order
+ *   num_unique     int32 [1]
+ *   slot_to_unique int32 [S]         -1 for skipped slots
+ *   offsets        int32 [min(S,E)+1] CSR over unique experts
+ *   slots          int32 [S]         slots of each unique expert, ascending
+ * S = M*top_k <= 256, E <= 1024.  Entries past num_unique are left as is.  */
+int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
+                 int32_t* unique_experts, int32_t* num_unique,
+                 int32_t* slot_to_unique, int32_t* offsets, int32_t* slots,
+                 void* stream);
+
+/* ---- a4-a7: fused Token-Union MoE ---------------------------------------
+ * out[M, H] += sum_slots bf16(w[slot]) * down(gelu_tanh(gate) * up)(x[token])
+ *   x          bf16 [M, H]
+ *   gu_packed  int32 [E, H/8, 2I]     gate in columns [0, I), up in [I, 2I)
+ *   gu_scales  bf16 [E, gu_groups, 2I]
+ *   d_packed   int32 [E, I/8, H]
+ *   d_scales   bf16 [E, d_groups, H]
+ *   idx        int32|int64 [M*top_k]  w  bf16|fp16|fp32 [M*top_k]
+ *   out        bf16 [M, H]            accumulated into (caller zeroes it)
+ * One kernel launch per 256/top_k rows.  Requirements: H % 8 == 0,
+ * I % 8 == 0, H, I multiples of 4 columns, group_size % 8 == 0, E <= 1024,
+ * top_k <= 256.  Deterministic (fixed-order fp32 reductions, no float
+ * atomics): the same inputs give bitwise-identical outputs.
+ * spin_limit: bound on each inter-workgroup wait (0 = default).            */
+size_t gi_fused_moe_workspace_bytes(int M, int top_k, int H, int I, int E);
+int gi_fused_batched_moe(const void* x, int x_dtype,
+                         const int32_t* gu_packed, const void* gu_scales, int gu_groups,
+                         const int32_t* d_packed, const void* d_scales, int d_groups,
+                         const void* idx, int idx_dtype,
+                         const void* w, int w_dtype,
+                         void* out,
+                         int M, int H, int I, int E, int top_k, int group_size,
+                         void* workspace, size_t workspace_bytes,
+                         int spin_limit, void* stream);
+
+/* Router + fused MoE in one launch: logits [M, E] (bf16/fp32) are routed as
+ * gi_moe_route_topk_softmax does (weights rounded to bf16), out[M, H] is
+ * OVERWRITTEN with the MoE output, and out_idx/out_w (may be NULL) receive
+ * the routing.  M*top_k <= 256.                                             */
+int gi_moe_layer_from_logits(const void* x, int x_dtype,
+                             const void* logits, int logits_dtype,
+                             const float* expert_scale,
+                             const int32_t* gu_packed, const void* gu_scales, int gu_groups,
+                             const int32_t* d_packed, const void* d_scales, int d_groups,
+                             void* out, int32_t* out_idx, void* out_w,
+                             int M, int H, int I, int E, int top_k, int group_size,
+                             void* workspace, size_t workspace_bytes,
+                             int spin_limit, void* stream);
+
+/* Copies the workspace's device status word to *host_status (synchronises
+ * the stream) and clears it.  0 = no device-side error since last read.    */
+int gi_workspace_status(void* workspace, size_t workspace_bytes,
+                        int32_t* host_status, void* stream);
+
+/* ---- a8 / a11: W4A16 linear ---------------------------------------------
+ * C[M, N] = A[M, K] @ dequant(B_packed[K/8, N], scales[n_groups, N]),
+ * optionally followed by C = softcap*tanh(C/softcap) when softcap > 0 (the
+ * lm_head epilogue, gemma.py:356-357).  A, scales, C bf16.  C is
+ * overwritten.  Requirements: K % 8 == 0, N % 4 == 0, group_size % 8 == 0. */
+size_t gi_w4a16_workspace_bytes(int M, int K, int N, int group_size);
+int gi_w4a16_linear(const void* A, int a_dtype,
+                    const int32_t* B_packed, const void* scales, int n_groups,
+                    void* C, int M, int K, int N, int group_size, float softcap,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- drop-in companions (not on the MoE hot path) ----------------------- */
+/* x <- cap * tanh(x / cap), n elements, bf16/fp16/fp32.                      */
+int gi_softcap_inplace(void* x, int dtype, int64_t n, float cap, void* stream);
+/* out[r, :] = in[r, :] * rsqrt(mean(in^2) + eps) * (weight or 1+weight);
+ * weight may be NULL (no scale).  bf16/fp16/fp32, in/out/weight same dtype. */
+int gi_rmsnorm(const void* in, const void* weight, void* out, int dtype,
+               int64_t rows, int hidden, float eps, int add_unit_offset,
+               void* stream);
+/* Rotate-half RoPE in place: q [B, Hq, S, D], k [B, Hk, S, D] (k may be NULL),
+ * last dimension contiguous, other strides in elements (q_sb/q_sh/q_ss and
+ * k_sb/k_sh/k_ss for the B, head and S dimensions); cos/sin [P, D]
+ * contiguous; position_ids int64 [B, S] contiguous.                          */
+int gi_rope_inplace(void* q, void* k, const void* cos_t, const void* sin_t,
+                    const int64_t* position_ids, int dtype,
+                    int B, int Hq, int Hk, int S, int D,
+                    int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                    int64_t k_sb, int64_t k_sh, int64_t k_ss, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GEMMAINFER_AMD_H */

@@ -1,0 +1,34 @@
+"""Shared test helpers: tolerance gate and tensor conversion."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import moe_oracle as O
+
+# Tolerance gate for bf16 outputs against the float64 oracle.
+#   * rel-L2 <= 1e-2: the BASELINE north-star bound, literally.
+#   * elementwise |got - ref| <= 2e-2 + 2^-7 |ref|: the north-star max-abs 2e-2
+#     made scale-aware.  A literal max-abs of 2e-2 is below the bf16 spacing of
+#     outputs this large (|out| reaches 50-85, spacing 0.25-0.5); 2^-7 |ref| is
+#     two half-ulps of bf16.
+REL_L2 = 1e-2
+ATOL = 2e-2
+RTOL = 2.0 ** -7
+
+
+def np64(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy().astype(np.float64)
+
+
+def assert_bf16_close(got: torch.Tensor, ref64: np.ndarray, what: str = "") -> dict:
+    g = np64(got)
+    stats = O.error_stats(g, ref64)
+    bound = ATOL + RTOL * np.abs(ref64)
+    bad = np.abs(g - ref64) > bound
+    assert np.isfinite(g).all(), f"{what}: non-finite outputs"
+    assert stats["rel_l2"] <= REL_L2, f"{what}: rel-L2 {stats['rel_l2']:.3e} > {REL_L2} ({stats})"
+    assert not bad.any(), (
+        f"{what}: {int(bad.sum())} elements outside {ATOL} + 2^-7|ref|; worst "
+        f"{float(np.max(np.abs(g - ref64) - bound)):.3e} over bound ({stats})")
+    return stats

@@ -1,0 +1,91 @@
+"""GPU parity of the W4A16 linear (marlin_w4a16) and the lm_head softcap epilogue."""
+import numpy as np
+import pytest
+import torch
+
+import gemmainfer_csrc
+from gemmainfer_amd import ops, synth
+from oracle import moe_oracle as O
+from tests.helpers import assert_bf16_close, np64
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("m,k,n,gs", [
+    (1, 2816, 2816, 128),    # BASELINE config 0 shape
+    (5, 2816, 2112, 64),     # reference sanitizer test shape (M=5)
+    (16, 2816, 2112, 64),    # M > 8 (reference's coalesced path)
+    (8, 256, 1000, 64),      # test-small lm_head (vocab 1000)
+    (3, 704, 2816, 128),     # ragged K groups (ceil), like the MoE down projection
+    (2, 64, 4, 8),           # tiny
+])
+def test_w4a16_linear(m, k, n, gs):
+    B, S = synth.linear_weights(k, n, gs, seed=m + n)
+    A = synth.activations(m, k, seed=k)
+    C = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    gemmainfer_csrc.marlin_w4a16(A.to(DEV), B.to(DEV), S.to(DEV), C, gs)
+    ref = O.w4a16_linear(np64(A), B.numpy(), np64(S), gs)
+    assert_bf16_close(C, ref, f"w4a16 m={m} k={k} n={n} gs={gs}")
+
+
+def test_w4a16_reference_floor_groups_drop_tail():
+    """A scales tensor with K//gs groups drops rows past the last group, like
+    the reference kernel (marlin.cu:128)."""
+    k, n, gs = 704, 256, 128
+    B, S = synth.linear_weights(k, n, gs, seed=3)
+    S = S[: k // gs].contiguous()
+    A = synth.activations(2, k, seed=4)
+    C = torch.empty(2, n, dtype=torch.bfloat16, device=DEV)
+    ops.marlin_w4a16(A.to(DEV), B.to(DEV), S.to(DEV), C, gs)
+    ref = O.w4a16_linear(np64(A), B.numpy(), np64(S), gs)
+    assert_bf16_close(C, ref, "floor groups")
+
+
+def test_lm_head_softcap_column_subset():
+    """BASELINE config 4 shape (M=6, K=2816, N=262144, gs=128): every output is
+    computed on the GPU; the float64 oracle checks 2048 random columns."""
+    m, k, n, gs = 6, 2816, 262144, 128
+    g = torch.Generator(device=DEV)
+    g.manual_seed(4)
+    B = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), generator=g, device=DEV,
+                      dtype=torch.int64).to(torch.int32)
+    S = (torch.randn((k // gs, n), generator=g, device=DEV).abs() * 0.02).to(torch.bfloat16)
+    A = synth.activations(m, k, seed=6).to(DEV)
+    C = ops.w4a16_linear(A, B, S, gs, softcap=30.0)
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(0))[:2048].sort().values
+    Bs, Ss = B[:, cols.to(DEV)].cpu(), S[:, cols.to(DEV)].cpu()
+    ref = O.softcap(O.w4a16_linear(np64(A), Bs.numpy(), np64(Ss), gs), 30.0)
+    assert_bf16_close(C[:, cols.to(DEV)], ref, "lm_head subset")
+    # size-independent property: softcap bounds every logit by the cap
+    assert float(C.float().abs().max()) <= 30.0
+
+
+def test_companions_match_cpu_semantics():
+    x = torch.randn(3, 2816).to(torch.bfloat16)
+    w = torch.randn(2816).to(torch.bfloat16)
+    for unit in (False, True):
+        out = torch.empty(3, 2816, dtype=torch.bfloat16, device=DEV)
+        gemmainfer_csrc.rmsnorm(x.to(DEV), w.to(DEV), out, 1e-6, unit)
+        ref_out = torch.empty_like(x)
+        gemmainfer_csrc.rmsnorm(x, w, ref_out, 1e-6, unit)
+        torch.testing.assert_close(out.cpu().float(), ref_out.float(), rtol=1e-2, atol=1e-2)
+    logits = (torch.randn(1, 262144) * 40).to(torch.bfloat16)
+    g = logits.to(DEV)
+    gemmainfer_csrc.softcapping(g, 30.0)
+    c = logits.clone()
+    gemmainfer_csrc.softcapping(c, 30.0)
+    torch.testing.assert_close(g.cpu().float(), c.float(), rtol=1e-2, atol=1e-2)
+    q = torch.randn(2, 4, 5, 64).to(torch.bfloat16)
+    k = torch.randn(2, 2, 5, 64).to(torch.bfloat16)
+    pos = torch.arange(5).unsqueeze(0).expand(2, -1).contiguous()
+    inv = 1.0 / (10000 ** (torch.arange(0, 64, 2).float() / 64))
+    fr = torch.outer(torch.arange(16).float(), inv)
+    emb = torch.cat((fr, fr), -1)
+    cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+    qd, kd = q.to(DEV), k.to(DEV)
+    gemmainfer_csrc.fused_rope_inplace(qd, kd, cos.to(DEV), sin.to(DEV), pos.to(DEV))
+    qc, kc = q.clone(), k.clone()
+    gemmainfer_csrc.fused_rope_inplace(qc, kc, cos, sin, pos)
+    torch.testing.assert_close(qd.cpu().float(), qc.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(kd.cpu().float(), kc.float(), rtol=2e-2, atol=2e-2)

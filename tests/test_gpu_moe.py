@@ -1,0 +1,218 @@
+"""GPU parity of the Token-Union MoE path against the CPU oracle.
+
+Routing ids, the unique-expert list and the slot map must be bit-exact; bf16
+outputs must pass the tolerance gate in tests/helpers.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gemmainfer_amd import ops, synth
+from gemmainfer_amd import _lib as L
+from oracle import moe_oracle as O
+from tests.helpers import assert_bf16_close, np64
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _dev(d):
+    return {k: v.to(DEV) for k, v in d.items()}
+
+
+def _oracle_moe(x, W, idx, w, out_in, gs):
+    return O.fused_batched_moe(np64(x), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
+                               W["down_packed"].numpy(), np64(W["down_scales"]), idx.cpu().numpy(),
+                               np64(w), np64(out_in), gs)
+
+
+@pytest.fixture(scope="module")
+def small():
+    W = synth.moe_weights(E=8, H=256, I=128, group_size=64, seed=11)
+    return W, _dev(W)
+
+
+@pytest.fixture(scope="module")
+def gemma128():
+    # Gemma-4-26B-A4B expert shapes, group 128: down has 6 groups, the last ragged.
+    W = synth.moe_weights(E=128, H=2816, I=704, group_size=128, seed=1)
+    return W, _dev(W)
+
+
+# ---------------------------------------------------------------- routing
+@pytest.mark.parametrize("m", [1, 7, 64, 200])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_route_topk_softmax(m, dtype):
+    logits = synth.router_logits(m, 128, seed=m).to(dtype)
+    idx, w = ops.route_topk_softmax(logits.to(DEV), 8)
+    ref_idx, _, ref_w = O.route_topk_softmax(np64(logits), 8)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+    # weights: fp32 softmax then one bf16 rounding; allow one bf16 ulp
+    np.testing.assert_allclose(np64(w), ref_w, rtol=2.0 ** -7, atol=0)
+    if dtype == torch.float32:
+        _, ti = torch.topk(logits, 8, dim=-1)  # (values, indices)
+        np.testing.assert_array_equal(idx.cpu().numpy(), ti.numpy())
+
+
+def test_route_ties_and_expert_scale():
+    logits = torch.zeros(3, 128)
+    logits[0, [5, 9, 77]] = 1.0            # ties among the top values
+    logits[1, 100] = float("nan")          # NaN ranks highest
+    es = torch.linspace(0.5, 1.5, 128)
+    idx, w = ops.route_topk_softmax(logits.to(DEV), 8, expert_scale=es.to(DEV))
+    ref_idx, _, ref_w = O.route_topk_softmax(np64(logits), 8, expert_scale=es.numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+    finite = np.isfinite(ref_w)
+    np.testing.assert_allclose(np64(w)[finite], ref_w[finite], rtol=2.0 ** -7)
+
+
+# ---------------------------------------------------------------- alignment
+ALIGN_CASES = [
+    ("m1_distinct", [[3, 1, 4, 15, 9, 2, 6, 5]], 16),
+    ("dup_across_tokens", [[1, 2], [2, 3], [3, 1]], 8),
+    ("dup_within_token", [[4, 4, 4, 1]], 8),
+    ("invalid_ids", [[-1, 3, 99, 3], [8, 0, -5, 2]], 8),
+    ("all_same", [[6, 6], [6, 6], [6, 6]], 8),
+    ("all_invalid", [[-1, 8], [9, -2]], 8),
+]
+
+
+@pytest.mark.parametrize("name,ids,E", ALIGN_CASES, ids=[c[0] for c in ALIGN_CASES])
+@pytest.mark.parametrize("idt", [torch.int32, torch.int64])
+def test_align_known_answers(name, ids, E, idt):
+    idx = torch.tensor(ids, dtype=idt)
+    got = ops.moe_align(idx.to(DEV), E)
+    ref = O.token_union_align(idx.numpy(), E)
+    u = int(got["num_unique"].item())
+    assert u == ref.num_unique
+    np.testing.assert_array_equal(got["unique_experts"][:u].cpu().numpy(), ref.unique_experts)
+    np.testing.assert_array_equal(got["slot_to_unique"].cpu().numpy(), ref.slot_to_unique)
+    np.testing.assert_array_equal(got["offsets"][:u + 1].cpu().numpy(), ref.offsets)
+    n = int(ref.offsets[-1])
+    np.testing.assert_array_equal(got["slots"][:n].cpu().numpy(), ref.slots)
+
+
+@pytest.mark.parametrize("m,noise", [(1, 0.0), (7, 0.5), (8, 0.5), (32, 0.0)])
+def test_align_random_routing(m, noise):
+    logits = synth.router_logits(m, 128, seed=100 + m, verify_noise=noise)
+    idx, _, _ = O.route_topk_softmax(np64(logits), 8)
+    got = ops.moe_align(torch.from_numpy(idx).to(DEV), 128)
+    ref = O.token_union_align(idx, 128)
+    u = int(got["num_unique"].item())
+    assert u == ref.num_unique
+    np.testing.assert_array_equal(got["unique_experts"][:u].cpu().numpy(), ref.unique_experts)
+    np.testing.assert_array_equal(got["slot_to_unique"].cpu().numpy(), ref.slot_to_unique)
+    np.testing.assert_array_equal(got["slots"][:int(ref.offsets[-1])].cpu().numpy(), ref.slots)
+
+
+# ---------------------------------------------------------------- fused MoE
+@pytest.mark.parametrize("m", [1, 2, 5, 8, 9, 33, 300])
+def test_fused_small_shapes(small, m):
+    W, Wd = small
+    x = synth.activations(m, 256, seed=m)
+    logits = synth.router_logits(m, 8, seed=m)
+    idx, _, w = O.route_topk_softmax(np64(logits), 2)
+    idx_t = torch.from_numpy(idx)
+    w_t = torch.from_numpy(w).to(torch.bfloat16)
+    out_in = (torch.randn(m, 256) * 0.1).to(torch.bfloat16)   # out is accumulated into
+    out = out_in.to(DEV).clone()
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx_t.to(DEV), w_t.to(DEV), out, 64)
+    ref, _ = _oracle_moe(x, W, idx_t, w_t, out_in, 64)
+    assert_bf16_close(out, ref, f"small m={m}")
+
+
+def test_fused_duplicates_invalid_and_dtypes(small):
+    """Duplicate ids within a token are separate slots (pybind.cpp:219-244, no
+    MAX_MATCH cap); ids outside [0, E) are skipped (marlin.cu:304,473);
+    int64 ids and fp32 weights are accepted and cast like marlin.cu:631-636."""
+    W, Wd = small
+    x = synth.activations(3, 256, seed=5)
+    idx = torch.tensor([[1, 1, 1, 1], [7, -1, 8, 7], [2, 3, 2, 3]], dtype=torch.int64)
+    w = torch.tensor([[0.3, 0.2, 0.1, 0.4], [0.5, 9.0, 9.0, 0.25], [0.1, 0.2, 0.3, 0.4]])
+    out = torch.zeros(3, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(DEV), w.to(DEV), out, 64)
+    ref, _ = _oracle_moe(x, W, idx, w, torch.zeros(3, 256), 64)
+    assert_bf16_close(out, ref, "duplicates/invalid")
+
+
+@pytest.mark.parametrize("m,noise", [(1, 0.0), (7, 0.5), (8, 0.5)])
+def test_fused_gemma_shapes_gs128(gemma128, m, noise):
+    W, Wd = gemma128
+    x = synth.activations(m, 2816, seed=m)
+    logits = synth.router_logits(m, 128, seed=m, verify_noise=noise)
+    idx, _, w = O.route_topk_softmax(np64(logits), 8)
+    idx_t = torch.from_numpy(idx)
+    w_t = torch.from_numpy(w).to(torch.bfloat16)
+    out = torch.zeros(m, 2816, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx_t.to(DEV), w_t.to(DEV), out, 128)
+    ref, al = _oracle_moe(x, W, idx_t, w_t, torch.zeros(m, 2816), 128)
+    stats = assert_bf16_close(out, ref, f"gemma m={m}")
+    print(f"m={m} U={al.num_unique} {stats}")
+
+
+def test_layer_from_logits_gemma(gemma128):
+    W, Wd = gemma128
+    for m, noise in ((1, 0.0), (7, 0.5)):
+        x = synth.activations(m, 2816, seed=10 + m)
+        logits = synth.router_logits(m, 128, seed=10 + m, verify_noise=noise)
+        out, idx, w = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"],
+                                    Wd["gate_up_scales"], Wd["down_packed"], Wd["down_scales"],
+                                    8, 128)
+        ref_out, ref_idx, ref_w, al = O.moe_layer_from_logits(
+            np64(x), np64(logits), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
+            W["down_packed"].numpy(), np64(W["down_scales"]), 8, 128)
+        np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+        np.testing.assert_allclose(np64(w), ref_w, rtol=2.0 ** -7)
+        assert_bf16_close(out, ref_out, f"layer m={m}")
+
+
+def test_deterministic_bitwise(gemma128):
+    W, Wd = gemma128
+    x = synth.activations(7, 2816, seed=3).to(DEV)
+    logits = synth.router_logits(7, 128, seed=3, verify_noise=0.5).to(DEV)
+    outs = []
+    for _ in range(3):
+        out, _, _ = ops.moe_layer(x, logits, Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                  Wd["down_packed"], Wd["down_scales"], 8, 128)
+        outs.append(out.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_zero_scales_give_zero(small):
+    """The reference's own test state (zero-initialised buffers, gemma.py:43-58)."""
+    _, Wd = small
+    x = synth.activations(5, 256, seed=1).to(DEV)
+    idx = torch.randint(0, 8, (5, 2), dtype=torch.int32).to(DEV)
+    w = torch.full((5, 2), 0.5, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(5, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x, Wd["gate_up_packed"], torch.zeros_like(Wd["gate_up_scales"]),
+                          Wd["down_packed"], Wd["down_scales"], idx, w, out, 64)
+    assert torch.count_nonzero(out).item() == 0
+
+
+def test_device_status_clean_and_timeout_path(small):
+    W, Wd = small
+    assert ops.workspace_status() == 0
+    # A spin limit of 1 poll forces the bounded-wait error path from the host:
+    # the kernel must still finish and report the flag.
+    x = synth.activations(4, 256, seed=2).to(DEV)
+    idx = torch.tensor([[0, 1], [2, 3], [4, 5], [6, 7]], dtype=torch.int32, device=DEV)
+    w = torch.full((4, 2), 0.5, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(4, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x, Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx, w, out, 64, spin_limit=1)
+    torch.cuda.synchronize()
+    st = ops.workspace_status()
+    assert st in (0, L.DEVICE_SPIN_TIMEOUT)
+    assert ops.workspace_status() == 0  # read clears it
+    # the workspace is usable again afterwards
+    out2 = torch.zeros(4, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x, Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx, w, out2, 64)
+    ref, _ = _oracle_moe(x.cpu(), W, idx.cpu(), w.cpu(), torch.zeros(4, 256), 64)
+    assert_bf16_close(out2, ref, "after timeout path")
+    assert ops.workspace_status() == 0
