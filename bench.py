@@ -1,0 +1,327 @@
+"""Benchmark of the fused Token-Union W4A16 MoE layer on one MI355X.
+
+Metric: fused W4A16 MoE layer time and achieved HBM GB/s at
+M=1 (configs[1], the headline ``value``) and M=7 (configs[2], reported beside
+it), Gemma-4-26B-A4B expert shapes: hidden 2816, 128 experts, top-8,
+intermediate 704, int4 weights with bf16 scales per group of 128 (the down
+projection has 6 groups, the last 64 rows wide).
+
+A step is one layer: router top-8 softmax + Token-Union alignment + gate_up +
+gelu_tanh*up + down + routing-weighted combine, as ONE kernel launch
+(gi_moe_layer_from_logits) from N(0,1) fp32 router logits.
+
+Measurement:
+  * Weights: 4 independent copies of the full 128-expert layer (1.57 GB).
+    Each step's N(0,1) logits are relabelled (a permutation of expert ids,
+    values unchanged) so that every copy's experts are visited in rotation:
+    >= 1 GB of other weights is read between two reads of the same expert
+    bytes, so the 256 MB MALL cannot serve them.  The realised minimum reuse
+    distance is reported.
+  * W warmup steps, then K steps captured in one HIP graph and replayed
+    between HIP events on the launch stream (synchronised on both sides);
+    us_per_layer = elapsed / K.  Hot-cache (same weights every step) and
+    stream-launched (no graph, Python ctypes per call) figures are reported
+    separately; neither is ``value``.
+  * Algorithmic bytes per layer = unique experts x 3,069,440 B (packed
+    gate_up + down words and their bf16 scales), activations excluded.
+  * cpu_baseline: the reference's PyTorch CPU dequant+matmul path
+    (oracle/cpu_baseline.py), timed on this host's cores on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import platform
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+from gemmainfer_amd import _lib as L  # noqa: E402
+from gemmainfer_amd import synth  # noqa: E402
+
+METRIC = "fused W4A16 MoE layer us + achieved HBM GB/s at M=1 and M=7 (1 GPU)"
+E, H, I, TOP_K, GS = 128, 2816, 704, 8, 128
+COPIES = 4
+PEAK_GBPS = 8000.0
+
+
+def expert_bytes(h=H, i=I, gs=GS) -> int:
+    """Packed words + bf16 scales of one expert (gate_up and down)."""
+    gu = (h // 8) * 2 * i * 4 + math.ceil(h / gs) * 2 * i * 2
+    dn = (i // 8) * h * 4 + math.ceil(i / gs) * h * 2
+    return gu + dn
+
+
+def first_occurrence_unique(idx_row_major):
+    seen, out = set(), []
+    for e in idx_row_major:
+        if e not in seen:
+            seen.add(e)
+            out.append(e)
+    return out
+
+
+def make_steps(m, noise, seed, n_desc):
+    """Per-step (copy, logits, unique experts) with expert ids relabelled so
+    that each copy's experts are used in rotation."""
+    cursor = [0] * COPIES
+    steps = []
+    for s in range(n_desc):
+        c = s % COPIES
+        logits = synth.router_logits(m, E, seed=seed * 100003 + s, verify_noise=noise)
+        top = torch.topk(logits, TOP_K, dim=-1).indices.reshape(-1).tolist()
+        uniq = first_occurrence_unique(top)
+        block = [(cursor[c] + j) % E for j in range(len(uniq))]
+        cursor[c] = (cursor[c] + len(uniq)) % E
+        rest_src = [e for e in range(E) if e not in set(uniq)]
+        rest_dst = [e for e in range(E) if e not in set(block)]
+        perm = [0] * E  # perm[old] = new
+        for o, n in zip(uniq, block):
+            perm[o] = n
+        for o, n in zip(rest_src, rest_dst):
+            perm[o] = n
+        new = torch.empty_like(logits)
+        new[:, torch.tensor(perm)] = logits
+        steps.append({"copy": c, "logits": new, "unique": sorted(block), "U": len(uniq)})
+    return steps
+
+
+def min_reuse_distance_bytes(steps, order):
+    """Smallest number of weight bytes read between two reads of one expert."""
+    eb = expert_bytes()
+    last, touched, best = {}, 0, None
+    for s in order:
+        st = steps[s]
+        for e in st["unique"]:
+            key = (st["copy"], e)
+            if key in last:
+                d = touched - last[key]
+                best = d if best is None else min(best, d)
+        for e in st["unique"]:
+            last[(st["copy"], e)] = touched
+        touched += st["U"] * eb
+    return best
+
+
+class LayerRunner:
+    """Direct C-ABI launches of gi_moe_layer_from_logits with fixed buffers."""
+
+    def __init__(self, m, steps, copies, device):
+        self.lib = L.load()
+        self.m = m
+        self.dev = device
+        self.copies = copies
+        self.x = synth.activations(m, H, seed=7).to(device)
+        self.logits = [st["logits"].to(device).contiguous() for st in steps]
+        self.copy_of = [st["copy"] for st in steps]
+        self.out = torch.empty(m, H, dtype=torch.bfloat16, device=device)
+        self.idx = torch.empty(m, TOP_K, dtype=torch.int32, device=device)
+        self.w = torch.empty(m, TOP_K, dtype=torch.bfloat16, device=device)
+        nbytes = self.lib.gi_fused_moe_workspace_bytes(m, TOP_K, H, I, E)
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        torch.cuda.synchronize()
+
+    def launch(self, s):
+        W = self.copies[self.copy_of[s]]
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        st = self.lib.gi_moe_layer_from_logits(
+            p(self.x), L.DTYPE_BF16, p(self.logits[s]), L.DTYPE_FP32, None,
+            p(W["gate_up_packed"]), p(W["gate_up_scales"]), W["gate_up_scales"].shape[1],
+            p(W["down_packed"]), p(W["down_scales"]), W["down_scales"].shape[1],
+            p(self.out), p(self.idx), p(self.w), self.m, H, I, E, TOP_K, GS,
+            p(self.ws), self.ws.numel(), 0, stream)
+        L.check(st, "gi_moe_layer_from_logits")
+
+    def status(self):
+        v = ctypes.c_int32(0)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        L.check(self.lib.gi_workspace_status(ctypes.c_void_p(self.ws.data_ptr()), self.ws.numel(),
+                                             ctypes.byref(v), stream), "status")
+        return v.value
+
+
+def time_graph(runner, order, device):
+    """Capture launches in `order` into one graph; return us per launch."""
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream(device)
+    s.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(s):
+        runner.launch(order[0])  # launch once on the capture stream before capturing
+    torch.cuda.current_stream(device).wait_stream(s)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for i in order:
+            runner.launch(i)
+    torch.cuda.synchronize()
+    g.replay()  # untimed replay: first replay uploads the graph
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / len(order)
+
+
+def time_stream(runner, order):
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in order:
+        runner.launch(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1000.0 / len(order)
+
+
+def bench_config(m, noise, seed, copies, steps, warmup, device):
+    # one descriptor per executed step, so the expert rotation never wraps
+    n_desc = warmup + steps
+    desc = make_steps(m, noise, seed, n_desc)
+    runner = LayerRunner(m, desc, copies, device)
+    for i in range(warmup):
+        runner.launch(i)
+    torch.cuda.synchronize()
+    order = [warmup + i for i in range(steps)]
+    us = time_graph(runner, order, device)
+    hot_us = time_graph(runner, [order[0]] * min(steps, 200), device)
+    stream_us = time_stream(runner, order[: min(steps, 200)])
+    if runner.status() != 0:
+        raise RuntimeError("device status word set during the benchmark")
+    mean_u = statistics.fmean(desc[i]["U"] for i in order)
+    nbytes = mean_u * expert_bytes()
+    return {
+        "M": m,
+        "us_per_layer": us,
+        "gbps": nbytes / (us * 1e-6) / 1e9,
+        "unique_experts_mean": mean_u,
+        "unique_experts_range": [min(desc[i]["U"] for i in order), max(desc[i]["U"] for i in order)],
+        "algorithmic_bytes_per_layer": nbytes,
+        "min_reuse_distance_bytes": min_reuse_distance_bytes(desc, order),
+        "hot_cache_us_per_layer": hot_us,
+        "stream_launched_us_per_layer": stream_us,
+    }
+
+
+def cpu_baseline(budget_s, max_reps):
+    """The reference's PyTorch CPU path on the same workload (M=1 layer),
+    bounded to about budget_s seconds of CPU work."""
+    from oracle import cpu_baseline as CB
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    W = synth.moe_weights(E, H, I, GS, seed=1)
+    x = synth.activations(1, H, seed=1)
+    logits = synth.router_logits(1, E, seed=1)
+    top, idx = torch.topk(logits, TOP_K, dim=-1)           # gemma.py:77-80
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(torch.bfloat16)
+    args = (x, idx, w, W["gate_up_packed"], W["gate_up_scales"], W["down_packed"], W["down_scales"], GS)
+    CB.moe_forward(*args)  # warmup
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
+        t0 = time.perf_counter()
+        CB.moe_forward(*args)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    u = len(set(idx.reshape(-1).tolist()))
+    nbytes = u * expert_bytes()
+    try:
+        model = [l for l in open("/proc/cpuinfo") if l.startswith("model name")][0].split(":")[1].strip()
+    except Exception:
+        model = platform.processor()
+    return {
+        "value": nbytes / t / 1e9,
+        "unit": "GB/s",
+        "us_per_layer": t * 1e6,
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{len(times)} timed reps (median) of one M=1 layer (U={u}) through "
+                   f"oracle/cpu_baseline.moe_forward, restating quant.py:67-75 + gemma.py:115-147; "
+                   f"host {model}, torch {torch.__version__}"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's path runs on a single MI355X "
+              f"(--gpus {args.gpus} is not supported; the sharding design is in DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    copies = [synth.device_moe_weights(E, H, I, GS, device, seed=100 + c) for c in range(COPIES)]
+    torch.cuda.synchronize()
+    print(f"[bench] weights ready: {COPIES} x {E} experts", file=sys.stderr, flush=True)
+    m1 = bench_config(1, 0.0, 1, copies, args.steps, args.warmup, device)
+    print(f"[bench] M=1 {m1['us_per_layer']:.2f} us {m1['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    m7 = bench_config(7, 0.5, 2, copies, args.steps, args.warmup, device)
+    print(f"[bench] M=7 {m7['us_per_layer']:.2f} us {m7['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(args.cpu_budget_s, 30)
+        print(f"[bench] cpu {cpu['us_per_layer']:.0f} us", file=sys.stderr, flush=True)
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_moe_layer_m1.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    res = {
+        "metric": METRIC,
+        "value": m1["gbps"],
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": m1["us_per_layer"] / 1000.0,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 activations and fp32 router logits, uniform int4 codes, |N(0,1)|*0.02 bf16 scales)",
+        "config": {
+            "workload": "fused W4A16 MoE layer, decode M=1 (configs[1]): route+align+gate_up+gelu+down+combine, one launch",
+            "M": 1, "hidden": H, "experts": E, "top_k": TOP_K, "moe_intermediate": I,
+            "group_size": GS, "weight_copies_rotated": COPIES, "timing": "HIP graph of K steps, HIP events",
+        },
+        "us_per_layer": m1["us_per_layer"],
+        "roofline": {
+            "bound": "hbm",
+            "achieved": m1["gbps"],
+            "peak": PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": m1["gbps"] / PEAK_GBPS,
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+        "m1": m1,
+        "m7": m7,
+    }
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -92,16 +92,40 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
 }
 
 // sum_{i<8} x_i * (q_i - 8) for one packed word, given pair-permuted x and
-// bias = -136 * sum x_i.  OR-ing a code into 0x4300 (bf16 128.0, ulp 1)
-// yields the exact bf16 value 128 + q, so two codes per mask-and-or feed one
-// v_dot2_f32_bf16; the bias removes the 136 = 128 + 8 offset.
-__device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias) {
-  const uint32_t m = 0x000F000Fu, mag = 0x43004300u;
-  float d = fdot2(xp.x, (w & m) | mag, bias);
-  d = fdot2(xp.y, ((w >> 4) & m) | mag, d);
-  d = fdot2(xp.z, ((w >> 8) & m) | mag, d);
-  d = fdot2(xp.w, ((w >> 12) & m) | mag, d);
+// bias = -136 * sum x_i.  A bf16 whose high byte is 0x43 and low byte is a
+// code q is exactly 128 + q (bf16 128.0 has unit spacing), so v_perm_b32 can
+// assemble two dequantised codes per instruction from the masked nibble bytes
+// and a register holding 0x43 bytes; each pair feeds one v_dot2_f32_bf16 and
+// the bias removes the 136 = 128 + 8 offset.  11 VALU ops per word.
+//   lo = w & 0x0F0F0F0F holds codes (q0, q2, q4, q6) in its bytes,
+//   hi = (w >> 4) & 0x0F0F0F0F holds (q1, q3, q5, q7).
+__device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias, uint32_t m43) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  float d = fdot2(xp.x, __builtin_amdgcn_perm(m43, lo, 0x04020400u), bias);  // (q0, q4)
+  d = fdot2(xp.z, __builtin_amdgcn_perm(m43, lo, 0x04030401u), d);           // (q2, q6)
+  d = fdot2(xp.y, __builtin_amdgcn_perm(m43, hi, 0x04020400u), d);           // (q1, q5)
+  d = fdot2(xp.w, __builtin_amdgcn_perm(m43, hi, 0x04030401u), d);           // (q3, q7)
   return d;
+}
+
+// 0x43434343 held in a VGPR (v_perm_b32 may read only one scalar operand).
+__device__ __forceinline__ uint32_t magic43() {
+  uint32_t v = 0x43434343u;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+// Makes `v` opaque to the optimiser (no instruction is emitted).  Used on
+// prefetched weight words inside loops so their dequantisation is not hoisted
+// out as loop-invariant, which would hold 4x the packed bytes in registers.
+__device__ __forceinline__ uint4 opaque(uint4 v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+  return v;
+}
+
+__device__ __forceinline__ uint2 opaque(uint2 v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y));
+  return v;
 }
 
 __device__ __forceinline__ float bf16lo(uint32_t v) { return __uint_as_float(v << 16); }
@@ -116,24 +140,45 @@ __device__ __forceinline__ float reduce_across_groups(float v) {
   return v;
 }
 
-// ---- inter-workgroup signalling (agent scope) -----------------------------
-__device__ __forceinline__ int atomic_add_release(int* p, int v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+// ---- inter-workgroup data and signals ---------------------------------------
+// Data handed between workgroups (possibly on different XCDs, whose L2 caches
+// are not coherent with each other) is written and read with relaxed
+// agent-scope atomic accesses: on gfx950 these are plain loads/stores with the
+// sc1 bit, i.e. performed at the device coherence point, so no L2 writeback
+// or invalidate (which acquire/release at agent scope would add to every
+// flag operation) is needed.  A producer waits for its sc1 stores to complete
+// (wait_vmem) before the workgroup barrier that precedes the counter update;
+// a consumer observes the counter, crosses a barrier, then issues its sc1 loads.
+__device__ __forceinline__ void st_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_coherent_f32(float* p, float v) {
+  __hip_atomic_store((uint32_t*)p, __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_coherent_f32(const float* p) {
+  return __uint_as_float(__hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+__device__ __forceinline__ uint4 ld_coherent_u4(const void* p) {
+  unsigned long long* q = (unsigned long long*)p;
+  const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+// Wait until every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
+
+// ---- counters (agent scope) -------------------------------------------------
+__device__ __forceinline__ int atomic_add_relaxed(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int atomic_add_acq_rel(int* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int load_acquire(int* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ int load_relaxed(int* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void store_relaxed(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void fence_acquire_agent() {
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {

@@ -1,0 +1,895 @@
+// Token-Union W4A16 fused MoE for small token counts (decode M=1, verify
+// M<=8, any launch of up to 256 slots) on gfx950.
+//
+// Reference behaviour restated (paths relative to the GemmaInfer repo):
+//   routing        gemmainfer/models/gemma.py:77-80
+//   dedup          csrc/marlin.cu:285-335 (gate_up) / :453-505 (down)
+//   gate_up + GELU csrc/marlin.cu:337-426
+//   down + combine csrc/marlin.cu:507-586
+//
+// One launch per layer, ONE inter-workgroup synchronisation.
+//
+//   prologue  Every workgroup routes the tokens (layer mode: top-k + softmax
+//             per token, one wave per token, DPP row reductions) and builds the
+//             Token-Union alignment in LDS: the distinct valid expert ids in
+//             first-occurrence slot order and each slot's unique index.
+//   tasks     Task (u, c) owns intermediate columns [c*CG, (c+1)*CG) of unique
+//             expert u.  It streams the matching gate and up columns over the
+//             whole hidden dimension (registers, 16-byte non-temporal loads),
+//             reduces them across lanes and waves, applies gelu_tanh(gate)*up
+//             and rounds to bf16 (where the reference stores its activation),
+//             then multiplies those CG activations by the CG/8 packed rows of
+//             the down projection they meet -- across all H output columns --
+//             whose words were streamed straight into LDS (global_load_lds)
+//             at task start.  The activation never leaves the workgroup.
+//             Result: an fp32 partial w[slot]*y for every slot of u, written
+//             to part[slot][c][:] with coherent (sc1) stores.
+//   barrier   One grid-wide arrival counter (all workgroups are resident: the
+//             grid is sized from the occupancy calculator).
+//   reduce    Every workgroup sums a slice of output columns over
+//             (slot of the token, c) in a fixed order, adds it to out and
+//             rounds once to bf16.  No float atomics; bitwise deterministic.
+//
+// Waits are bounded (spin_limit) and report GI_DEVICE_SPIN_TIMEOUT instead of
+// hanging; the counters are reset by the last workgroup out.
+
+#include <limits.h>
+
+#include <mutex>
+
+#include "../../include/gemmainfer_amd.h"
+#include "gi_common.h"
+#include "gi_internal.h"
+
+namespace gi {
+
+namespace {
+
+constexpr int kMaxSlots = 256;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxWaves = 16;
+constexpr int kDefaultSpin = 1 << 22;
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
+
+struct Args {
+  const uint16_t* x;
+  const int32_t* gu_packed;
+  const uint16_t* gu_scales;
+  const int32_t* d_packed;
+  const uint16_t* d_scales;
+  const void* idx;
+  const void* w;
+  const void* logits;
+  const float* expert_scale;
+  int32_t* out_idx;
+  uint16_t* out_w;
+  uint16_t* out;
+  float* part;      // [S][Tg][H] fp32 partials
+  int* ctr;         // [0] arrivals, [1] departures
+  int* status;
+  int idx_is64, w_dtype, logits_dtype;
+  int M, H, I, E, top_k, gs, Ggu, Gd, S, Tg;
+  int overwrite, spin_limit;
+  int qpw;          // reduction: output quads per workgroup pass (power of two)
+  // dynamic LDS layout (bytes)
+  int off_slab, off_xs, off_xb, off_sct, off_red, off_actp, off_actb;
+};
+
+struct Prologue {
+  int first_slot[kMaxExperts];
+  int slot_e[kMaxSlots];
+  int slot_u[kMaxSlots];      // unique index of each slot, -1 if skipped
+  float slot_w[kMaxSlots];    // routing weight (bf16-rounded)
+  int rank_of_slot[kMaxSlots];
+  int uexp[kMaxSlots];        // expert id of each unique index
+  int list[kMaxSlots];        // slots of the current task's expert, ascending
+  int wave_cnt[kMaxWaves];
+  int n_unique;
+  int n_list;
+};
+
+// ---------------------------------------------------------------------------
+// routing
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t orderable_key(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (f != f) return 0xffffffffu;  // NaN ranks above every number
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+  if (k == 0xffffffffu) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
+
+// Maximum over the wave: DPP inside each 16-lane row (quad swaps, half-row
+// and row mirrors), then the four row results through readlane.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
+  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
+  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
+  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return umax(umax(r0, r1), umax(r2, r3));
+}
+
+// Top-k + softmax of token t by one wave (gemma.py:77-80).  Lane l holds the
+// keys of experts l, l+64, ...  Each round takes the wave maximum of the keys
+// and, among equal keys, the lowest expert index (first set ballot bit in the
+// lowest register), then retires it (key 0; every real value has a non-zero
+// key).  Lane r < top_k ends with the r-th expert and its weight.
+template <int VPL>
+__device__ __forceinline__ void route_token(const Args& a, int t, int lane, int* idx_out,
+                                            float* w_out) {
+  uint32_t keys[VPL];
+  const size_t base = (size_t)t * a.E;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int e = lane + v * kWave;
+    uint32_t k = 0;
+    if (e < a.E) {
+      const float f = a.logits_dtype == GI_DTYPE_BF16
+                          ? bf16_to_f32(((const uint16_t*)a.logits)[base + e])
+                          : ((const float*)a.logits)[base + e];
+      k = orderable_key(f);
+    }
+    keys[v] = k;
+  }
+  int my_idx = 0;
+  float my_val = 0.f;
+  for (int r = 0; r < a.top_k; ++r) {
+    uint32_t lm = keys[0];
+#pragma unroll
+    for (int v = 1; v < VPL; ++v) lm = umax(lm, keys[v]);
+    const uint32_t m = wave_max_u32(lm);
+    int win = -1;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const unsigned long long b = __ballot(keys[v] == m);
+      if (win < 0 && b) win = v * kWave + (int)__builtin_ctzll(b);
+    }
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      if (lane + v * kWave == win) keys[v] = 0u;
+    if (lane == r) {
+      my_idx = win;
+      my_val = key_value(m);
+    }
+  }
+  const float vmax = __shfl(my_val, 0, kWave);
+  const float ex = lane < a.top_k ? expf(my_val - vmax) : 0.f;
+  float sum = ex;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  if (lane < a.top_k) {
+    float p = ex / sum;
+    if (a.expert_scale) p *= a.expert_scale[my_idx];
+    idx_out[lane] = my_idx;
+    w_out[lane] = p;
+  }
+}
+
+__device__ __forceinline__ void route_token_any(const Args& a, int t, int lane, int* idx_out,
+                                                float* w_out) {
+  if (a.E <= 2 * kWave) route_token<2>(a, t, lane, idx_out, w_out);
+  else if (a.E <= 4 * kWave) route_token<4>(a, t, lane, idx_out, w_out);
+  else route_token<kMaxExperts / kWave>(a, t, lane, idx_out, w_out);
+}
+
+// Routing (layer mode) or id/weight load, then the Token-Union alignment:
+// the first-occurrence rank of every distinct valid id in slot order
+// (marlin.cu:298-319) and each slot's unique index.  All T threads.
+template <int T>
+__device__ void prologue(const Args& a, Prologue& P) {
+  constexpr int W = T / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int S = a.S;
+  if (a.logits) {
+    for (int t = wave; t < a.M; t += W) {
+      // lane r writes slot t*top_k + r directly
+      route_token_any(a, t, lane, P.slot_e + t * a.top_k, P.slot_w + t * a.top_k);
+    }
+    __syncthreads();
+    if (tid < S) {
+      const float wr = round_to_bf16(P.slot_w[tid]);
+      P.slot_w[tid] = wr;
+      if (blockIdx.x == 0) {
+        if (a.out_idx) a.out_idx[tid] = P.slot_e[tid];
+        if (a.out_w) a.out_w[tid] = f32_to_bf16(wr);
+      }
+    }
+  } else if (tid < S) {
+    const int e = load_expert_id(a.idx, a.idx_is64, tid);
+    P.slot_e[tid] = (e >= 0 && e < a.E) ? e : -1;
+    P.slot_w[tid] = a.w ? load_weight_as_bf16(a.w, a.w_dtype, tid) : 0.f;
+  }
+  for (int i = tid; i < a.E; i += T) P.first_slot[i] = INT_MAX;
+  __syncthreads();
+  int e = -1;
+  if (tid < S) {
+    e = P.slot_e[tid];
+    if (e >= 0) atomicMin(&P.first_slot[e], tid);
+  }
+  __syncthreads();
+  const bool is_first = tid < S && e >= 0 && P.first_slot[e] == tid;
+  const unsigned long long bal = __ballot(is_first);
+  const int below = __popcll(bal & ((1ull << lane) - 1ull));
+  if (lane == 0) P.wave_cnt[wave] = __popcll(bal);
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int c = P.wave_cnt[w];
+    base += (w < wave) ? c : 0;
+    total += c;
+  }
+  if (is_first) {
+    P.uexp[base + below] = e;
+    P.rank_of_slot[tid] = base + below;
+  }
+  if (tid == 0) P.n_unique = total;
+  __syncthreads();
+  if (tid < S) P.slot_u[tid] = e >= 0 ? P.rank_of_slot[P.first_slot[e]] : -1;
+  __syncthreads();
+}
+
+// Collect the slots (ascending) routed to unique expert u into P.list.
+template <int T>
+__device__ void gather_list(const Args& a, Prologue& P, int u) {
+  constexpr int W = T / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const bool mine = tid < a.S && P.slot_u[tid] == u;
+  const unsigned long long bal = __ballot(mine);
+  const int below = __popcll(bal & ((1ull << lane) - 1ull));
+  __syncthreads();  // earlier readers of list / wave_cnt are done
+  if (lane == 0) P.wave_cnt[wave] = __popcll(bal);
+  __syncthreads();
+  int base = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < W; ++w) {
+    const int c = P.wave_cnt[w];
+    base += (w < wave) ? c : 0;
+    total += c;
+  }
+  if (mine) P.list[base + below] = tid;
+  if (tid == 0) P.n_list = total;
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------------------
+// task (u, c)
+// ---------------------------------------------------------------------------
+template <int CG, int NT, int JGM>
+__device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char* smem) {
+  constexpr int T = 16 * CG;      // threads
+  constexpr int W = T / kWave;    // waves
+  constexpr int L = CG / 2;       // lanes per packed row: CG/4 gate quads + CG/4 up quads
+  constexpr int HALF = CG / 4;
+  constexpr int DR = CG / 8;      // packed rows of the down projection this task meets
+  const int tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA base in M0
+  const int q = tid % L, rl = tid / L;  // rl in [0, 32): this lane's row within a 32-row step
+  const bool is_up = q >= HALF;
+  const int cq = is_up ? q - HALF : q;
+  const int icol = c * CG + cq * 4;     // intermediate column of this lane's quad
+  const bool col_ok = icol < a.I;
+  const int e = P.uexp[u];
+  const int Kp = a.H >> 3, Ip = a.I >> 3, twoI = 2 * a.I, rpg = a.gs >> 3, HQ = a.H >> 2;
+
+  uint32_t* slab = (uint32_t*)(smem + a.off_slab);
+  uint4* xs = (uint4*)(smem + a.off_xs);
+  float* xb = (float*)(smem + a.off_xb);
+  uint2* sct = (uint2*)(smem + a.off_sct);
+  float* red = (float*)(smem + a.off_red);
+  uint16_t* actp = (uint16_t*)(smem + a.off_actp);
+  float* actb = (float*)(smem + a.off_actb);
+
+  // (1) Down-projection rows [c*DR, c*DR+DR) of expert e, all H columns,
+  //     straight into LDS: one wave instruction moves 1 KB (64 lanes x 16 B).
+  {
+    const int32_t* dp = a.d_packed + (size_t)e * Ip * a.H;
+    const int cpr = (HQ + kWave - 1) / kWave;  // 1 KB chunks per row
+    for (int ch = wave; ch < DR * cpr; ch += W) {
+      const int r = ch / cpr, cc = ch - r * cpr;
+      const int row = c * DR + r;
+      const int qd = cc * kWave + lane;
+      if (row < Ip && qd < HQ) {
+        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(dp + (size_t)row * a.H + 4 * qd),
+                                         (lds_ptr_t)(slab + r * a.H + 4 * cc * kWave), 16, 0, 0);
+      }
+    }
+  }
+
+  // (2) gate/up scales of the tile -> LDS as [group][gate quads | up quads].
+  //     Loaded before the weights: the in-order vmcnt wait their LDS stores
+  //     need does not then wait for the weight stream.
+  {
+    const uint16_t* sp = a.gu_scales + (size_t)e * a.Ggu * twoI;
+    for (int i = tid; i < a.Ggu * L; i += T) {
+      const int g = i / L, qq = i - g * L;
+      const int cqq = qq < HALF ? qq : qq - HALF;
+      const int ic = c * CG + cqq * 4;
+      uint2 v = make_uint2(0u, 0u);
+      if (ic < a.I) v = *(const uint2*)(sp + (size_t)g * twoI + (qq < HALF ? 0 : a.I) + ic);
+      sct[i] = v;
+    }
+  }
+
+  // (3) gate/up words of this lane's column quad, every 32nd row: registers.
+  const int32_t* gp = a.gu_packed + (size_t)e * Kp * twoI + (is_up ? a.I : 0) + icol;
+  uint4 wv[JGM];
+  bool ok[JGM];
+#pragma unroll
+  for (int j = 0; j < JGM; ++j) {
+    const int r = 32 * j + rl;
+    ok[j] = col_ok && r < Kp && r / rpg < a.Ggu;
+    wv[j] = ok[j] ? load_nt_u4(gp + (size_t)r * twoI) : make_uint4(0u, 0u, 0u, 0u);
+  }
+
+  // (4) down scales of this thread's output quads (one group per slab when
+  //     gs is a multiple of CG; otherwise looked up per row below).
+  constexpr int DQM = 2;  // output quads per thread (H <= 2*4*T)
+  const int g0 = (c * DR) / rpg, g1 = (c * DR + DR - 1) / rpg;
+  const bool one_group = g0 == g1;
+  const uint16_t* dsp = a.d_scales + (size_t)e * a.Gd * a.H;
+  uint2 sd[DQM];
+  const uint32_t m43 = magic43();
+#pragma unroll
+  for (int m = 0; m < DQM; ++m) {
+    const int hq = tid + m * T;
+    sd[m] = (one_group && g0 < a.Gd && hq < HQ) ? *(const uint2*)(dsp + (size_t)g0 * a.H + 4 * hq)
+                                                 : make_uint2(0u, 0u);
+  }
+
+  gather_list<T>(a, P, u);
+  const int nmatch = P.n_list;
+
+  for (int c0 = 0; c0 < nmatch; c0 += NT) {
+    const int nch = min(NT, nmatch - c0);
+    // stage x rows of the chunk's tokens (pair-permuted + bias)
+    for (int i = tid; i < nch * Kp; i += T) {
+      const int n = i / Kp, r = i - n * Kp;
+      const int tok = P.list[c0 + n] / a.top_k;
+      const uint4 d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
+      xs[n * Kp + r] = pair_permute(d);
+      xb[n * Kp + r] = neg_bias_136(d);
+    }
+    __syncthreads();
+
+    // gate/up partial sums over this lane's rows
+    float acc[4][NT];
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[qq][n] = 0.f;
+#pragma unroll
+    for (int j = 0; j < JGM; ++j) {
+      if (!ok[j]) continue;
+      const int r = 32 * j + rl;
+      const uint2 s2 = sct[(r / rpg) * L + q];
+      const float s[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const uint4 w = opaque(wv[j]);
+      const uint32_t wq[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+      for (int n = 0; n < NT; ++n) {
+        if (n < nch) {
+          const uint4 xp = xs[n * Kp + r];
+          const float b = xb[n * Kp + r];
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) acc[qq][n] += s[qq] * dot8_q4(wq[qq], xp, b, m43);
+        }
+      }
+    }
+    // lanes of one wave that share q hold different rows: reduce, then waves via LDS
+#pragma unroll
+    for (int qq = 0; qq < 4; ++qq)
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[qq][n] = reduce_across_groups<L>(acc[qq][n]);
+    if (lane < L) {
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq)
+          red[(wave * NT + n) * 2 * CG + (is_up ? CG : 0) + cq * 4 + qq] = acc[qq][n];
+    }
+    __syncthreads();
+
+    // gelu_tanh(gate) * up, rounded to bf16, pair-permuted per packed row, + bias
+    if (tid < nch * CG) {
+      const int n = tid / CG, ci = tid - n * CG;
+      float g = 0.f, up = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < W; ++w2) {
+        g += red[(w2 * NT + n) * 2 * CG + ci];
+        up += red[(w2 * NT + n) * 2 * CG + CG + ci];
+      }
+      const float av = (c * CG + ci < a.I) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
+      float s8 = av;  // sum over the 8 activations of this packed row (8 adjacent lanes)
+      s8 += __shfl_xor(s8, 1, kWave);
+      s8 += __shfl_xor(s8, 2, kWave);
+      s8 += __shfl_xor(s8, 4, kWave);
+      const int r8 = ci >> 3, p = ci & 7;
+      actp[(n * DR + r8) * 8 + 2 * (p & 3) + (p >> 2)] = f32_to_bf16(av);
+      if (p == 0) actb[n * DR + r8] = -136.0f * s8;
+    }
+    wait_vmem();       // this thread's direct-to-LDS loads of the down rows
+    __syncthreads();
+
+    // down: y[h] = sum over the task's CG activations of act * w_down
+    const uint4* actq = (const uint4*)actp;
+#pragma unroll
+    for (int m = 0; m < DQM; ++m) {
+      const int hq = tid + m * T;
+      if (hq >= HQ) continue;
+      uint4 dw[DR];
+      float s[DR][4];
+#pragma unroll
+      for (int r = 0; r < DR; ++r) {
+        const int row = c * DR + r;
+        const int g = row / rpg;
+        const bool rok = row < Ip && g < a.Gd;
+        dw[r] = rok ? *(const uint4*)(slab + r * a.H + 4 * hq) : make_uint4(0u, 0u, 0u, 0u);
+        uint2 s2 = sd[m];
+        if (!one_group) s2 = rok ? *(const uint2*)(dsp + (size_t)g * a.H + 4 * hq) : make_uint2(0u, 0u);
+        if (!rok) s2 = make_uint2(0u, 0u);
+        s[r][0] = bf16lo(s2.x);
+        s[r][1] = bf16hi(s2.x);
+        s[r][2] = bf16lo(s2.y);
+        s[r][3] = bf16hi(s2.y);
+      }
+      for (int n = 0; n < nch; ++n) {
+        float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < DR; ++r) {
+          const uint4 xp = actq[n * DR + r];
+          const float b = actb[n * DR + r];
+          const uint32_t wq[4] = {dw[r].x, dw[r].y, dw[r].z, dw[r].w};
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) y[qq] += s[r][qq] * dot8_q4(wq[qq], xp, b, m43);
+        }
+        const int slot = P.list[c0 + n];
+        const float ws = P.slot_w[slot];
+        float* dst = a.part + ((size_t)slot * a.Tg + c) * a.H + 4 * hq;
+        st_coherent_f32(dst + 0, y[0] * ws);
+        st_coherent_f32(dst + 1, y[1] * ws);
+        st_coherent_f32(dst + 2, y[2] * ws);
+        st_coherent_f32(dst + 3, y[3] * ws);
+      }
+    }
+    __syncthreads();  // xs / red / act reused by the next chunk or task
+  }
+}
+
+// ---------------------------------------------------------------------------
+// reduction of the partials into out
+// ---------------------------------------------------------------------------
+template <int T>
+__device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratch) {
+  const int tid = threadIdx.x;
+  const int HQ = a.H >> 2, total = a.M * HQ;
+  const int qpw = a.qpw, stripes = T / qpw;
+  const int qi = tid & (qpw - 1), st = tid / qpw;
+  const int np = a.top_k * a.Tg;
+  for (int qb = blockIdx.x * qpw; qb < total; qb += gridDim.x * qpw) {
+    const int quad = qb + qi;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (quad < total) {
+      const int t = quad / HQ, hq = quad - t * HQ;
+      for (int p = st; p < np; p += stripes) {
+        const int k = p / a.Tg, cc = p - k * a.Tg;
+        const int s = t * a.top_k + k;
+        if (P.slot_u[s] >= 0) {
+          const float* src = a.part + ((size_t)s * a.Tg + cc) * a.H + 4 * hq;
+          const uint4 v = ld_coherent_u4(src);
+          acc.x += __uint_as_float(v.x);
+          acc.y += __uint_as_float(v.y);
+          acc.z += __uint_as_float(v.z);
+          acc.w += __uint_as_float(v.w);
+        }
+      }
+    }
+    scratch[tid] = acc;
+    __syncthreads();
+    // fixed-shape tree over the stripes (deterministic order)
+    for (int half = stripes >> 1; half >= 1; half >>= 1) {
+      if (st < half) {
+        const float4 v = scratch[tid + half * qpw];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+        scratch[tid] = acc;
+      }
+      __syncthreads();
+    }
+    if (tid < qpw && quad < total) {
+      float4 sum = acc;
+      const int t = quad / HQ, hq = quad - t * HQ;
+      uint2* o = (uint2*)(a.out + (size_t)t * a.H + 4 * hq);
+      if (!a.overwrite) {
+        const uint2 old = *o;
+        sum.x += bf16lo(old.x);
+        sum.y += bf16hi(old.x);
+        sum.z += bf16lo(old.y);
+        sum.w += bf16hi(old.y);
+      }
+      *o = make_uint2((uint32_t)f32_to_bf16(sum.x) | ((uint32_t)f32_to_bf16(sum.y) << 16),
+                      (uint32_t)f32_to_bf16(sum.z) | ((uint32_t)f32_to_bf16(sum.w) << 16));
+    }
+    __syncthreads();
+  }
+}
+
+template <int CG, int NT, int JGM>
+__global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
+  constexpr int T = 16 * CG;
+  __shared__ Prologue P;
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int tid = threadIdx.x;
+  prologue<T>(a, P);
+  const int ntask = P.n_unique * a.Tg;
+  for (int t = blockIdx.x; t < ntask; t += gridDim.x) run_task<CG, NT, JGM>(a, P, t / a.Tg, t % a.Tg, smem);
+
+  // grid-wide barrier: every partial of every task is written
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0) {
+    atomic_add_relaxed(&a.ctr[0], 1);
+    int spins = 0;
+    while (load_relaxed(&a.ctr[0]) < (int)gridDim.x) {
+      if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
+        atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
+  __syncthreads();
+  reduce_partials<T>(a, P, (float4*)(smem + a.off_slab));
+  if (tid == 0) {
+    if (atomic_add_relaxed(&a.ctr[1], 1) == (int)gridDim.x - 1) {
+      store_relaxed(&a.ctr[0], 0);
+      store_relaxed(&a.ctr[1], 0);
+    }
+  }
+}
+
+// Export of the alignment (gi_moe_align): one workgroup of 256 threads.
+__global__ __launch_bounds__(256) void moe_align_kernel(Args a, int32_t* uniq, int32_t* nuniq,
+                                                         int32_t* s2u, int32_t* offsets,
+                                                         int32_t* slots) {
+  __shared__ Prologue P;
+  prologue<256>(a, P);
+  const int tid = threadIdx.x;
+  const int U = P.n_unique;
+  if (tid < U) uniq[tid] = P.uexp[tid];
+  if (tid == 0) *nuniq = U;
+  if (tid < a.S) s2u[tid] = P.slot_u[tid];
+  if (tid == 0) {
+    int run = 0;
+    offsets[0] = 0;
+    for (int u = 0; u < U; ++u) {
+      int cnt = 0;
+      for (int s = 0; s < a.S; ++s) cnt += P.slot_u[s] == u;
+      run += cnt;
+      offsets[u + 1] = run;
+    }
+  }
+  if (tid < a.S && P.slot_u[tid] >= 0) {
+    const int u = P.slot_u[tid];
+    int before = 0, pos = 0;
+    for (int s = 0; s < a.S; ++s) {
+      const int su = P.slot_u[s];
+      before += (su >= 0 && su < u);
+      pos += (s < tid && su == u);
+    }
+    slots[before + pos] = tid;
+  }
+}
+
+// Router only (gi_moe_route_topk_softmax): one wave per token.
+__global__ __launch_bounds__(256) void route_kernel(Args a, int32_t* out_idx, void* out_w,
+                                                    int w_dtype) {
+  __shared__ int r_idx[4][64];
+  __shared__ float r_w[4][64];
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  if (t >= a.M) return;
+  route_token_any(a, t, lane, r_idx[wave], r_w[wave]);
+  if (lane < a.top_k) {
+    const int s = t * a.top_k + lane;
+    out_idx[s] = r_idx[wave][lane];
+    const float p = r_w[wave][lane];
+    if (w_dtype == GI_DTYPE_BF16) ((uint16_t*)out_w)[s] = f32_to_bf16(p);
+    else if (w_dtype == GI_DTYPE_FP16) ((_Float16*)out_w)[s] = (_Float16)p;
+    else ((float*)out_w)[s] = p;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+constexpr size_t kAlign = 256;
+inline size_t round_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a; }
+
+struct WsLayout {
+  size_t status, ctr, part, total;
+};
+
+int pick_cg(int rows) { return rows <= 1 ? 32 : 32; }
+int tiles_per_expert(int I, int cg) { return (I + cg - 1) / cg; }
+
+WsLayout ws_layout(int S, int H, int I, int cg) {
+  WsLayout L;
+  L.status = 0;
+  L.ctr = 64;
+  L.part = kAlign;
+  L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
+  return L;
+}
+
+struct LdsLayout {
+  int slab, xs, xb, sct, red, actp, actb, total;
+};
+
+LdsLayout lds_layout(int cg, int nt, int H, int I, int Ggu) {
+  const int T = 16 * cg, W = T / 64, DR = cg / 8, Kp = H / 8;
+  (void)I;
+  LdsLayout L;
+  int off = 0;
+  auto take = [&](int bytes) {
+    const int o = off;
+    off += (bytes + 15) / 16 * 16;
+    return o;
+  };
+  const int slab = DR * H * 4, scratch = T * 16;
+  L.slab = take(slab > scratch ? slab : scratch);
+  L.xs = take(nt * Kp * 16);
+  L.xb = take(nt * Kp * 4);
+  L.sct = take(Ggu * (cg / 2) * 8);
+  L.red = take(W * nt * 2 * cg * 4);
+  L.actp = take(nt * DR * 16);
+  L.actb = take(nt * DR * 4);
+  L.total = off;
+  return L;
+}
+
+struct OccEntry {
+  int device;
+  const void* fn;
+  size_t dyn;
+  int blocks;
+};
+std::mutex g_occ_mu;
+OccEntry g_occ[64];
+int g_occ_n = 0;
+
+int blocks_per_cu(const void* fn, int threads, size_t dyn, int* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  {
+    std::lock_guard<std::mutex> lk(g_occ_mu);
+    for (int i = 0; i < g_occ_n; ++i)
+      if (g_occ[i].device == dev && g_occ[i].fn == fn && g_occ[i].dyn == dyn) {
+        *out = g_occ[i].blocks;
+        return GI_OK;
+      }
+  }
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
+  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
+  int b = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, threads, dyn);
+  if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  std::lock_guard<std::mutex> lk(g_occ_mu);
+  if (g_occ_n < 64) g_occ[g_occ_n++] = OccEntry{dev, fn, dyn, b};
+  *out = b;
+  return GI_OK;
+}
+
+template <int CG, int NT, int JGM>
+int launch_variant(Args k, int umax, hipStream_t stream) {
+  constexpr int T = 16 * CG;
+  const LdsLayout L = lds_layout(CG, NT, k.H, k.I, k.Ggu);
+  k.off_slab = L.slab;
+  k.off_xs = L.xs;
+  k.off_xb = L.xb;
+  k.off_sct = L.sct;
+  k.off_red = L.red;
+  k.off_actp = L.actp;
+  k.off_actb = L.actb;
+  const void* fn = (const void*)fused_moe_kernel<CG, NT, JGM>;
+  int bpc = 0;
+  int st = blocks_per_cu(fn, T, (size_t)L.total, &bpc);
+  if (st != GI_OK) return st;
+  if (bpc < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE kernel does not fit on a CU");
+  const long long tasks = (long long)(umax > 0 ? umax : 1) * k.Tg;
+  const long long resident = (long long)bpc * device_cu_count();
+  const int grid = (int)(tasks < resident ? tasks : resident);
+  // reduction split: output quads per workgroup pass (power of two <= T)
+  const int total_quads = k.M * (k.H / 4);
+  const int per = (total_quads + grid - 1) / grid;
+  int qpw = 1;
+  while (qpw < per && qpw < T) qpw <<= 1;
+  k.qpw = qpw;
+  hipLaunchKernelGGL((fused_moe_kernel<CG, NT, JGM>), dim3(grid), dim3(T), (size_t)L.total,
+                     stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
+  return GI_OK;
+}
+
+template <int CG, int NT>
+int launch_jgm(const Args& k, int umax, hipStream_t stream) {
+  const int steps = ((k.H >> 3) + 31) / 32;
+  if (steps <= 2) return launch_variant<CG, NT, 2>(k, umax, stream);
+  if (steps <= 11) return launch_variant<CG, NT, 11>(k, umax, stream);
+  return launch_variant<CG, NT, 16>(k, umax, stream);
+}
+
+int check_moe_shapes(const MoeHostArgs& a) {
+  if (a.M < 0 || a.H <= 0 || a.I <= 0 || a.E <= 0 || a.top_k <= 0)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: M must be >= 0 and H, I, E, top_k positive");
+  if (a.H % 8 || a.I % 8)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: H and I must be multiples of 8 (8 codes per int32)");
+  if (a.gs <= 0 || a.gs % 8)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: group_size must be a positive multiple of 8");
+  if (a.E > kMaxExperts) return fail(GI_ERR_UNSUPPORTED, "fused MoE: at most 1024 experts");
+  if (a.top_k > kMaxSlots) return fail(GI_ERR_UNSUPPORTED, "fused MoE: top_k must be <= 256");
+  if (a.Ggu <= 0 || a.Gd <= 0)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: scale tensors need at least one group");
+  if (a.H > 4096) return fail(GI_ERR_UNSUPPORTED, "fused MoE: H <= 4096 is supported");
+  if (a.logits && a.top_k > 64)
+    return fail(GI_ERR_UNSUPPORTED, "fused MoE: in-kernel routing supports top_k <= 64");
+  if (!a.x || !a.gu_packed || !a.gu_scales || !a.d_packed || !a.d_scales || !a.out)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: null tensor pointer");
+  if (!a.logits && (!a.idx || !a.w))
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: null expert_indices / expert_weights");
+  if ((((uintptr_t)a.x) | ((uintptr_t)a.gu_packed) | ((uintptr_t)a.d_packed)) % 16)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: x and packed weights must be 16-byte aligned");
+  if ((((uintptr_t)a.gu_scales) | ((uintptr_t)a.d_scales) | ((uintptr_t)a.out)) % 8)
+    return fail(GI_ERR_INVALID_ARG, "fused MoE: scales and out must be 8-byte aligned");
+  return GI_OK;
+}
+
+}  // namespace
+
+int moe_rows_per_launch(int top_k) { return top_k > 0 ? kMaxSlots / top_k : 0; }
+
+size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
+  (void)E;
+  const int per = moe_rows_per_launch(top_k);
+  int r = rows < per ? rows : per;
+  if (r < 1) r = 1;
+  // the largest tile count any launch of this call may use
+  const size_t a = ws_layout(r * top_k, H, I, pick_cg(r)).total;
+  const size_t b = ws_layout(r * top_k, H, I, pick_cg(1)).total;
+  return a > b ? a : b;
+}
+
+int launch_fused_moe(const MoeHostArgs& h) {
+  int st = check_moe_shapes(h);
+  if (st != GI_OK) return st;
+  if (h.M == 0) return GI_OK;
+  const int rows_per = moe_rows_per_launch(h.top_k);
+  if (h.logits && h.M > rows_per)
+    return fail(GI_ERR_UNSUPPORTED, "fused MoE layer: M*top_k must be <= 256");
+  if (!h.workspace || h.workspace_bytes < moe_workspace_bytes(h.M, h.top_k, h.H, h.I, h.E))
+    return fail(GI_ERR_WORKSPACE,
+                "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
+  if (((uintptr_t)h.workspace) % kAlign)
+    return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
+
+  char* ws = (char*)h.workspace;
+  Args k{};
+  k.gu_packed = h.gu_packed;
+  k.gu_scales = (const uint16_t*)h.gu_scales;
+  k.d_packed = h.d_packed;
+  k.d_scales = (const uint16_t*)h.d_scales;
+  k.logits = h.logits;
+  k.logits_dtype = h.logits_dtype;
+  k.expert_scale = h.expert_scale;
+  k.out_idx = h.out_idx;
+  k.out_w = (uint16_t*)h.out_w;
+  k.idx_is64 = h.idx_is64;
+  k.w_dtype = h.w_dtype;
+  k.H = h.H;
+  k.I = h.I;
+  k.E = h.E;
+  k.top_k = h.top_k;
+  k.gs = h.gs;
+  k.Ggu = h.Ggu;
+  k.Gd = h.Gd;
+  k.overwrite = h.overwrite;
+  k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
+
+  const size_t idx_es = h.idx_is64 ? 8 : 4;
+  const size_t w_es = h.w_dtype == GI_DTYPE_FP32 ? 4 : 2;
+  for (int r0 = 0; r0 < h.M; r0 += rows_per) {
+    const int rows = (h.M - r0) < rows_per ? (h.M - r0) : rows_per;
+    const int cg = pick_cg(rows);
+    const WsLayout L = ws_layout(rows * h.top_k, h.H, h.I, cg);
+    k.status = (int*)(ws + L.status);
+    k.ctr = (int*)(ws + L.ctr);
+    k.part = (float*)(ws + L.part);
+    k.M = rows;
+    k.S = rows * h.top_k;
+    k.Tg = tiles_per_expert(h.I, cg);
+    k.x = (const uint16_t*)h.x + (size_t)r0 * h.H;
+    k.out = (uint16_t*)h.out + (size_t)r0 * h.H;
+    k.idx = h.idx ? (const char*)h.idx + (size_t)r0 * h.top_k * idx_es : nullptr;
+    k.w = h.w ? (const char*)h.w + (size_t)r0 * h.top_k * w_es : nullptr;
+    if (h.logits) k.logits = (const char*)h.logits + (size_t)r0 * h.E * (h.logits_dtype == GI_DTYPE_FP32 ? 4 : 2);
+    const int umax = k.S < h.E ? k.S : h.E;
+    st = rows == 1 ? launch_jgm<32, 1>(k, umax, h.stream) : launch_jgm<32, 4>(k, umax, h.stream);
+    if (st != GI_OK) return st;
+  }
+  return GI_OK;
+}
+
+int launch_moe_align(const void* idx, int is64, int M, int top_k, int E, int32_t* uniq,
+                     int32_t* nuniq, int32_t* s2u, int32_t* offsets, int32_t* slots,
+                     hipStream_t stream) {
+  if (M <= 0 || top_k <= 0 || E <= 0)
+    return fail(GI_ERR_INVALID_ARG, "moe_align: M, top_k, E must be positive");
+  if ((long long)M * top_k > kMaxSlots) return fail(GI_ERR_UNSUPPORTED, "moe_align: M*top_k must be <= 256");
+  if (E > kMaxExperts) return fail(GI_ERR_UNSUPPORTED, "moe_align: at most 1024 experts");
+  if (!idx || !uniq || !nuniq || !s2u || !offsets || !slots)
+    return fail(GI_ERR_INVALID_ARG, "moe_align: null pointer");
+  Args k{};
+  k.idx = idx;
+  k.idx_is64 = is64;
+  k.M = M;
+  k.top_k = top_k;
+  k.E = E;
+  k.S = M * top_k;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(256), 0, stream, k, uniq, nuniq, s2u, offsets,
+                     slots);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "moe_align launch");
+  return GI_OK;
+}
+
+int launch_route(const void* logits, int logits_dtype, const float* expert_scale, int M, int E,
+                 int top_k, int32_t* out_idx, void* out_w, int w_dtype, hipStream_t stream) {
+  if (M < 0 || E <= 0 || top_k <= 0) return fail(GI_ERR_INVALID_ARG, "route: bad M, E or top_k");
+  if (E > kMaxExperts) return fail(GI_ERR_UNSUPPORTED, "route: at most 1024 experts");
+  if (top_k > E || top_k > 64) return fail(GI_ERR_UNSUPPORTED, "route: top_k must be <= min(E, 64)");
+  if (logits_dtype != GI_DTYPE_BF16 && logits_dtype != GI_DTYPE_FP32)
+    return fail(GI_ERR_UNSUPPORTED, "route: logits must be bf16 or fp32");
+  if (w_dtype != GI_DTYPE_BF16 && w_dtype != GI_DTYPE_FP16 && w_dtype != GI_DTYPE_FP32)
+    return fail(GI_ERR_UNSUPPORTED, "route: weights must be bf16, fp16 or fp32");
+  if (!logits || !out_idx || !out_w) return fail(GI_ERR_INVALID_ARG, "route: null pointer");
+  if (M == 0) return GI_OK;
+  Args k{};
+  k.logits = logits;
+  k.logits_dtype = logits_dtype;
+  k.expert_scale = expert_scale;
+  k.M = M;
+  k.E = E;
+  k.top_k = top_k;
+  hipLaunchKernelGGL(route_kernel, dim3((M + 3) / 4), dim3(256), 0, stream, k, out_idx, out_w,
+                     w_dtype);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "route launch");
+  return GI_OK;
+}
+
+int read_workspace_status(void* workspace, int32_t* host_status, hipStream_t stream) {
+  if (!workspace || !host_status) return fail(GI_ERR_INVALID_ARG, "workspace_status: null pointer");
+  hipError_t e = hipMemcpyAsync(host_status, workspace, sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return hip_fail(e, "workspace_status copy");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "workspace_status sync");
+  e = hipMemsetAsync(workspace, 0, sizeof(int32_t), stream);
+  if (e != hipSuccess) return hip_fail(e, "workspace_status clear");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "workspace_status sync");
+  return GI_OK;
+}
+
+}  // namespace gi

@@ -69,6 +69,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
   const int col = tile * kCols + colq * 4;
   const bool col_ok = col < a.N;
   const int steps = (nrows + kRowsPerStep - 1) / kRowsPerStep;
+  const uint32_t m43 = magic43();
   const int nbatch = (steps + kBatch - 1) / kBatch;
 
   for (int t0 = 0; t0 < a.M; t0 += NT) {
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
               const uint4 xp = xs[n * a.stage_stride + rl];
               const float bias = xb[n * a.stage_stride + rl];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) acc[q][n] += sv[q] * dot8_q4(wv[q], xp, bias);
+              for (int q = 0; q < 4; ++q) acc[q][n] += sv[q] * dot8_q4(wv[q], xp, bias, m43);
             }
           }
         }
@@ -156,15 +157,17 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
         for (int w = 0; w < kWaves; ++w) y += red[(w * NT + n) * kCols + cc];
         const size_t o = (size_t)(t0 + n) * a.N + oc;
         if (a.ks == 1) a.C[o] = f32_to_bf16(epilogue(y, a.cap));
-        else a.part[(size_t)split * a.M * a.N + o] = y;
+        else st_coherent_f32(a.part + (size_t)split * a.M * a.N + o, y);
       }
     }
   }
   if (a.ks == 1) return;
 
-  // Last K-slice to arrive for this column tile reduces the partials in order.
+  // Last K-slice to arrive for this column tile reduces the partials in order
+  // (partials travel through sc1 stores/loads, see gi_common.h).
+  wait_vmem();
   __syncthreads();
-  if (tid == 0) last = atomic_add_acq_rel(&a.ctr[tile], 1) == a.ks - 1;
+  if (tid == 0) last = atomic_add_relaxed(&a.ctr[tile], 1) == a.ks - 1;
   __syncthreads();
   if (!last) return;
   for (int i = tid; i < a.M * kCols; i += kThreads) {
@@ -173,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
     if (oc < a.N) {
       const size_t o = (size_t)t * a.N + oc;
       float y = 0.f;
-      for (int s = 0; s < a.ks; ++s) y += a.part[(size_t)s * a.M * a.N + o];
+      for (int s = 0; s < a.ks; ++s) y += ld_coherent_f32(a.part + (size_t)s * a.M * a.N + o);
       a.C[o] = f32_to_bf16(epilogue(y, a.cap));
     }
   }
