@@ -89,3 +89,21 @@ def test_companions_match_cpu_semantics():
     gemmainfer_csrc.fused_rope_inplace(qc, kc, cos, sin, pos)
     torch.testing.assert_close(qd.cpu().float(), qc.float(), rtol=2e-2, atol=2e-2)
     torch.testing.assert_close(kd.cpu().float(), kc.float(), rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("name", ["linear_m1_k256_n96_gs64", "linear_m5_k512_n128_gs128",
+                                  "linear_m3_k2816_n64_gs128"])
+def test_w4a16_matches_reference_golden(name):
+    """Inputs/outputs produced by the reference's own CPU fallback (pybind.cpp:46-85)."""
+    from pathlib import Path
+    g = dict(np.load(Path(__file__).resolve().parent / "golden" / f"{name}.npz"))
+    bf = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)  # noqa: E731
+    A, S = bf(g["A_bf16"]), bf(g["scales_bf16"])
+    B = torch.from_numpy(g["B_packed"])
+    gs = int(g["group_size"])
+    C = torch.empty(A.shape[0], B.shape[1], dtype=torch.bfloat16, device=DEV)
+    gemmainfer_csrc.marlin_w4a16(A.to(DEV), B.to(DEV), S.to(DEV), C, gs)
+    ref = O.bf16_bits_to_f64(g["C_bf16"])
+    st = O.error_stats(np64(C), ref)
+    assert st["rel_l2"] < 4e-3, st
+    assert np.all(np.abs(np64(C) - ref) <= 2.0 ** -6 * np.abs(ref) + 1e-2), st

@@ -216,3 +216,32 @@ def test_device_status_clean_and_timeout_path(small):
     ref, _ = _oracle_moe(x.cpu(), W, idx.cpu(), w.cpu(), torch.zeros(4, 256), 64)
     assert_bf16_close(out2, ref, "after timeout path")
     assert ops.workspace_status() == 0
+
+
+# ---------------------------------------------------------------- golden vectors
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+
+
+def _bits_to_bf16(a):
+    return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+
+
+@pytest.mark.parametrize("name", ["moe_m5_small_top2_gs64", "moe_m1_small_top2_gs64", "moe_m3_dups_gs64"])
+def test_fused_matches_reference_golden(name):
+    """Inputs/outputs produced by the reference's own CPU fallback (pybind.cpp:198-245)."""
+    g = dict(np.load(GOLDEN / f"{name}.npz"))
+    x = _bits_to_bf16(g["x_bf16"])
+    gus, ds, w = (_bits_to_bf16(g[k]) for k in ("gate_up_scales_bf16", "down_scales_bf16", "w_bf16"))
+    gu, dp, idx = (torch.from_numpy(g[k]) for k in ("gate_up_packed", "down_packed", "idx"))
+    gs = int(g["group_size"])
+    out = torch.zeros_like(x).to(DEV)
+    ops.fused_batched_moe(x.to(DEV), gu.to(DEV), gus.to(DEV), dp.to(DEV), ds.to(DEV), idx.to(DEV),
+                          w.to(DEV), out, gs)
+    ref_golden = O.bf16_bits_to_f64(g["out_bf16"])
+    # the reference fallback rounds several intermediates to bf16 (see tests/test_oracle.py)
+    st = O.error_stats(np64(out), ref_golden)
+    assert st["rel_l2"] < 1.5e-2 and st["max_abs_over_rms"] < 0.1, st
+    # and the strict gate against the float64 oracle on the same inputs
+    oracle, _ = O.fused_batched_moe(np64(x), g["gate_up_packed"], np64(gus), g["down_packed"], np64(ds),
+                                    g["idx"], np64(w), np.zeros(x.shape), gs)
+    assert_bf16_close(out, oracle, name)
