@@ -48,7 +48,10 @@ namespace {
 constexpr int kMaxSlots = 256;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxWaves = 16;
+constexpr int kRankMax = 256;  // M*E of the rank-counting router (4 lanes per key)
 constexpr int kDefaultSpin = 1 << 22;
+constexpr int kBarrierSubs = 8;    // first-level arrival counters of the grid barrier
+constexpr int kCtrStride = 32;     // ints between counters (128 bytes: separate lines)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -67,14 +70,14 @@ struct Args {
   uint16_t* out_w;
   uint16_t* out;
   float* part;      // [S][Tg][H] fp32 partials
-  int* ctr;         // [0] arrivals, [1] departures
+  int* ctr;         // grid barrier: [0] generation, [kCtrStride] top, [2*kCtrStride + i*kCtrStride] sub i
   int* status;
   int idx_is64, w_dtype, logits_dtype;
   int M, H, I, E, top_k, gs, Ggu, Gd, S, Tg;
   int overwrite, spin_limit;
   int qpw;          // reduction: output quads per workgroup pass (power of two)
   // dynamic LDS layout (bytes)
-  int off_slab, off_xs, off_xb, off_sct, off_red, off_actp, off_actb;
+  int off_slab, off_xs, off_xb, off_red, off_actp, off_actb;
 };
 
 struct Prologue {
@@ -86,6 +89,7 @@ struct Prologue {
   int uexp[kMaxSlots];        // expert id of each unique index
   int list[kMaxSlots];        // slots of the current task's expert, ascending
   int wave_cnt[kMaxWaves];
+  uint32_t keys[kRankMax];    // routing keys, rank path (M*E*4 <= threads)
   int n_unique;
   int n_list;
 };
@@ -188,12 +192,60 @@ __device__ void prologue(const Args& a, Prologue& P) {
   constexpr int W = T / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int S = a.S;
-  if (a.logits) {
+  if (a.logits && a.M * a.E * 4 <= T) {
+    // Rank counting: four lanes per (token, expert) count, over a quarter of
+    // the token's keys each, the keys that beat it (greater, or equal with a
+    // lower index); the quad's total is the expert's position in descending
+    // order.  One pass, no dependent rounds.
+    const int me = a.M * a.E;
+    if (tid < me) {
+      const float f = a.logits_dtype == GI_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[tid])
+                                                      : ((const float*)a.logits)[tid];
+      P.keys[tid] = orderable_key(f);
+    }
+    __syncthreads();
+    const int item = tid >> 2, part = tid & 3;
+    int cnt = 0;
+    uint32_t k = 0;
+    int t = 0, e = 0;
+    if (item < me) {
+      t = item / a.E;
+      e = item - t * a.E;
+      k = P.keys[item];
+      const uint32_t* row = P.keys + t * a.E;
+      for (int j = part; j < a.E; j += 4) {
+        const uint32_t kj = row[j];
+        cnt += (kj > k) | ((kj == k) & (j < e));
+      }
+    }
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+    if (item < me && part == 0 && cnt < a.top_k) {
+      P.slot_e[t * a.top_k + cnt] = e;
+      P.slot_w[t * a.top_k + cnt] = key_value(k);  // logit for now
+    }
+    __syncthreads();
+    if (tid < a.M) {  // softmax over each token's top_k logits (slot 0 holds the maximum)
+      float* wv = P.slot_w + tid * a.top_k;
+      const float vmax = wv[0];
+      float sum = 0.f;
+      for (int r = 0; r < a.top_k; ++r) sum += expf(wv[r] - vmax);
+      for (int r = 0; r < a.top_k; ++r) {
+        float pr = expf(wv[r] - vmax) / sum;
+        if (a.expert_scale) pr *= a.expert_scale[P.slot_e[tid * a.top_k + r]];
+        wv[r] = pr;
+      }
+    }
+    __syncthreads();
+  }
+  if (a.logits && a.M * a.E * 4 > T) {
     for (int t = wave; t < a.M; t += W) {
       // lane r writes slot t*top_k + r directly
       route_token_any(a, t, lane, P.slot_e + t * a.top_k, P.slot_w + t * a.top_k);
     }
     __syncthreads();
+  }
+  if (a.logits) {
     if (tid < S) {
       const float wr = round_to_bf16(P.slot_w[tid]);
       P.slot_w[tid] = wr;
@@ -263,13 +315,17 @@ __device__ void gather_list(const Args& a, Prologue& P, int u) {
 // ---------------------------------------------------------------------------
 // task (u, c)
 // ---------------------------------------------------------------------------
-template <int CG, int NT, int JGM>
+template <int CG, int NT, int JGM, int CPR>
 __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char* smem) {
   constexpr int T = 16 * CG;      // threads
   constexpr int W = T / kWave;    // waves
   constexpr int L = CG / 2;       // lanes per packed row: CG/4 gate quads + CG/4 up quads
   constexpr int HALF = CG / 4;
   constexpr int DR = CG / 8;      // packed rows of the down projection this task meets
+  constexpr int DQM = (CPR * kWave + T - 1) / T;      // output quads per thread in the down step
+  constexpr int XPT = (NT * 32 * JGM + T - 1) / T;    // x words per thread (first chunk)
+  constexpr int SPW = (DR * CPR + W - 1) / W;         // 1 KB slab chunks per wave
+  constexpr int HP = CPR * kWave * 4;                 // LDS slab row stride (uint32)
   const int tid = threadIdx.x, lane = tid & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA base in M0
   const int q = tid % L, rl = tid / L;  // rl in [0, 32): this lane's row within a 32-row step
@@ -283,84 +339,94 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
   uint32_t* slab = (uint32_t*)(smem + a.off_slab);
   uint4* xs = (uint4*)(smem + a.off_xs);
   float* xb = (float*)(smem + a.off_xb);
-  uint2* sct = (uint2*)(smem + a.off_sct);
   float* red = (float*)(smem + a.off_red);
   uint16_t* actp = (uint16_t*)(smem + a.off_actp);
   float* actb = (float*)(smem + a.off_actb);
 
-  // (1) Down-projection rows [c*DR, c*DR+DR) of expert e, all H columns,
-  //     straight into LDS: one wave instruction moves 1 KB (64 lanes x 16 B).
+  gather_list<T>(a, P, u);
+  const int nmatch = P.n_list;
+
+  // Every load below is straight-line with a fixed count per wave (addresses
+  // of unused lanes/rows are clamped, not skipped), so the compiler's vmcnt
+  // waits are exact: staging x waits only for the x words (issued first), and
+  // row j of the gate/up sum waits only for the loads up to row j.
+  // (1) x words of the first token chunk
+  uint4 xr[XPT];
   {
-    const int32_t* dp = a.d_packed + (size_t)e * Ip * a.H;
-    const int cpr = (HQ + kWave - 1) / kWave;  // 1 KB chunks per row
-    for (int ch = wave; ch < DR * cpr; ch += W) {
-      const int r = ch / cpr, cc = ch - r * cpr;
-      const int row = c * DR + r;
-      const int qd = cc * kWave + lane;
-      if (row < Ip && qd < HQ) {
-        __builtin_amdgcn_global_load_lds((gbl_ptr_t)(dp + (size_t)row * a.H + 4 * qd),
-                                         (lds_ptr_t)(slab + r * a.H + 4 * cc * kWave), 16, 0, 0);
-      }
+    const int nch0 = min(NT, nmatch);
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int id = tid + i * T, n = id / Kp, r = id - n * Kp;
+      const bool v = n < nch0;
+      const int tok = P.list[v ? n : 0] / a.top_k;
+      xr[i] = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * (v ? r : 0));
     }
   }
-
-  // (2) gate/up scales of the tile -> LDS as [group][gate quads | up quads].
-  //     Loaded before the weights: the in-order vmcnt wait their LDS stores
-  //     need does not then wait for the weight stream.
-  {
-    const uint16_t* sp = a.gu_scales + (size_t)e * a.Ggu * twoI;
-    for (int i = tid; i < a.Ggu * L; i += T) {
-      const int g = i / L, qq = i - g * L;
-      const int cqq = qq < HALF ? qq : qq - HALF;
-      const int ic = c * CG + cqq * 4;
-      uint2 v = make_uint2(0u, 0u);
-      if (ic < a.I) v = *(const uint2*)(sp + (size_t)g * twoI + (qq < HALF ? 0 : a.I) + ic);
-      sct[i] = v;
-    }
-  }
-
-  // (3) gate/up words of this lane's column quad, every 32nd row: registers.
-  const int32_t* gp = a.gu_packed + (size_t)e * Kp * twoI + (is_up ? a.I : 0) + icol;
+  // (2) gate/up words of this lane's column quad, every 32nd row, and their scales
+  const int icol_c = col_ok ? icol : 0;
+  const int32_t* gp = a.gu_packed + (size_t)e * Kp * twoI + (is_up ? a.I : 0) + icol_c;
+  const uint16_t* gsp = a.gu_scales + (size_t)e * a.Ggu * twoI + (is_up ? a.I : 0) + icol_c;
   uint4 wv[JGM];
+  uint2 sg[JGM];
   bool ok[JGM];
 #pragma unroll
   for (int j = 0; j < JGM; ++j) {
     const int r = 32 * j + rl;
-    ok[j] = col_ok && r < Kp && r / rpg < a.Ggu;
-    wv[j] = ok[j] ? load_nt_u4(gp + (size_t)r * twoI) : make_uint4(0u, 0u, 0u, 0u);
+    const int g = r / rpg;
+    ok[j] = col_ok && r < Kp && g < a.Ggu;
+    wv[j] = load_nt_u4(gp + (size_t)(ok[j] ? r : 0) * twoI);
+    sg[j] = *(const uint2*)(gsp + (size_t)(ok[j] ? g : 0) * twoI);
   }
-
-  // (4) down scales of this thread's output quads (one group per slab when
-  //     gs is a multiple of CG; otherwise looked up per row below).
-  constexpr int DQM = 2;  // output quads per thread (H <= 2*4*T)
+  // (3) down scales of this thread's output quads (one group per slab when
+  //     gs is a multiple of CG; otherwise looked up per row in the down step)
   const int g0 = (c * DR) / rpg, g1 = (c * DR + DR - 1) / rpg;
   const bool one_group = g0 == g1;
   const uint16_t* dsp = a.d_scales + (size_t)e * a.Gd * a.H;
   uint2 sd[DQM];
-  const uint32_t m43 = magic43();
 #pragma unroll
   for (int m = 0; m < DQM; ++m) {
-    const int hq = tid + m * T;
-    sd[m] = (one_group && g0 < a.Gd && hq < HQ) ? *(const uint2*)(dsp + (size_t)g0 * a.H + 4 * hq)
-                                                 : make_uint2(0u, 0u);
+    const int hq = min(tid + m * T, HQ - 1);
+    sd[m] = *(const uint2*)(dsp + (size_t)min(g0, a.Gd - 1) * a.H + 4 * hq);
   }
-
-  gather_list<T>(a, P, u);
-  const int nmatch = P.n_list;
+  // (4) down-projection rows [c*DR, c*DR+DR) of expert e, all H columns,
+  //     straight into LDS (row stride HP): one instruction moves 1 KB.
+  {
+    const int32_t* dp = a.d_packed + (size_t)e * Ip * a.H;
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      const int ch = min(wave + i * W, DR * CPR - 1);
+      const int r = ch / CPR, cc = ch - r * CPR;
+      const int row = min(c * DR + r, Ip - 1);
+      const int qd = min(cc * kWave + lane, HQ - 1);
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)(dp + (size_t)row * a.H + 4 * qd),
+                                       (lds_ptr_t)(slab + r * HP + cc * kWave * 4), 16, 0, 0);
+    }
+  }
+  const uint32_t m43 = magic43();
 
   for (int c0 = 0; c0 < nmatch; c0 += NT) {
     const int nch = min(NT, nmatch - c0);
-    // stage x rows of the chunk's tokens (pair-permuted + bias)
-    for (int i = tid; i < nch * Kp; i += T) {
-      const int n = i / Kp, r = i - n * Kp;
-      const int tok = P.list[c0 + n] / a.top_k;
-      const uint4 d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
-      xs[n * Kp + r] = pair_permute(d);
-      xb[n * Kp + r] = neg_bias_136(d);
+    if (c0 == 0) {
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) {
+        const int id = tid + i * T, n = id / Kp, r = id - n * Kp;
+        if (n < nch) {
+          xs[n * Kp + r] = pair_permute(xr[i]);
+          xb[n * Kp + r] = neg_bias_136(xr[i]);
+        }
+      }
+    } else {
+      for (int i = tid; i < nch * Kp; i += T) {
+        const int n = i / Kp, r = i - n * Kp;
+        const int tok = P.list[c0 + n] / a.top_k;
+        const uint4 d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
+        xs[n * Kp + r] = pair_permute(d);
+        xb[n * Kp + r] = neg_bias_136(d);
+      }
     }
     __syncthreads();
 
-    // gate/up partial sums over this lane's rows
+    // gate/up partial sums over this lane's rows, row by row as words arrive
     float acc[4][NT];
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq)
@@ -368,19 +434,20 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
       for (int n = 0; n < NT; ++n) acc[qq][n] = 0.f;
 #pragma unroll
     for (int j = 0; j < JGM; ++j) {
-      if (!ok[j]) continue;
       const int r = 32 * j + rl;
-      const uint2 s2 = sct[(r / rpg) * L + q];
+      const uint2 s2 = opaque(sg[j]);
       const float s[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
       const uint4 w = opaque(wv[j]);
       const uint32_t wq[4] = {w.x, w.y, w.z, w.w};
+      if (ok[j]) {
 #pragma unroll
-      for (int n = 0; n < NT; ++n) {
-        if (n < nch) {
-          const uint4 xp = xs[n * Kp + r];
-          const float b = xb[n * Kp + r];
+        for (int n = 0; n < NT; ++n) {
+          if (n < nch) {
+            const uint4 xp = xs[n * Kp + r];
+            const float b = xb[n * Kp + r];
 #pragma unroll
-          for (int qq = 0; qq < 4; ++qq) acc[qq][n] += s[qq] * dot8_q4(wq[qq], xp, b, m43);
+            for (int qq = 0; qq < 4; ++qq) acc[qq][n] += s[qq] * dot8_q4(wq[qq], xp, b, m43);
+          }
         }
       }
     }
@@ -432,7 +499,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
         const int row = c * DR + r;
         const int g = row / rpg;
         const bool rok = row < Ip && g < a.Gd;
-        dw[r] = rok ? *(const uint4*)(slab + r * a.H + 4 * hq) : make_uint4(0u, 0u, 0u, 0u);
+        dw[r] = *(const uint4*)(slab + r * HP + 4 * hq);
         uint2 s2 = sd[m];
         if (!one_group) s2 = rok ? *(const uint2*)(dsp + (size_t)g * a.H + 4 * hq) : make_uint2(0u, 0u);
         if (!rok) s2 = make_uint2(0u, 0u);
@@ -524,38 +591,52 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
   }
 }
 
-template <int CG, int NT, int JGM>
+template <int CG, int NT, int JGM, int CPR>
 __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
   constexpr int T = 16 * CG;
   __shared__ Prologue P;
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   const int tid = threadIdx.x;
+  // barrier generation of this launch (read before this workgroup can arrive)
+  const int my_gen = tid == 0 ? load_relaxed(a.ctr) : 0;
   prologue<T>(a, P);
   const int ntask = P.n_unique * a.Tg;
-  for (int t = blockIdx.x; t < ntask; t += gridDim.x) run_task<CG, NT, JGM>(a, P, t / a.Tg, t % a.Tg, smem);
+  for (int t = blockIdx.x; t < ntask; t += gridDim.x)
+    run_task<CG, NT, JGM, CPR>(a, P, t / a.Tg, t % a.Tg, smem);
 
-  // grid-wide barrier: every partial of every task is written
+  // Grid-wide barrier (every partial of every task is written), two-level
+  // and sense-reversing: arrivals are spread over kBarrierSubs counters on
+  // separate cache lines (one counter serialises every atomic); the last
+  // arrival of a sub-counter bumps the top counter; the last of those resets
+  // the counters and advances the generation word that the others poll.
   wait_vmem();
   __syncthreads();
   if (tid == 0) {
-    atomic_add_relaxed(&a.ctr[0], 1);
-    int spins = 0;
-    while (load_relaxed(&a.ctr[0]) < (int)gridDim.x) {
-      if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
-        atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
-        break;
+    const int G = gridDim.x, ns = G < kBarrierSubs ? G : kBarrierSubs, i = blockIdx.x % ns;
+    const int members = G / ns + (i < G % ns);
+    int* gen = a.ctr;
+    int* top = a.ctr + kCtrStride;
+    int* sub = a.ctr + 2 * kCtrStride;
+    bool last = false;
+    if (atomic_add_relaxed(sub + i * kCtrStride, 1) == members - 1)
+      last = atomic_add_relaxed(top, 1) == ns - 1;
+    if (last) {
+      for (int k2 = 0; k2 < ns; ++k2) store_relaxed(sub + k2 * kCtrStride, 0);
+      store_relaxed(top, 0);
+      wait_vmem();
+      store_relaxed(gen, my_gen + 1);
+    } else {
+      int spins = 0;
+      while (load_relaxed(gen) == my_gen) {
+        if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
+          atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+          break;
+        }
       }
-      __builtin_amdgcn_s_sleep(2);
     }
   }
   __syncthreads();
   reduce_partials<T>(a, P, (float4*)(smem + a.off_slab));
-  if (tid == 0) {
-    if (atomic_add_relaxed(&a.ctr[1], 1) == (int)gridDim.x - 1) {
-      store_relaxed(&a.ctr[0], 0);
-      store_relaxed(&a.ctr[1], 0);
-    }
-  }
 }
 
 // Export of the alignment (gi_moe_align): one workgroup of 256 threads.
@@ -620,14 +701,17 @@ struct WsLayout {
   size_t status, ctr, part, total;
 };
 
-int pick_cg(int rows) { return rows <= 1 ? 32 : 32; }
+// Intermediate columns per task.  32 columns (512-thread workgroups) beat 16
+// for a single token as well: half the partial slabs, half the per-task
+// prologue, and 176 tasks at U=8 still cover most of the chip.
+constexpr int kTaskCols = 32;
 int tiles_per_expert(int I, int cg) { return (I + cg - 1) / cg; }
 
 WsLayout ws_layout(int S, int H, int I, int cg) {
   WsLayout L;
   L.status = 0;
-  L.ctr = 64;
-  L.part = kAlign;
+  L.ctr = kAlign;
+  L.part = kAlign + round_up((size_t)(2 + kBarrierSubs) * kCtrStride * sizeof(int));
   L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
   return L;
 }
@@ -636,9 +720,9 @@ struct LdsLayout {
   int slab, xs, xb, sct, red, actp, actb, total;
 };
 
-LdsLayout lds_layout(int cg, int nt, int H, int I, int Ggu) {
+LdsLayout lds_layout(int cg, int nt, int slab_stride, int H, int Ggu) {
   const int T = 16 * cg, W = T / 64, DR = cg / 8, Kp = H / 8;
-  (void)I;
+  (void)Ggu;
   LdsLayout L;
   int off = 0;
   auto take = [&](int bytes) {
@@ -646,11 +730,11 @@ LdsLayout lds_layout(int cg, int nt, int H, int I, int Ggu) {
     off += (bytes + 15) / 16 * 16;
     return o;
   };
-  const int slab = DR * H * 4, scratch = T * 16;
+  const int slab = DR * slab_stride * 4, scratch = T * 16;
   L.slab = take(slab > scratch ? slab : scratch);
   L.xs = take(nt * Kp * 16);
   L.xb = take(nt * Kp * 4);
-  L.sct = take(Ggu * (cg / 2) * 8);
+  L.sct = 0;
   L.red = take(W * nt * 2 * cg * 4);
   L.actp = take(nt * DR * 16);
   L.actb = take(nt * DR * 4);
@@ -691,18 +775,17 @@ int blocks_per_cu(const void* fn, int threads, size_t dyn, int* out) {
   return GI_OK;
 }
 
-template <int CG, int NT, int JGM>
+template <int CG, int NT, int JGM, int CPR>
 int launch_variant(Args k, int umax, hipStream_t stream) {
   constexpr int T = 16 * CG;
-  const LdsLayout L = lds_layout(CG, NT, k.H, k.I, k.Ggu);
+  const LdsLayout L = lds_layout(CG, NT, CPR * 256, k.H, k.Ggu);
   k.off_slab = L.slab;
   k.off_xs = L.xs;
   k.off_xb = L.xb;
-  k.off_sct = L.sct;
   k.off_red = L.red;
   k.off_actp = L.actp;
   k.off_actb = L.actb;
-  const void* fn = (const void*)fused_moe_kernel<CG, NT, JGM>;
+  const void* fn = (const void*)fused_moe_kernel<CG, NT, JGM, CPR>;
   int bpc = 0;
   int st = blocks_per_cu(fn, T, (size_t)L.total, &bpc);
   if (st != GI_OK) return st;
@@ -716,7 +799,7 @@ int launch_variant(Args k, int umax, hipStream_t stream) {
   int qpw = 1;
   while (qpw < per && qpw < T) qpw <<= 1;
   k.qpw = qpw;
-  hipLaunchKernelGGL((fused_moe_kernel<CG, NT, JGM>), dim3(grid), dim3(T), (size_t)L.total,
+  hipLaunchKernelGGL((fused_moe_kernel<CG, NT, JGM, CPR>), dim3(grid), dim3(T), (size_t)L.total,
                      stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
@@ -724,11 +807,11 @@ int launch_variant(Args k, int umax, hipStream_t stream) {
 }
 
 template <int CG, int NT>
-int launch_jgm(const Args& k, int umax, hipStream_t stream) {
-  const int steps = ((k.H >> 3) + 31) / 32;
-  if (steps <= 2) return launch_variant<CG, NT, 2>(k, umax, stream);
-  if (steps <= 11) return launch_variant<CG, NT, 11>(k, umax, stream);
-  return launch_variant<CG, NT, 16>(k, umax, stream);
+int launch_shape(const Args& k, int umax, hipStream_t stream) {
+  // (row steps of 32 packed rows, 1 KB chunks per down row) by hidden size
+  if (k.H <= 512) return launch_variant<CG, NT, 2, 4>(k, umax, stream);
+  if (k.H <= 2816) return launch_variant<CG, NT, 11, 11>(k, umax, stream);
+  return launch_variant<CG, NT, 16, 16>(k, umax, stream);
 }
 
 int check_moe_shapes(const MoeHostArgs& a) {
@@ -766,9 +849,7 @@ size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
   int r = rows < per ? rows : per;
   if (r < 1) r = 1;
   // the largest tile count any launch of this call may use
-  const size_t a = ws_layout(r * top_k, H, I, pick_cg(r)).total;
-  const size_t b = ws_layout(r * top_k, H, I, pick_cg(1)).total;
-  return a > b ? a : b;
+  return ws_layout(r * top_k, H, I, kTaskCols).total;
 }
 
 int launch_fused_moe(const MoeHostArgs& h) {
@@ -811,7 +892,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
   const size_t w_es = h.w_dtype == GI_DTYPE_FP32 ? 4 : 2;
   for (int r0 = 0; r0 < h.M; r0 += rows_per) {
     const int rows = (h.M - r0) < rows_per ? (h.M - r0) : rows_per;
-    const int cg = pick_cg(rows);
+    const int cg = kTaskCols;
     const WsLayout L = ws_layout(rows * h.top_k, h.H, h.I, cg);
     k.status = (int*)(ws + L.status);
     k.ctr = (int*)(ws + L.ctr);
@@ -825,7 +906,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
     k.w = h.w ? (const char*)h.w + (size_t)r0 * h.top_k * w_es : nullptr;
     if (h.logits) k.logits = (const char*)h.logits + (size_t)r0 * h.E * (h.logits_dtype == GI_DTYPE_FP32 ? 4 : 2);
     const int umax = k.S < h.E ? k.S : h.E;
-    st = rows == 1 ? launch_jgm<32, 1>(k, umax, h.stream) : launch_jgm<32, 4>(k, umax, h.stream);
+    st = rows == 1 ? launch_shape<kTaskCols, 1>(k, umax, h.stream) : launch_shape<kTaskCols, 4>(k, umax, h.stream);
     if (st != GI_OK) return st;
   }
   return GI_OK;
