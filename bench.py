@@ -217,6 +217,173 @@ def bench_config(m, noise, seed, copies, steps, warmup, device):
     }
 
 
+CALIB_BYTES = 256 << 20
+
+# Dense W4A16 workloads (BASELINE configs 0 and 4): (M, K, N, group, softcap, copies)
+LINEAR_WORKLOADS = {
+    "linear": (1, 2816, 2816, 128, 0.0, 300),        # configs[0] shape, 4.09 MB per weight copy
+    "lm_head": (6, 2816, 262144, 128, 30.0, 4),      # configs[4], 380.6 MB per copy
+}
+
+
+def linear_bytes(k, n, gs):
+    return (k // 8) * n * 4 + math.ceil(k / gs) * n * 2
+
+
+class LinearRunner:
+    """Direct C-ABI launches of gi_w4a16_linear over rotated weight copies."""
+
+    def __init__(self, m, k, n, gs, softcap, copies, device):
+        self.lib = L.load()
+        self.m, self.k, self.n, self.gs, self.softcap = m, k, n, gs, softcap
+        g = torch.Generator(device=device)
+        g.manual_seed(0)
+        self.B, self.S = [], []
+        for _ in range(copies):
+            self.B.append(torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), generator=g, device=device,
+                                        dtype=torch.int64).to(torch.int32))
+            self.S.append((torch.randn((math.ceil(k / gs), n), generator=g, device=device).abs() * 0.02)
+                          .to(torch.bfloat16))
+        self.A = synth.activations(m, k, seed=0).to(device)
+        self.C = torch.empty(m, n, dtype=torch.bfloat16, device=device)
+        nbytes = self.lib.gi_w4a16_workspace_bytes(m, k, n, gs)
+        self.ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+        self.dev = device
+        torch.cuda.synchronize()
+
+    def launch(self, i):
+        c = i % len(self.B)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        st = self.lib.gi_w4a16_linear(p(self.A), L.DTYPE_BF16, p(self.B[c]), p(self.S[c]), self.S[c].shape[0],
+                                      p(self.C), self.m, self.k, self.n, self.gs, self.softcap,
+                                      p(self.ws), self.ws.numel(), stream)
+        L.check(st, "gi_w4a16_linear")
+
+
+def cpu_baseline_linear(name, budget_s):
+    """The reference's PyTorch CPU dequant+matmul (quant.py:67-75; + softcap for
+    lm_head, gemma.py:351-357) on a bounded sample: the full configs[0]
+    weight, or for lm_head a 16384-column slice of the vocabulary."""
+    from oracle import cpu_baseline as CB
+
+    m, k, n, gs, softcap, _ = LINEAR_WORKLOADS[name]
+    n_s = n if n <= 16384 else 16384
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    B, S = synth.linear_weights(k, n_s, gs, seed=0)
+    A = synth.activations(m, k, seed=0)
+    run = (lambda: CB.lm_head_softcap(A, B, S, gs, softcap)) if softcap else \
+        (lambda: CB.dequant_matmul(A, B, S, gs, n_s))
+    run()
+    times, t_start = [], time.perf_counter()
+    while time.perf_counter() - t_start < budget_s:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": linear_bytes(k, n_s, gs) / t / 1e9, "unit": "GB/s", "us_per_launch_sample": t * 1e6,
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{len(times)} timed reps (median) of M={m}, K={k}, N={n_s} through "
+                      f"oracle/cpu_baseline ({'lm_head_softcap' if softcap else 'dequant_matmul'}), "
+                      f"restating quant.py:67-75; torch {torch.__version__}"}
+
+
+def bench_linear(name, steps, warmup, device, cpu_budget_s=None):
+    m, k, n, gs, softcap, copies = LINEAR_WORKLOADS[name]
+    runner = LinearRunner(m, k, n, gs, softcap, copies, device)
+    for i in range(warmup):
+        runner.launch(i)
+    torch.cuda.synchronize()
+    order = [warmup + i for i in range(steps)]
+    us = time_graph(runner, order, device)
+    hot_us = time_graph(runner, [order[0]] * min(steps, 200), device)
+    nbytes = linear_bytes(k, n, gs)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {
+        "metric": f"W4A16 linear us + achieved HBM GB/s ({name}: M={m}, K={k}, N={n}, gs={gs}"
+                  + (f", softcap {softcap:g}" if softcap else "") + ", 1 GPU)",
+        "value": gbps, "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": us / 1000.0, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (uniform int4 words, |N(0,1)|*0.02 bf16 scales, N(0,1) bf16 activations)",
+        "config": {"workload": f"{name}: gi_w4a16_linear, one launch per step", "M": m, "K": k, "N": n,
+                   "group_size": gs, "softcap": softcap, "weight_copies_rotated": copies,
+                   "timing": "HIP graph of K steps, HIP events"},
+        "us_per_launch": us, "hot_cache_us_per_launch": hot_us,
+        "algorithmic_bytes_per_launch": nbytes,
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / PEAK_GBPS, "traffic": None},
+        "cpu_baseline": cpu_baseline_linear(name, cpu_budget_s) if cpu_budget_s else None,
+    }
+
+
+def pmc_pass(copies, steps, warmup, device):
+    """Eager launches for one rocprofv3 --pmc pass (FETCH_SIZE or WRITE_SIZE).
+
+    First three float32 negations of a 256 MiB buffer (a plain streaming
+    kernel that reads and writes exactly CALIB_BYTES each: the calibration
+    for the counter), then W warmup + K rotated M=1 layers launched one by
+    one.  The profiler serialises dispatches; the rotation keeps >= 1 GB of
+    other weights between reuses, as in the timed run.  Per-dispatch HBM
+    bytes of the layer kernel = mean counter over the K layers after warmup,
+    scaled by CALIB_BYTES / (mean counter of the calibration kernel).
+    """
+    src = torch.randn(CALIB_BYTES // 4, device=device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    desc = make_steps(1, 0.0, 1, warmup + steps)
+    runner = LayerRunner(1, desc, copies, device)
+    for i in range(warmup + steps):
+        runner.launch(i)
+    torch.cuda.synchronize()
+    if runner.status() != 0:
+        raise RuntimeError("device status word set during the pmc pass")
+    mean_u = statistics.fmean(desc[i]["U"] for i in range(warmup, warmup + steps))
+    print(json.dumps({"pmc_pass": {"calibration_kernel": "neg float32", "calibration_bytes_read": CALIB_BYTES,
+                                   "calibration_bytes_written": CALIB_BYTES, "calibration_dispatches": 3,
+                                   "layer_dispatches": warmup + steps, "warmup": warmup,
+                                   "algorithmic_bytes_per_layer": mean_u * expert_bytes()}}))
+
+
+def pmc_reduce(fetch_csv, write_csv, out_path):
+    """Per-dispatch HBM bytes of the M=1 layer kernel from the counter CSVs of
+    two --pmc-pass runs (FETCH_SIZE, then WRITE_SIZE; values in KiB per
+    dispatch).  Each counter is scaled by CALIB_BYTES / its reading on the
+    calibration kernel, which reads and writes exactly CALIB_BYTES."""
+    import csv
+    import collections
+
+    def per_dispatch(path):
+        vals, names = collections.defaultdict(float), {}
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                d = int(r["Dispatch_Id"])
+                vals[d] += float(r["Counter_Value"])
+                names[d] = r["Kernel_Name"]
+        ids = sorted(vals)
+        cal = [vals[d] for d in ids if "neg" in names[d].lower()][-3:]
+        lay = [vals[d] for d in ids if "fused_moe_kernel" in names[d]]
+        if len(cal) != 3 or not lay:
+            raise SystemExit(f"{path}: expected 3 calibration and >= 1 layer dispatches")
+        return cal, lay
+
+    res = {}
+    for key, path in (("fetch", fetch_csv), ("write", write_csv)):
+        cal, lay = per_dispatch(path)
+        lay = lay[10:] if len(lay) > 10 else lay  # the pass's 10 warmup layers
+        factor = (CALIB_BYTES / 1024.0) / statistics.fmean(cal)
+        res[key] = {"counter_kib_mean": statistics.fmean(lay), "calibration_kib": cal,
+                    "calibration_factor": factor, "bytes_per_dispatch": statistics.fmean(lay) * 1024.0 * factor,
+                    "dispatches": len(lay)}
+    res["hbm_bytes_per_launch"] = res["fetch"]["bytes_per_dispatch"] + res["write"]["bytes_per_dispatch"]
+    res["algorithmic_bytes_per_launch"] = 8 * expert_bytes()
+    Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
+    print(json.dumps(res))
+
+
 def cpu_baseline(budget_s, max_reps):
     """The reference's PyTorch CPU path on the same workload (M=1 layer),
     bounded to about budget_s seconds of CPU work."""
@@ -263,7 +430,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--workload", choices=["moe", *LINEAR_WORKLOADS], default="moe",
+                    help="moe (default: the BASELINE metric, M=1 value with M=7 beside it) or a dense "
+                         "W4A16 shape (linear = configs[0], lm_head = configs[4])")
+    ap.add_argument("--pmc-reduce", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
+                    help="reduce two --pmc-pass counter CSVs to per-launch HBM bytes (no GPU needed)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="eager calibration copy + rotated M=1 layers for a rocprofv3 --pmc run; no timing")
     args = ap.parse_args()
+    if args.pmc_reduce:
+        pmc_reduce(*args.pmc_reduce)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X "
               f"(--gpus {args.gpus} is not supported; the sharding design is in DESIGN.md)",
@@ -274,16 +451,23 @@ def main():
         sys.exit(2)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.workload != "moe":
+        print(json.dumps(bench_linear(args.workload, args.steps, args.warmup, device,
+                                      None if args.no_cpu_baseline else args.cpu_budget_s)))
+        return
     copies = [synth.device_moe_weights(E, H, I, GS, device, seed=100 + c) for c in range(COPIES)]
     torch.cuda.synchronize()
     print(f"[bench] weights ready: {COPIES} x {E} experts", file=sys.stderr, flush=True)
+    if args.pmc_pass:
+        pmc_pass(copies, args.steps, args.warmup, device)
+        return
     m1 = bench_config(1, 0.0, 1, copies, args.steps, args.warmup, device)
     print(f"[bench] M=1 {m1['us_per_layer']:.2f} us {m1['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
     m7 = bench_config(7, 0.5, 2, copies, args.steps, args.warmup, device)
     print(f"[bench] M=7 {m7['us_per_layer']:.2f} us {m7['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(args.cpu_budget_s, 30)
+        cpu = cpu_baseline(args.cpu_budget_s, 100000)
         print(f"[bench] cpu {cpu['us_per_layer']:.0f} us", file=sys.stderr, flush=True)
     traffic = None
     tfile = ROOT / "profiles" / "traffic_moe_layer_m1.json"

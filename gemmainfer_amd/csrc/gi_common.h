@@ -108,6 +108,24 @@ __device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias, uint3
   return d;
 }
 
+// The same product split in two, so that one unpacked word serves several
+// activation rows: unpack_q4 gives the four bf16 pairs (128+q) of dot8_q4,
+// dot_unpacked takes them with one row's pair-permuted x and bias.
+struct Q4Pairs {
+  uint32_t p0, p1, p2, p3;  // (q0,q4) (q2,q6) (q1,q5) (q3,q7)
+};
+__device__ __forceinline__ Q4Pairs unpack_q4(uint32_t w, uint32_t m43) {
+  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+  return Q4Pairs{__builtin_amdgcn_perm(m43, lo, 0x04020400u), __builtin_amdgcn_perm(m43, lo, 0x04030401u),
+                 __builtin_amdgcn_perm(m43, hi, 0x04020400u), __builtin_amdgcn_perm(m43, hi, 0x04030401u)};
+}
+__device__ __forceinline__ float dot_unpacked(const Q4Pairs& d, uint4 xp, float bias) {
+  float r = fdot2(xp.x, d.p0, bias);
+  r = fdot2(xp.z, d.p1, r);
+  r = fdot2(xp.y, d.p2, r);
+  return fdot2(xp.w, d.p3, r);
+}
+
 // 0x43434343 held in a VGPR (v_perm_b32 may read only one scalar operand).
 __device__ __forceinline__ uint32_t magic43() {
   uint32_t v = 0x43434343u;
@@ -163,6 +181,27 @@ __device__ __forceinline__ uint4 ld_coherent_u4(const void* p) {
   const unsigned long long lo = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const unsigned long long hi = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return make_uint4((uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32));
+}
+// 16-byte forms of the same accesses, through a buffer resource: the cache
+// policy argument 16 is the sc1 bit (what the compiler emits for the 4- and
+// 8-byte atomics above).  One instruction covers whole cache lines, so a
+// wave's 1 KB of partials leaves the L2 as 8 full lines instead of 4 partial
+// writes per line.  Offsets past `bytes` read 0 and drop stores.
+constexpr int kCpolAgent = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void st_coherent_f4(__amdgpu_buffer_rsrc_t r, uint32_t off, float4 v) {
+  u32x4_t w;
+  w.x = __float_as_uint(v.x);
+  w.y = __float_as_uint(v.y);
+  w.z = __float_as_uint(v.z);
+  w.w = __float_as_uint(v.w);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, kCpolAgent);
+}
+__device__ __forceinline__ float4 ld_coherent_f4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t w = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolAgent);
+  return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
 }
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }

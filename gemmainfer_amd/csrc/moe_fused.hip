@@ -48,7 +48,6 @@ namespace {
 constexpr int kMaxSlots = 256;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxWaves = 16;
-constexpr int kRankMax = 256;  // M*E of the rank-counting router (4 lanes per key)
 constexpr int kDefaultSpin = 1 << 22;
 constexpr int kBarrierSubs = 8;    // first-level arrival counters of the grid barrier
 constexpr int kCtrStride = 32;     // ints between counters (128 bytes: separate lines)
@@ -70,14 +69,24 @@ struct Args {
   uint16_t* out_w;
   uint16_t* out;
   float* part;      // [S][Tg][H] fp32 partials
+  uint32_t part_bytes;
   int* ctr;         // grid barrier: [0] generation, [kCtrStride] top, [2*kCtrStride + i*kCtrStride] sub i
   int* status;
   int idx_is64, w_dtype, logits_dtype;
   int M, H, I, E, top_k, gs, Ggu, Gd, S, Tg;
   int overwrite, spin_limit;
   int qpw;          // reduction: output quads per workgroup pass (power of two)
-  // dynamic LDS layout (bytes)
-  int off_slab, off_xs, off_xb, off_red, off_actp, off_actb;
+};
+
+// LDS of one task (static __shared__ arrays declared by the kernel).
+template <int CG, int NT, int JGM, int CPR>
+struct TaskLds {
+  static constexpr int T = 16 * CG, W = T / 64, DR = CG / 8, KPM = 32 * JGM;
+  uint4* xs;        // [NT][KPM] pair-permuted x words
+  float* xb;        // [NT][KPM] -136 * sum of each x word
+  float* red;       // [W][NT][2*CG] per-wave gate/up sums
+  uint16_t* actp;   // [NT][DR][8] pair-permuted bf16 activations
+  float* actb;      // [NT][DR] -136 * sum of each activation row
 };
 
 struct Prologue {
@@ -87,9 +96,10 @@ struct Prologue {
   float slot_w[kMaxSlots];    // routing weight (bf16-rounded)
   int rank_of_slot[kMaxSlots];
   int uexp[kMaxSlots];        // expert id of each unique index
-  int list[kMaxSlots];        // slots of the current task's expert, ascending
+  int list[kMaxSlots];        // slots of the current task's expert, ascending (S > 64)
+  int uoff[kMaxSlots + 1];    // S <= 64: slots of unique u are csr[uoff[u] .. uoff[u+1])
+  int csr[kMaxSlots];
   int wave_cnt[kMaxWaves];
-  uint32_t keys[kRankMax];    // routing keys, rank path (M*E*4 <= threads)
   int n_unique;
   int n_list;
 };
@@ -184,80 +194,71 @@ __device__ __forceinline__ void route_token_any(const Args& a, int t, int lane, 
   else route_token<kMaxExperts / kWave>(a, t, lane, idx_out, w_out);
 }
 
-// Routing (layer mode) or id/weight load, then the Token-Union alignment:
-// the first-occurrence rank of every distinct valid id in slot order
-// (marlin.cu:298-319) and each slot's unique index.  All T threads.
+// Token-Union alignment of up to 64 slots by one wave, without LDS atomics
+// or barriers: lane s holds slot s's expert id; each round takes the lowest
+// remaining slot, retires every slot routed to the same expert, and so
+// enumerates the distinct ids in first-occurrence order (marlin.cu:298-319).
+// Also writes the per-expert slot lists (CSR, slots ascending).
+__device__ __forceinline__ void align_wave(const Args& a, Prologue& P, int lane) {
+  const int e = lane < a.S ? P.slot_e[lane] : -1;
+  unsigned long long rem = __ballot(e >= 0);
+  int u = 0, run = 0, my_u = -1, my_pos = 0;
+  while (rem) {
+    const int s0 = __builtin_ctzll(rem);
+    const int e0 = __builtin_amdgcn_readlane(e, s0);
+    const unsigned long long m = __ballot(e == e0) & rem;
+    if ((m >> lane) & 1ull) {
+      my_u = u;
+      my_pos = run + __popcll(m & ((1ull << lane) - 1ull));
+    }
+    if (lane == 0) {
+      P.uexp[u] = e0;
+      P.uoff[u] = run;
+    }
+    run += __popcll(m);
+    rem &= ~m;
+    ++u;
+  }
+  if (lane < a.S) {
+    P.slot_u[lane] = my_u;
+    if (my_u >= 0) P.csr[my_pos] = lane;
+  }
+  if (lane == 0) {
+    P.uoff[u] = run;
+    P.n_unique = u;
+  }
+}
+
+// Routing (layer mode: one wave per token, gemma.py:77-80) or id/weight load,
+// then the Token-Union alignment: the distinct valid ids in first-occurrence
+// slot order (marlin.cu:298-319) and each slot's unique index.  All T threads.
 template <int T>
 __device__ void prologue(const Args& a, Prologue& P) {
   constexpr int W = T / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int S = a.S;
-  if (a.logits && a.M * a.E * 4 <= T) {
-    // Rank counting: four lanes per (token, expert) count, over a quarter of
-    // the token's keys each, the keys that beat it (greater, or equal with a
-    // lower index); the quad's total is the expert's position in descending
-    // order.  One pass, no dependent rounds.
-    const int me = a.M * a.E;
-    if (tid < me) {
-      const float f = a.logits_dtype == GI_DTYPE_BF16 ? bf16_to_f32(((const uint16_t*)a.logits)[tid])
-                                                      : ((const float*)a.logits)[tid];
-      P.keys[tid] = orderable_key(f);
-    }
-    __syncthreads();
-    const int item = tid >> 2, part = tid & 3;
-    int cnt = 0;
-    uint32_t k = 0;
-    int t = 0, e = 0;
-    if (item < me) {
-      t = item / a.E;
-      e = item - t * a.E;
-      k = P.keys[item];
-      const uint32_t* row = P.keys + t * a.E;
-      for (int j = part; j < a.E; j += 4) {
-        const uint32_t kj = row[j];
-        cnt += (kj > k) | ((kj == k) & (j < e));
-      }
-    }
-    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-    cnt += __builtin_amdgcn_update_dpp(0, cnt, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-    if (item < me && part == 0 && cnt < a.top_k) {
-      P.slot_e[t * a.top_k + cnt] = e;
-      P.slot_w[t * a.top_k + cnt] = key_value(k);  // logit for now
-    }
-    __syncthreads();
-    if (tid < a.M) {  // softmax over each token's top_k logits (slot 0 holds the maximum)
-      float* wv = P.slot_w + tid * a.top_k;
-      const float vmax = wv[0];
-      float sum = 0.f;
-      for (int r = 0; r < a.top_k; ++r) sum += expf(wv[r] - vmax);
-      for (int r = 0; r < a.top_k; ++r) {
-        float pr = expf(wv[r] - vmax) / sum;
-        if (a.expert_scale) pr *= a.expert_scale[P.slot_e[tid * a.top_k + r]];
-        wv[r] = pr;
-      }
-    }
-    __syncthreads();
-  }
-  if (a.logits && a.M * a.E * 4 > T) {
-    for (int t = wave; t < a.M; t += W) {
-      // lane r writes slot t*top_k + r directly
-      route_token_any(a, t, lane, P.slot_e + t * a.top_k, P.slot_w + t * a.top_k);
-    }
-    __syncthreads();
-  }
   if (a.logits) {
-    if (tid < S) {
-      const float wr = round_to_bf16(P.slot_w[tid]);
-      P.slot_w[tid] = wr;
-      if (blockIdx.x == 0) {
-        if (a.out_idx) a.out_idx[tid] = P.slot_e[tid];
-        if (a.out_w) a.out_w[tid] = f32_to_bf16(wr);
-      }
-    }
+    for (int t = wave; t < a.M; t += W)
+      route_token_any(a, t, lane, P.slot_e + t * a.top_k, P.slot_w + t * a.top_k);
   } else if (tid < S) {
     const int e = load_expert_id(a.idx, a.idx_is64, tid);
     P.slot_e[tid] = (e >= 0 && e < a.E) ? e : -1;
     P.slot_w[tid] = a.w ? load_weight_as_bf16(a.w, a.w_dtype, tid) : 0.f;
+  }
+  // A single routed token lives in wave 0, which can go on without a barrier.
+  if (!(a.logits && a.M == 1)) __syncthreads();
+  if (a.logits && tid < S) {
+    const float wr = round_to_bf16(P.slot_w[tid]);
+    P.slot_w[tid] = wr;
+    if (blockIdx.x == 0) {
+      if (a.out_idx) a.out_idx[tid] = P.slot_e[tid];
+      if (a.out_w) a.out_w[tid] = f32_to_bf16(wr);
+    }
+  }
+  if (S <= kWave) {
+    if (wave == 0) align_wave(a, P, lane);
+    __syncthreads();
+    return;
   }
   for (int i = tid; i < a.E; i += T) P.first_slot[i] = INT_MAX;
   __syncthreads();
@@ -315,19 +316,40 @@ __device__ void gather_list(const Args& a, Prologue& P, int u) {
 // ---------------------------------------------------------------------------
 // task (u, c)
 // ---------------------------------------------------------------------------
+template <int N>
+struct Count {
+  static constexpr int value = N;
+};
+// f(Count<n>{}) for the runtime n in [1, NMAX]: one straight-line body per n.
+template <int NMAX, typename F>
+__device__ __forceinline__ void with_count(int n, F&& f) {
+  if constexpr (NMAX > 1) {
+    if (n >= NMAX) {
+      f(Count<NMAX>{});
+      return;
+    }
+    with_count<NMAX - 1>(n, f);
+  } else {
+    f(Count<1>{});
+  }
+}
 template <int CG, int NT, int JGM, int CPR>
-__device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char* smem) {
+__device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds<CG, NT, JGM, CPR>& S) {
   constexpr int T = 16 * CG;      // threads
   constexpr int W = T / kWave;    // waves
   constexpr int L = CG / 2;       // lanes per packed row: CG/4 gate quads + CG/4 up quads
   constexpr int HALF = CG / 4;
   constexpr int DR = CG / 8;      // packed rows of the down projection this task meets
-  constexpr int DQM = (CPR * kWave + T - 1) / T;      // output quads per thread in the down step
-  constexpr int XPT = (NT * 32 * JGM + T - 1) / T;    // x words per thread (first chunk)
-  constexpr int SPW = (DR * CPR + W - 1) / W;         // 1 KB slab chunks per wave
-  constexpr int HP = CPR * kWave * 4;                 // LDS slab row stride (uint32)
-  const int tid = threadIdx.x, lane = tid & (kWave - 1);
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS-DMA base in M0
+  constexpr int KPM = 32 * JGM;   // packed rows of x staged (>= H/8)
+  constexpr int DQM = (CPR * kWave + T - 1) / T;  // output quads per thread in the down step
+  constexpr int XPT = (NT * KPM + T - 1) / T;     // staged x words per thread (first chunk)
+  // The per-lane offsets below are recomputed per task (a few integer ops)
+  // rather than hoisted out of the task loop, where they would sit in
+  // registers through the whole kernel.
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & (kWave - 1);
+  const int wave = tid >> 6;
   const int q = tid % L, rl = tid / L;  // rl in [0, 32): this lane's row within a 32-row step
   const bool is_up = q >= HALF;
   const int cq = is_up ? q - HALF : q;
@@ -335,138 +357,162 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
   const bool col_ok = icol < a.I;
   const int e = P.uexp[u];
   const int Kp = a.H >> 3, Ip = a.I >> 3, twoI = 2 * a.I, rpg = a.gs >> 3, HQ = a.H >> 2;
+  // Rows without a scale group are dropped (the reference sizes its loops by
+  // the scale tensor, marlin.cu:128): x is staged as zero from row Kv on, and
+  // activations from column Iv on, so no per-row mask is needed below.
+  const int Kv = min(Kp, a.Ggu * rpg), Iv = min(a.I, a.Gd * a.gs);
 
-  uint32_t* slab = (uint32_t*)(smem + a.off_slab);
-  uint4* xs = (uint4*)(smem + a.off_xs);
-  float* xb = (float*)(smem + a.off_xb);
-  float* red = (float*)(smem + a.off_red);
-  uint16_t* actp = (uint16_t*)(smem + a.off_actp);
-  float* actb = (float*)(smem + a.off_actb);
+  uint4* xs = S.xs;
+  float* xb = S.xb;
+  float* red = S.red;
+  uint16_t* actp = S.actp;
+  float* actb = S.actb;
+  const __amdgpu_buffer_rsrc_t part = buffer_rsrc(a.part, a.part_bytes);
 
-  gather_list<T>(a, P, u);
-  const int nmatch = P.n_list;
+  // slots routed to expert u, ascending
+  const int* list;
+  int nmatch;
+  if (a.S <= kWave) {
+    list = P.csr + P.uoff[u];
+    nmatch = P.uoff[u + 1] - P.uoff[u];
+  } else {
+    gather_list<T>(a, P, u);
+    list = P.list;
+    nmatch = P.n_list;
+  }
 
-  // Every load below is straight-line with a fixed count per wave (addresses
-  // of unused lanes/rows are clamped, not skipped), so the compiler's vmcnt
-  // waits are exact: staging x waits only for the x words (issued first), and
-  // row j of the gate/up sum waits only for the loads up to row j.
+  // Every load below is a plain register load, straight-line with a fixed
+  // count per thread (addresses of unused lanes/rows are clamped, not
+  // skipped), so the compiler's vmcnt waits are exact: staging x waits only
+  // for the x words (issued first), row j of the gate/up sum only for the
+  // loads up to row j, and the down step finds its words already in flight.
+  // (Direct-to-LDS loads or stores pending here would turn every such wait
+  // into a full drain: the wait-count pass treats mixed events as unordered.)
   // (1) x words of the first token chunk
   uint4 xr[XPT];
   {
     const int nch0 = min(NT, nmatch);
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
-      const int id = tid + i * T, n = id / Kp, r = id - n * Kp;
-      const bool v = n < nch0;
-      const int tok = P.list[v ? n : 0] / a.top_k;
+      const int id = tid + i * T, n = id / KPM, r = id - n * KPM;
+      const bool v = n < nch0 && r < Kv;
+      const int tok = list[v ? n : 0] / a.top_k;
       xr[i] = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * (v ? r : 0));
     }
   }
-  // (2) gate/up words of this lane's column quad, every 32nd row, and their scales
   const int icol_c = col_ok ? icol : 0;
   const int32_t* gp = a.gu_packed + (size_t)e * Kp * twoI + (is_up ? a.I : 0) + icol_c;
   const uint16_t* gsp = a.gu_scales + (size_t)e * a.Ggu * twoI + (is_up ? a.I : 0) + icol_c;
-  uint4 wv[JGM];
-  uint2 sg[JGM];
-  bool ok[JGM];
-#pragma unroll
-  for (int j = 0; j < JGM; ++j) {
-    const int r = 32 * j + rl;
-    const int g = r / rpg;
-    ok[j] = col_ok && r < Kp && g < a.Ggu;
-    wv[j] = load_nt_u4(gp + (size_t)(ok[j] ? r : 0) * twoI);
-    sg[j] = *(const uint2*)(gsp + (size_t)(ok[j] ? g : 0) * twoI);
-  }
-  // (3) down scales of this thread's output quads (one group per slab when
-  //     gs is a multiple of CG; otherwise looked up per row in the down step)
   const int g0 = (c * DR) / rpg, g1 = (c * DR + DR - 1) / rpg;
   const bool one_group = g0 == g1;
   const uint16_t* dsp = a.d_scales + (size_t)e * a.Gd * a.H;
+  const int32_t* dp = a.d_packed + (size_t)e * Ip * a.H;
+  uint4 wv[JGM];
+  uint2 sg[JGM];
   uint2 sd[DQM];
+  uint4 dw[DQM][DR];
+  auto load_weights = [&]() {
+    __builtin_amdgcn_sched_barrier(0);  // keep the issue order: x, gate/up, down scales, down words
+    // (2) gate/up words of this lane's column quad, every 32nd row, and their scales
 #pragma unroll
-  for (int m = 0; m < DQM; ++m) {
-    const int hq = min(tid + m * T, HQ - 1);
-    sd[m] = *(const uint2*)(dsp + (size_t)min(g0, a.Gd - 1) * a.H + 4 * hq);
-  }
-  // (4) down-projection rows [c*DR, c*DR+DR) of expert e, all H columns,
-  //     straight into LDS (row stride HP): one instruction moves 1 KB.
-  {
-    const int32_t* dp = a.d_packed + (size_t)e * Ip * a.H;
-#pragma unroll
-    for (int i = 0; i < SPW; ++i) {
-      const int ch = min(wave + i * W, DR * CPR - 1);
-      const int r = ch / CPR, cc = ch - r * CPR;
-      const int row = min(c * DR + r, Ip - 1);
-      const int qd = min(cc * kWave + lane, HQ - 1);
-      __builtin_amdgcn_global_load_lds((gbl_ptr_t)(dp + (size_t)row * a.H + 4 * qd),
-                                       (lds_ptr_t)(slab + r * HP + cc * kWave * 4), 16, 0, 0);
+    for (int j = 0; j < JGM; ++j) {
+      const int r = min(32 * j + rl, Kv - 1);
+      wv[j] = load_nt_u4(gp + r * twoI);
+      sg[j] = *(const uint2*)(gsp + (r / rpg) * twoI);
     }
-  }
+    __builtin_amdgcn_sched_barrier(0);
+    // (3) down scales of this thread's output quads (one group per task when
+    //     gs is a multiple of CG; otherwise looked up per row in the down step)
+#pragma unroll
+    for (int m = 0; m < DQM; ++m) {
+      const int hq = min(tid + m * T, HQ - 1);
+      sd[m] = *(const uint2*)(dsp + min(g0, a.Gd - 1) * a.H + 4 * hq);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // (4) the packed down rows [c*DR, c*DR+DR) of expert e at this thread's
+    //     output quads: the CG/8 rows the task's activations meet.
+#pragma unroll
+    for (int m = 0; m < DQM; ++m) {
+      const int hq = min(tid + m * T, HQ - 1);
+#pragma unroll
+      for (int r = 0; r < DR; ++r) dw[m][r] = load_nt_u4(dp + min(c * DR + r, Ip - 1) * a.H + 4 * hq);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_weights();
   const uint32_t m43 = magic43();
 
-  for (int c0 = 0; c0 < nmatch; c0 += NT) {
-    const int nch = min(NT, nmatch - c0);
-    if (c0 == 0) {
+  // One chunk of NC (1..NT) of the expert's slots, straight-line for each NC.
+  // The first chunk is peeled out of the loop below, so that its waits stay
+  // exact.
+  auto chunk = [&](auto nc_tag, int c0, bool first) {
+    constexpr int NC = decltype(nc_tag)::value;
+    const int nch = NC;
+    if (first) {
 #pragma unroll
       for (int i = 0; i < XPT; ++i) {
-        const int id = tid + i * T, n = id / Kp, r = id - n * Kp;
-        if (n < nch) {
-          xs[n * Kp + r] = pair_permute(xr[i]);
-          xb[n * Kp + r] = neg_bias_136(xr[i]);
+        const int id = tid + i * T, n = id / KPM, r = id - n * KPM;
+        if (n < NT) {
+          const bool v = n < nch && r < Kv;
+          const uint4 d = v ? xr[i] : make_uint4(0u, 0u, 0u, 0u);
+          xs[n * KPM + r] = pair_permute(d);
+          xb[n * KPM + r] = neg_bias_136(d);
         }
       }
     } else {
-      for (int i = tid; i < nch * Kp; i += T) {
-        const int n = i / Kp, r = i - n * Kp;
-        const int tok = P.list[c0 + n] / a.top_k;
-        const uint4 d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
-        xs[n * Kp + r] = pair_permute(d);
-        xb[n * Kp + r] = neg_bias_136(d);
+      for (int i = tid; i < NT * KPM; i += T) {
+        const int n = i / KPM, r = i - n * KPM;
+        uint4 d = make_uint4(0u, 0u, 0u, 0u);
+        if (n < nch && r < Kv) {
+          const int tok = list[c0 + n] / a.top_k;
+          d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
+        }
+        xs[n * KPM + r] = pair_permute(d);
+        xb[n * KPM + r] = neg_bias_136(d);
       }
     }
     __syncthreads();
 
-    // gate/up partial sums over this lane's rows, row by row as words arrive
-    float acc[4][NT];
+    // gate/up partial sums over this lane's rows, row by row as words arrive;
+    // each word is unpacked once for every token of the chunk
+    float acc[4][NC];
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq)
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[qq][n] = 0.f;
+      for (int n = 0; n < NC; ++n) acc[qq][n] = 0.f;
 #pragma unroll
     for (int j = 0; j < JGM; ++j) {
       const int r = 32 * j + rl;
       const uint2 s2 = opaque(sg[j]);
-      const float s[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
       const uint4 w = opaque(wv[j]);
-      const uint32_t wq[4] = {w.x, w.y, w.z, w.w};
-      if (ok[j]) {
+      const Q4Pairs d[4] = {unpack_q4(w.x, m43), unpack_q4(w.y, m43), unpack_q4(w.z, m43),
+                            unpack_q4(w.w, m43)};
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-          if (n < nch) {
-            const uint4 xp = xs[n * Kp + r];
-            const float b = xb[n * Kp + r];
+      for (int n = 0; n < NC; ++n) {
+        const uint4 xp = xs[n * KPM + r];
+        const float b = xb[n * KPM + r];
 #pragma unroll
-            for (int qq = 0; qq < 4; ++qq) acc[qq][n] += s[qq] * dot8_q4(wq[qq], xp, b, m43);
-          }
-        }
+        for (int qq = 0; qq < 4; ++qq) acc[qq][n] += sc[qq] * dot_unpacked(d[qq], xp, b);
       }
     }
     // lanes of one wave that share q hold different rows: reduce, then waves via LDS
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq)
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[qq][n] = reduce_across_groups<L>(acc[qq][n]);
+      for (int n = 0; n < NC; ++n) acc[qq][n] = reduce_across_groups<L>(acc[qq][n]);
     if (lane < L) {
 #pragma unroll
-      for (int n = 0; n < NT; ++n)
+      for (int n = 0; n < NC; ++n)
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq)
           red[(wave * NT + n) * 2 * CG + (is_up ? CG : 0) + cq * 4 + qq] = acc[qq][n];
     }
     __syncthreads();
 
-    // gelu_tanh(gate) * up, rounded to bf16, pair-permuted per packed row, + bias
-    if (tid < nch * CG) {
+    // gelu_tanh(gate) * up, rounded to bf16 (where the reference stores its
+    // activation, marlin.cu:421-423), pair-permuted per packed row, + bias
+    if (tid < NC * CG) {
       const int n = tid / CG, ci = tid - n * CG;
       float g = 0.f, up = 0.f;
 #pragma unroll
@@ -474,7 +520,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
         g += red[(w2 * NT + n) * 2 * CG + ci];
         up += red[(w2 * NT + n) * 2 * CG + CG + ci];
       }
-      const float av = (c * CG + ci < a.I) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
+      const float av = (c * CG + ci < Iv) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
       float s8 = av;  // sum over the 8 activations of this packed row (8 adjacent lanes)
       s8 += __shfl_xor(s8, 1, kWave);
       s8 += __shfl_xor(s8, 2, kWave);
@@ -483,7 +529,6 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
       actp[(n * DR + r8) * 8 + 2 * (p & 3) + (p >> 2)] = f32_to_bf16(av);
       if (p == 0) actb[n * DR + r8] = -136.0f * s8;
     }
-    wait_vmem();       // this thread's direct-to-LDS loads of the down rows
     __syncthreads();
 
     // down: y[h] = sum over the task's CG activations of act * w_down
@@ -492,42 +537,42 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, unsigned char
     for (int m = 0; m < DQM; ++m) {
       const int hq = tid + m * T;
       if (hq >= HQ) continue;
-      uint4 dw[DR];
-      float s[DR][4];
+      float y[NC][4];
+#pragma unroll
+      for (int n = 0; n < NC; ++n) y[n][0] = y[n][1] = y[n][2] = y[n][3] = 0.f;
 #pragma unroll
       for (int r = 0; r < DR; ++r) {
-        const int row = c * DR + r;
-        const int g = row / rpg;
-        const bool rok = row < Ip && g < a.Gd;
-        dw[r] = *(const uint4*)(slab + r * HP + 4 * hq);
-        uint2 s2 = sd[m];
-        if (!one_group) s2 = rok ? *(const uint2*)(dsp + (size_t)g * a.H + 4 * hq) : make_uint2(0u, 0u);
-        if (!rok) s2 = make_uint2(0u, 0u);
-        s[r][0] = bf16lo(s2.x);
-        s[r][1] = bf16hi(s2.x);
-        s[r][2] = bf16lo(s2.y);
-        s[r][3] = bf16hi(s2.y);
-      }
-      for (int n = 0; n < nch; ++n) {
-        float y[4] = {0.f, 0.f, 0.f, 0.f};
+        uint2 s2 = opaque(sd[m]);  // a value, so the select below stays a select of values
+        if (!one_group) {
+          const int g = min((c * DR + r) / rpg, a.Gd - 1);
+          s2 = *(const uint2*)(dsp + g * a.H + 4 * hq);
+        }
+        const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+        const uint4 w = opaque(dw[m][r]);
+        const Q4Pairs dq[4] = {unpack_q4(w.x, m43), unpack_q4(w.y, m43), unpack_q4(w.z, m43),
+                               unpack_q4(w.w, m43)};
 #pragma unroll
-        for (int r = 0; r < DR; ++r) {
+        for (int n = 0; n < NC; ++n) {
           const uint4 xp = actq[n * DR + r];
           const float b = actb[n * DR + r];
-          const uint32_t wq[4] = {dw[r].x, dw[r].y, dw[r].z, dw[r].w};
 #pragma unroll
-          for (int qq = 0; qq < 4; ++qq) y[qq] += s[r][qq] * dot8_q4(wq[qq], xp, b, m43);
+          for (int qq = 0; qq < 4; ++qq) y[n][qq] += sc[qq] * dot_unpacked(dq[qq], xp, b);
         }
-        const int slot = P.list[c0 + n];
+      }
+#pragma unroll
+      for (int n = 0; n < NC; ++n) {
+        const int slot = list[c0 + n];
         const float ws = P.slot_w[slot];
-        float* dst = a.part + ((size_t)slot * a.Tg + c) * a.H + 4 * hq;
-        st_coherent_f32(dst + 0, y[0] * ws);
-        st_coherent_f32(dst + 1, y[1] * ws);
-        st_coherent_f32(dst + 2, y[2] * ws);
-        st_coherent_f32(dst + 3, y[3] * ws);
+        const uint32_t off = (uint32_t)(((slot * a.Tg + c) * a.H + 4 * hq) * 4);
+        st_coherent_f4(part, off, make_float4(y[n][0] * ws, y[n][1] * ws, y[n][2] * ws, y[n][3] * ws));
       }
     }
     __syncthreads();  // xs / red / act reused by the next chunk or task
+  };
+  with_count<NT>(min(NT, nmatch), [&](auto nc) { chunk(nc, 0, true); });
+  for (int c0 = NT; c0 < nmatch; c0 += NT) {  // more slots than NT: reload the weights
+    load_weights();
+    with_count<NT>(min(NT, nmatch - c0), [&](auto nc) { chunk(nc, c0, false); });
   }
 }
 
@@ -541,6 +586,7 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
   const int qpw = a.qpw, stripes = T / qpw;
   const int qi = tid & (qpw - 1), st = tid / qpw;
   const int np = a.top_k * a.Tg;
+  const __amdgpu_buffer_rsrc_t part = buffer_rsrc(a.part, a.part_bytes);
   for (int qb = blockIdx.x * qpw; qb < total; qb += gridDim.x * qpw) {
     const int quad = qb + qi;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -550,12 +596,11 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
         const int k = p / a.Tg, cc = p - k * a.Tg;
         const int s = t * a.top_k + k;
         if (P.slot_u[s] >= 0) {
-          const float* src = a.part + ((size_t)s * a.Tg + cc) * a.H + 4 * hq;
-          const uint4 v = ld_coherent_u4(src);
-          acc.x += __uint_as_float(v.x);
-          acc.y += __uint_as_float(v.y);
-          acc.z += __uint_as_float(v.z);
-          acc.w += __uint_as_float(v.w);
+          const float4 v = ld_coherent_f4(part, (uint32_t)(((s * a.Tg + cc) * a.H + 4 * hq) * 4));
+          acc.x += v.x;
+          acc.y += v.y;
+          acc.z += v.z;
+          acc.w += v.w;
         }
       }
     }
@@ -594,15 +639,22 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
 template <int CG, int NT, int JGM, int CPR>
 __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
   constexpr int T = 16 * CG;
+  using Lds = TaskLds<CG, NT, JGM, CPR>;
   __shared__ Prologue P;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ float4 s_scratch[T];
+  __shared__ uint4 s_xs[NT * Lds::KPM];
+  __shared__ float s_xb[NT * Lds::KPM];
+  __shared__ float s_red[Lds::W * NT * 2 * CG];
+  __shared__ __attribute__((aligned(16))) uint16_t s_actp[NT * Lds::DR * 8];
+  __shared__ float s_actb[NT * Lds::DR];
+  const Lds S{s_xs, s_xb, s_red, s_actp, s_actb};
   const int tid = threadIdx.x;
   // barrier generation of this launch (read before this workgroup can arrive)
   const int my_gen = tid == 0 ? load_relaxed(a.ctr) : 0;
   prologue<T>(a, P);
   const int ntask = P.n_unique * a.Tg;
   for (int t = blockIdx.x; t < ntask; t += gridDim.x)
-    run_task<CG, NT, JGM, CPR>(a, P, t / a.Tg, t % a.Tg, smem);
+    run_task<CG, NT, JGM, CPR>(a, P, t / a.Tg, t % a.Tg, S);
 
   // Grid-wide barrier (every partial of every task is written), two-level
   // and sense-reversing: arrivals are spread over kBarrierSubs counters on
@@ -636,7 +688,7 @@ __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
     }
   }
   __syncthreads();
-  reduce_partials<T>(a, P, (float4*)(smem + a.off_slab));
+  reduce_partials<T>(a, P, s_scratch);
 }
 
 // Export of the alignment (gi_moe_align): one workgroup of 256 threads.
@@ -716,32 +768,6 @@ WsLayout ws_layout(int S, int H, int I, int cg) {
   return L;
 }
 
-struct LdsLayout {
-  int slab, xs, xb, sct, red, actp, actb, total;
-};
-
-LdsLayout lds_layout(int cg, int nt, int slab_stride, int H, int Ggu) {
-  const int T = 16 * cg, W = T / 64, DR = cg / 8, Kp = H / 8;
-  (void)Ggu;
-  LdsLayout L;
-  int off = 0;
-  auto take = [&](int bytes) {
-    const int o = off;
-    off += (bytes + 15) / 16 * 16;
-    return o;
-  };
-  const int slab = DR * slab_stride * 4, scratch = T * 16;
-  L.slab = take(slab > scratch ? slab : scratch);
-  L.xs = take(nt * Kp * 16);
-  L.xb = take(nt * Kp * 4);
-  L.sct = 0;
-  L.red = take(W * nt * 2 * cg * 4);
-  L.actp = take(nt * DR * 16);
-  L.actb = take(nt * DR * 4);
-  L.total = off;
-  return L;
-}
-
 struct OccEntry {
   int device;
   const void* fn;
@@ -764,8 +790,6 @@ int blocks_per_cu(const void* fn, int threads, size_t dyn, int* out) {
         return GI_OK;
       }
   }
-  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dyn);
-  if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(MaxDynamicSharedMemorySize)");
   int b = 0;
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, fn, threads, dyn);
   if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
@@ -778,16 +802,9 @@ int blocks_per_cu(const void* fn, int threads, size_t dyn, int* out) {
 template <int CG, int NT, int JGM, int CPR>
 int launch_variant(Args k, int umax, hipStream_t stream) {
   constexpr int T = 16 * CG;
-  const LdsLayout L = lds_layout(CG, NT, CPR * 256, k.H, k.Ggu);
-  k.off_slab = L.slab;
-  k.off_xs = L.xs;
-  k.off_xb = L.xb;
-  k.off_red = L.red;
-  k.off_actp = L.actp;
-  k.off_actb = L.actb;
   const void* fn = (const void*)fused_moe_kernel<CG, NT, JGM, CPR>;
   int bpc = 0;
-  int st = blocks_per_cu(fn, T, (size_t)L.total, &bpc);
+  int st = blocks_per_cu(fn, T, 0, &bpc);
   if (st != GI_OK) return st;
   if (bpc < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE kernel does not fit on a CU");
   const long long tasks = (long long)(umax > 0 ? umax : 1) * k.Tg;
@@ -799,7 +816,7 @@ int launch_variant(Args k, int umax, hipStream_t stream) {
   int qpw = 1;
   while (qpw < per && qpw < T) qpw <<= 1;
   k.qpw = qpw;
-  hipLaunchKernelGGL((fused_moe_kernel<CG, NT, JGM, CPR>), dim3(grid), dim3(T), (size_t)L.total,
+  hipLaunchKernelGGL((fused_moe_kernel<CG, NT, JGM, CPR>), dim3(grid), dim3(T), 0,
                      stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
@@ -826,6 +843,9 @@ int check_moe_shapes(const MoeHostArgs& a) {
   if (a.Ggu <= 0 || a.Gd <= 0)
     return fail(GI_ERR_INVALID_ARG, "fused MoE: scale tensors need at least one group");
   if (a.H > 4096) return fail(GI_ERR_UNSUPPORTED, "fused MoE: H <= 4096 is supported");
+  // partial slabs are addressed with 32-bit byte offsets
+  if ((long long)kMaxSlots * tiles_per_expert(a.I, kTaskCols) * a.H * 4 >= (1LL << 31))
+    return fail(GI_ERR_UNSUPPORTED, "fused MoE: 256 * ceil(I/32) * H * 4 must stay below 2^31 bytes");
   if (a.logits && a.top_k > 64)
     return fail(GI_ERR_UNSUPPORTED, "fused MoE: in-kernel routing supports top_k <= 64");
   if (!a.x || !a.gu_packed || !a.gu_scales || !a.d_packed || !a.d_scales || !a.out)
@@ -897,6 +917,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
     k.status = (int*)(ws + L.status);
     k.ctr = (int*)(ws + L.ctr);
     k.part = (float*)(ws + L.part);
+    k.part_bytes = (uint32_t)(L.total - L.part);
     k.M = rows;
     k.S = rows * h.top_k;
     k.Tg = tiles_per_expert(h.I, cg);
@@ -906,7 +927,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
     k.w = h.w ? (const char*)h.w + (size_t)r0 * h.top_k * w_es : nullptr;
     if (h.logits) k.logits = (const char*)h.logits + (size_t)r0 * h.E * (h.logits_dtype == GI_DTYPE_FP32 ? 4 : 2);
     const int umax = k.S < h.E ? k.S : h.E;
-    st = rows == 1 ? launch_shape<kTaskCols, 1>(k, umax, h.stream) : launch_shape<kTaskCols, 4>(k, umax, h.stream);
+    st = rows == 1 ? launch_shape<kTaskCols, 1>(k, umax, h.stream) : launch_shape<kTaskCols, 2>(k, umax, h.stream);
     if (st != GI_OK) return st;
   }
   return GI_OK;
