@@ -32,6 +32,9 @@ COMMON_FLAGS = [
     "-Wall",
     "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep small private arrays in registers: moved to LDS they cost a full
+    # vmem drain and an LDS round trip per element
+    "-mllvm", "-disable-promote-alloca-to-lds",
 ]
 
 

@@ -49,7 +49,6 @@ constexpr int kMaxSlots = 256;
 constexpr int kMaxExperts = 1024;
 constexpr int kMaxWaves = 16;
 constexpr int kDefaultSpin = 1 << 22;
-constexpr int kBarrierSubs = 8;    // first-level arrival counters of the grid barrier
 constexpr int kCtrStride = 32;     // ints between counters (128 bytes: separate lines)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -70,7 +69,7 @@ struct Args {
   uint16_t* out;
   float* part;      // [S][Tg][H] fp32 partials
   uint32_t part_bytes;
-  int* ctr;         // grid barrier: [0] generation, [kCtrStride] top, [2*kCtrStride + i*kCtrStride] sub i
+  int* ctr;         // grid barrier: [0] launch epoch, [(1 + p) * kCtrStride] arrivals of parity p
   int* status;
   int idx_is64, w_dtype, logits_dtype;
   int M, H, I, E, top_k, gs, Ggu, Gd, S, Tg;
@@ -581,7 +580,8 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
 // ---------------------------------------------------------------------------
 template <int T>
 __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratch) {
-  const int tid = threadIdx.x;
+  constexpr int W = T / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int HQ = a.H >> 2, total = a.M * HQ;
   const int qpw = a.qpw, stripes = T / qpw;
   const int qi = tid & (qpw - 1), st = tid / qpw;
@@ -592,34 +592,52 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (quad < total) {
       const int t = quad / HQ, hq = quad - t * HQ;
-      for (int p = st; p < np; p += stripes) {
-        const int k = p / a.Tg, cc = p - k * a.Tg;
-        const int s = t * a.top_k + k;
-        if (P.slot_u[s] >= 0) {
-          const float4 v = ld_coherent_f4(part, (uint32_t)(((s * a.Tg + cc) * a.H + 4 * hq) * 4));
-          acc.x += v.x;
-          acc.y += v.y;
-          acc.z += v.z;
-          acc.w += v.w;
+      // batches of four partials: addresses and validity first, then the
+      // four loads in flight together (slots without an expert wrote nothing)
+      for (int p0 = st; p0 < np; p0 += 4 * stripes) {
+        float4 v[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = min(p0 + i * stripes, np - 1);
+          const int k = p / a.Tg, cc = p - k * a.Tg;
+          const int s = t * a.top_k + k;
+          ok[i] = p0 + i * stripes < np && P.slot_u[s] >= 0;
+          v[i] = ld_coherent_f4(part, (uint32_t)(((s * a.Tg + cc) * a.H + 4 * hq) * 4));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (ok[i]) {
+            acc.x += v[i].x;
+            acc.y += v[i].y;
+            acc.z += v[i].z;
+            acc.w += v[i].w;
+          }
         }
       }
     }
-    scratch[tid] = acc;
-    __syncthreads();
-    // fixed-shape tree over the stripes (deterministic order)
-    for (int half = stripes >> 1; half >= 1; half >>= 1) {
-      if (st < half) {
-        const float4 v = scratch[tid + half * qpw];
-        acc.x += v.x;
-        acc.y += v.y;
-        acc.z += v.z;
-        acc.w += v.w;
-        scratch[tid] = acc;
-      }
-      __syncthreads();
+    // fixed-shape reduction over the stripes (deterministic order): lanes of
+    // a wave that share qi first, then the waves through LDS
+    for (int off = qpw; off < kWave; off <<= 1) {
+      acc.x += __shfl_xor(acc.x, off, kWave);
+      acc.y += __shfl_xor(acc.y, off, kWave);
+      acc.z += __shfl_xor(acc.z, off, kWave);
+      acc.w += __shfl_xor(acc.w, off, kWave);
     }
+    const int per_wave = qpw < kWave ? qpw : kWave;  // distinct stripes' sums a wave holds
+    if (lane < per_wave) scratch[wave * per_wave + lane] = acc;
+    __syncthreads();
     if (tid < qpw && quad < total) {
-      float4 sum = acc;
+      // quad qi was summed by waves qi / per_wave + k * (qpw / per_wave), in increasing order
+      float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int wstep = qpw / per_wave;  // waves between two holders of the same quad
+      for (int w = qi / per_wave; w < W; w += wstep) {
+        const float4 v = scratch[w * per_wave + (qi % per_wave)];
+        sum.x += v.x;
+        sum.y += v.y;
+        sum.z += v.z;
+        sum.w += v.w;
+      }
       const int t = quad / HQ, hq = quad - t * HQ;
       uint2* o = (uint2*)(a.out + (size_t)t * a.H + 4 * hq);
       if (!a.overwrite) {
@@ -634,6 +652,40 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
     }
     __syncthreads();
   }
+}
+
+// Grid-wide barrier (every partial of every task is written), then the
+// reduction of the partials into out.
+template <int T>
+__device__ __forceinline__ void finish_layer(const Args& a, const Prologue& P, int my_gen, float4* scratch) {
+  const int tid = threadIdx.x;
+  // Grid-wide barrier (every partial of every task is written).  Launches
+  // alternate between two arrival counters by the parity of the launch epoch
+  // (read above, before this workgroup can arrive, so every workgroup of a
+  // launch reads the same value).  Each workgroup adds one arrival; the last
+  // one clears the other parity's counter (idle until the next launch) and
+  // advances the epoch, which the others poll (a separate cache line, so the
+  // polling does not queue behind the arrivals).
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0) {
+    const int G = gridDim.x;
+    int* cnt = a.ctr + (1 + (my_gen & 1)) * kCtrStride;
+    if (atomic_add_relaxed(cnt, 1) == G - 1) {
+      store_relaxed(a.ctr + (1 + ((my_gen + 1) & 1)) * kCtrStride, 0);
+      store_relaxed(a.ctr, my_gen + 1);
+    } else {
+      int spins = 0;
+      while (load_relaxed(a.ctr) == my_gen) {
+        if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
+          atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+          break;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  reduce_partials<T>(a, P, scratch);
 }
 
 template <int CG, int NT, int JGM, int CPR>
@@ -656,42 +708,296 @@ __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
   for (int t = blockIdx.x; t < ntask; t += gridDim.x)
     run_task<CG, NT, JGM, CPR>(a, P, t / a.Tg, t % a.Tg, S);
 
-  // Grid-wide barrier (every partial of every task is written), two-level
-  // and sense-reversing: arrivals are spread over kBarrierSubs counters on
-  // separate cache lines (one counter serialises every atomic); the last
-  // arrival of a sub-counter bumps the top counter; the last of those resets
-  // the counters and advances the generation word that the others poll.
-  wait_vmem();
-  __syncthreads();
-  if (tid == 0) {
-    const int G = gridDim.x, ns = G < kBarrierSubs ? G : kBarrierSubs, i = blockIdx.x % ns;
-    const int members = G / ns + (i < G % ns);
-    int* gen = a.ctr;
-    int* top = a.ctr + kCtrStride;
-    int* sub = a.ctr + 2 * kCtrStride;
-    bool last = false;
-    if (atomic_add_relaxed(sub + i * kCtrStride, 1) == members - 1)
-      last = atomic_add_relaxed(top, 1) == ns - 1;
-    if (last) {
-      for (int k2 = 0; k2 < ns; ++k2) store_relaxed(sub + k2 * kCtrStride, 0);
-      store_relaxed(top, 0);
-      wait_vmem();
-      store_relaxed(gen, my_gen + 1);
-    } else {
-      int spins = 0;
-      while (load_relaxed(gen) == my_gen) {
-        if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
-          atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
-          break;
-        }
-      }
-    }
-  }
-  __syncthreads();
-  reduce_partials<T>(a, P, s_scratch);
+  finish_layer<T>(a, P, my_gen, s_scratch);
 }
 
 // Export of the alignment (gi_moe_align): one workgroup of 256 threads.
+// ---------------------------------------------------------------------------
+// Matrix-core task (group_size a multiple of 32; up to 8 resident tokens)
+//
+// Both projections run on v_mfma_f32_16x16x32_bf16, D[16x16] += A[16x32] *
+// B[32x16], lane l holding A[l%16][8(l/16)..+8), B[8(l/16)..+8][l%16] and
+// D[4(l/16)..+4][l%16].  B is the weights: one packed word per lane is
+// exactly 8 consecutive k of one output column, unpacked to bf16 (128+q)
+// pairs in the order (0,4)(2,6)(1,5)(3,7).  A is the activations of up to 16
+// slots (rows), kept in LDS in that same k order.  A second product against a
+// constant -136 matrix supplies -136*sum(a), so D + Db = sum a*(q-8) exactly
+// as the fp32 accumulation of bf16 products; the group scale multiplies that
+// when a scale group ends.  Per packed word this is 7 VALU (the unpack),
+// whatever the number of tokens.
+//
+//   gate/up  wave w owns k blocks [w*KBW, (w+1)*KBW) (32 k each) for all 64
+//            task columns: lane (lq = l/16, lr = l%16) loads the 16-byte word
+//            quad of columns 4lr..4lr+3 (gate for lr < 8, up otherwise) at
+//            packed row 4kb+lq; word i feeds MFMA i, whose column lr is task
+//            column 4lr+i.  Partial sums per wave go through LDS.
+//   act      gelu_tanh(gate)*up rounded to bf16 (marlin.cu:421-423).
+//   down     one A operand for the task (the activations); wave w owns the
+//            64-column output groups [w*DGW, (w+1)*DGW), one word quad per
+//            lane and group, the scale of the task's (single) group.
+// ---------------------------------------------------------------------------
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaThreads = 512;
+constexpr int kMfmaWaves = kMfmaThreads / kWave;
+constexpr int kResidentTokens = 8;   // x rows staged in LDS by the prologue
+constexpr int kChunkRows = 16;       // slots per MFMA pass
+constexpr uint32_t kNeg136Pair = 0xC308C308u;  // bf16 -136, twice
+
+__device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+// 8 bf16 values in the k order of an unpacked word: (0,4) (2,6) (1,5) (3,7)
+__device__ __forceinline__ uint4 mfma_k_order(uint4 d) {
+  const uint4 p = pair_permute(d);
+  return make_uint4(p.x, p.z, p.y, p.w);
+}
+__device__ __forceinline__ uint4 q4_operand(uint32_t w, uint32_t m43) {
+  const Q4Pairs q = unpack_q4(w, m43);
+  return make_uint4(q.p0, q.p1, q.p2, q.p3);
+}
+// position of element p (0..7) of a packed row in that order
+__device__ __forceinline__ int mfma_k_pos(int p) { return (p & 1) * 4 + (p & 2) + (p >> 2); }
+
+template <int KBW, int DGW>
+struct MfmaLds {
+  static constexpr int KPM = 4 * KBW * kMfmaWaves;  // packed x rows staged (>= H/8)
+  static constexpr int GW = KBW + 1;                // scale groups one wave's k blocks can touch
+};
+
+template <int KBW, int DGW>
+__device__ void run_task_mfma(const Args& a, Prologue& P, int u, int c, const uint4* s_x, float4* s_red,
+                              uint4* s_act, uint4* s_sc) {
+  constexpr int KPM = MfmaLds<KBW, DGW>::KPM;
+  constexpr int GW = MfmaLds<KBW, DGW>::GW;
+  constexpr int SCT = (GW * 8 + kWave - 1) / kWave;  // scale chunks per lane
+  static_assert(SCT <= 3, "three scale chunks per lane at most");
+  constexpr int W = kMfmaWaves;
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));  // per-task lane offsets, not hoisted out of the task loop
+  const int lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lr = lane & 15, lq = lane >> 4;
+  const int e = P.uexp[u];
+  const int Kp = a.H >> 3, Ip = a.I >> 3, twoI = 2 * a.I;
+  const int HG = (a.H + 63) >> 6;            // 64-column output groups
+  const int KPG = a.gs >> 5;                 // 32-k blocks per scale group
+  const int Iv = min(a.I, a.Gd * a.gs);      // activations past the last down group are dropped
+
+  const int* list;
+  int nmatch;
+  if (a.S <= kWave) {
+    list = P.csr + P.uoff[u];
+    nmatch = P.uoff[u + 1] - P.uoff[u];
+  } else {
+    gather_list<kMfmaThreads>(a, P, u);
+    list = P.list;
+    nmatch = P.n_list;
+  }
+
+  // this lane's four task columns (gate for lr < 8, up otherwise)
+  const int tcol = 4 * lr;
+  const int icol = c * 32 + (tcol & 31);
+  const bool col_ok = icol < a.I;
+  const int gcol = (col_ok ? icol : 0) + (lr < 8 ? 0 : a.I);
+  const int32_t* gp = a.gu_packed + (size_t)e * Kp * twoI + gcol;
+  const int prow = min(c * 4 + lq, Ip - 1);  // this lane's packed down row
+  const int gd = min((c * 32) / a.gs, a.Gd - 1);
+  const int32_t* dp = a.d_packed + ((size_t)e * Ip + prow) * a.H;
+  const uint16_t* dsp = a.d_scales + ((size_t)e * a.Gd + gd) * a.H;
+  const int kb0 = wave * KBW;
+
+  // The gate/up scale rows of the groups this wave's k blocks touch,
+  // [group][64 task columns] bf16, go to the wave's own LDS slice (8 x 16
+  // bytes per group: gate quarters, then up quarters); no workgroup barrier.
+  const int wg0 = kb0 / KPG;  // first scale group of this wave
+  const uint16_t* sc_base = a.gu_scales + (size_t)e * a.Ggu * twoI;
+  uint4* w_sc = s_sc + wave * GW * 8;
+  // (named values, not an array: a private array may be placed in LDS)
+  uint4 scv0 = make_uint4(0u, 0u, 0u, 0u), scv1 = scv0, scv2 = scv0;
+  auto sc_load = [&](int i) {
+    const int id = lane + i * kWave, g = min(wg0 + (id >> 3), a.Ggu - 1), part = id & 7;
+    return *(const uint4*)(sc_base + (size_t)g * twoI + (part < 4 ? 0 : a.I) + min(c * 32 + 8 * (part & 3), a.I - 8));
+  };
+  uint4 wv[KBW];
+  uint4 dw[DGW];
+  uint2 sdw[DGW];
+  // Fixed-count register loads (clamped addresses): scales, gate/up, down,
+  // in that order, so the compiler's vmcnt waits stay exact.
+  auto load_weights = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    scv0 = sc_load(0);
+    if constexpr (SCT > 1) scv1 = sc_load(1);
+    if constexpr (SCT > 2) scv2 = sc_load(2);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < KBW; ++j) {
+      const int kb = kb0 + j;
+      wv[j] = load_nt_u4(gp + min(4 * kb + lq, Kp - 1) * twoI);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int m = 0; m < DGW; ++m) {
+      const int col = min((wave * DGW + m) * 64 + tcol, a.H - 4);
+      dw[m] = load_nt_u4(dp + col);
+      sdw[m] = *(const uint2*)(dsp + col);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  load_weights();
+  const uint32_t m43 = magic43();
+  const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
+  const uint4 bneg = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < nmatch; c0 += kChunkRows) {
+    if (c0 > 0) load_weights();  // more than 16 slots: stream the weights again
+    bool sc_staged = false;
+    const int nc = min(kChunkRows, nmatch - c0);
+    // A rows: row lr is slot list[c0 + lr]
+    const int my_slot = lr < nc ? list[c0 + lr] : 0;
+    const uint4* xrow = s_x + (size_t)(my_slot / a.top_k) * KPM;
+    const bool a_ok = lr < nc;
+
+    // ---- gate/up over this wave's k blocks
+    f32x4_t D[4] = {zf, zf, zf, zf};
+    f32x4_t Db = zf;
+    float y[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i][0] = y[i][1] = y[i][2] = y[i][3] = 0.f;
+    int next_end = (kb0 / KPG + 1) * KPG;  // first k block of the next scale group
+#pragma unroll
+    for (int j = 0; j < KBW; ++j) {
+      const int kb = kb0 + j;
+      const uint4 A = a_ok ? xrow[4 * kb + lq] : zero4;
+      const uint4 w = opaque(wv[j]);
+      D[0] = mfma_bf16(A, q4_operand(w.x, m43), D[0]);
+      D[1] = mfma_bf16(A, q4_operand(w.y, m43), D[1]);
+      D[2] = mfma_bf16(A, q4_operand(w.z, m43), D[2]);
+      D[3] = mfma_bf16(A, q4_operand(w.w, m43), D[3]);
+      Db = mfma_bf16(A, bneg, Db);
+      if (kb + 1 == next_end || j == KBW - 1) {  // a scale group ends here
+        if (!sc_staged) {  // first group end of the wave: its scale loads (issued first) are in
+          if (lane < GW * 8) w_sc[lane] = scv0;  // (the wave's slice holds GW groups)
+          if constexpr (SCT > 1) {
+            if (lane + kWave < GW * 8) w_sc[lane + kWave] = scv1;
+          }
+          if constexpr (SCT > 2) {
+            if (lane + 2 * kWave < GW * 8) w_sc[lane + 2 * kWave] = scv2;
+          }
+          sc_staged = true;
+        }
+        const uint2 s2 = ((const uint2*)(w_sc + (kb / KPG - wg0) * 8))[lr];  // task columns 4lr..4lr+3
+        const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (D[i][jj] + Db[jj]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) D[i] = zf;
+        Db = zf;
+        next_end += KPG;
+      }
+    }
+    // per-wave partials: row 4lq+jj, task columns 4lr..4lr+3
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int row = 4 * lq + jj;
+      if (row < nc) s_red[(wave * kChunkRows + row) * 16 + lr] = make_float4(y[0][jj], y[1][jj], y[2][jj], y[3][jj]);
+    }
+    __syncthreads();
+
+    // ---- activation: row n, intermediate column c*32 + ci
+    if (tid < nc * 32) {
+      const int n = tid >> 5, ci = tid & 31;
+      float g = 0.f, up = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < W; ++w2) {
+        const float* rg = (const float*)(s_red + (w2 * kChunkRows + n) * 16);
+        g += rg[ci];
+        up += rg[32 + ci];
+      }
+      const float av = (c * 32 + ci < Iv) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
+      ((uint16_t*)s_act)[(n * 4 + (ci >> 3)) * 8 + mfma_k_pos(ci & 7)] = f32_to_bf16(av);
+    }
+    __syncthreads();
+
+    // ---- down over this wave's 64-column groups
+    const uint4 Ad = a_ok ? s_act[lr * 4 + lq] : zero4;
+    const f32x4_t Dbd = mfma_bf16(Ad, bneg, zf);
+    int slot_r[4];
+    float ws_r[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int row = 4 * lq + jj;
+      slot_r[jj] = row < nc ? list[c0 + row] : -1;
+      ws_r[jj] = row < nc ? P.slot_w[slot_r[jj]] : 0.f;
+    }
+    const __amdgpu_buffer_rsrc_t part = buffer_rsrc(a.part, a.part_bytes);
+#pragma unroll
+    for (int m = 0; m < DGW; ++m) {
+      const int gc = wave * DGW + m;
+      if (gc >= HG) break;
+      const uint4 w = opaque(dw[m]);
+      const f32x4_t D0 = mfma_bf16(Ad, q4_operand(w.x, m43), zf);
+      const f32x4_t D1 = mfma_bf16(Ad, q4_operand(w.y, m43), zf);
+      const f32x4_t D2 = mfma_bf16(Ad, q4_operand(w.z, m43), zf);
+      const f32x4_t D3 = mfma_bf16(Ad, q4_operand(w.w, m43), zf);
+      const uint2 s2 = opaque(sdw[m]);
+      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const int col = gc * 64 + tcol;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        if (slot_r[jj] >= 0 && col < a.H) {
+          const float wgt = ws_r[jj];
+          const uint32_t off = (uint32_t)(((slot_r[jj] * a.Tg + c) * a.H + col) * 4);
+          st_coherent_f4(part, off, make_float4(sc[0] * (D0[jj] + Dbd[jj]) * wgt, sc[1] * (D1[jj] + Dbd[jj]) * wgt,
+                                                sc[2] * (D2[jj] + Dbd[jj]) * wgt, sc[3] * (D3[jj] + Dbd[jj]) * wgt));
+        }
+      }
+    }
+    __syncthreads();  // s_red / s_act reused by the next chunk or task
+  }
+}
+
+template <int KBW, int DGW>
+__global__ __launch_bounds__(kMfmaThreads) void fused_moe_mfma_kernel(Args a) {
+  constexpr int T = kMfmaThreads;
+  constexpr int KPM = MfmaLds<KBW, DGW>::KPM;
+  constexpr int XPT = (kResidentTokens * KPM + T - 1) / T;
+  __shared__ Prologue P;
+  __shared__ float4 s_scratch[T];
+  __shared__ uint4 s_x[kResidentTokens * KPM];
+  __shared__ float4 s_red[kMfmaWaves * kChunkRows * 16];
+  __shared__ uint4 s_act[kChunkRows * 4];
+  __shared__ uint4 s_sc[kMfmaWaves * MfmaLds<KBW, DGW>::GW * 8];
+  const int tid = threadIdx.x;
+  // The launch's tokens' activations, loaded before routing so that their
+  // latency overlaps the router logits' (x does not depend on the routing).
+  const int Kp = a.H >> 3, Kv = min(Kp, a.Ggu * (a.gs >> 3));
+  uint4 xr[XPT];
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int id = tid + i * T, n = id / KPM, r = id - n * KPM;
+    const bool v = n < a.M && r < Kv;
+    xr[i] = v ? *(const uint4*)(a.x + (size_t)n * a.H + 8 * r) : make_uint4(0u, 0u, 0u, 0u);
+  }
+  // barrier generation of this launch (read before this workgroup can arrive)
+  const int my_gen = tid == 0 ? load_relaxed(a.ctr) : 0;
+  prologue<T>(a, P);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int id = tid + i * T;
+    if (id < a.M * KPM) s_x[id] = mfma_k_order(xr[i]);
+  }
+  __syncthreads();
+  const int ntask = P.n_unique * a.Tg;
+  for (int t = blockIdx.x; t < ntask; t += gridDim.x)
+    run_task_mfma<KBW, DGW>(a, P, t / a.Tg, t % a.Tg, s_x, s_red, s_act, s_sc);
+  finish_layer<T>(a, P, my_gen, s_scratch);
+}
+
 __global__ __launch_bounds__(256) void moe_align_kernel(Args a, int32_t* uniq, int32_t* nuniq,
                                                          int32_t* s2u, int32_t* offsets,
                                                          int32_t* slots) {
@@ -763,7 +1069,7 @@ WsLayout ws_layout(int S, int H, int I, int cg) {
   WsLayout L;
   L.status = 0;
   L.ctr = kAlign;
-  L.part = kAlign + round_up((size_t)(2 + kBarrierSubs) * kCtrStride * sizeof(int));
+  L.part = kAlign + round_up((size_t)3 * kCtrStride * sizeof(int));
   L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
   return L;
 }
@@ -797,6 +1103,44 @@ int blocks_per_cu(const void* fn, int threads, size_t dyn, int* out) {
   if (g_occ_n < 64) g_occ[g_occ_n++] = OccEntry{dev, fn, dyn, b};
   *out = b;
   return GI_OK;
+}
+
+// Persistent grid: every workgroup resident (the grid barrier needs it), no
+// more workgroups than tasks; the reduction's output quads per pass.
+int launch_grid(const void* fn, int T, Args& k, int umax, int* grid_out) {
+  int bpc = 0;
+  int st = blocks_per_cu(fn, T, 0, &bpc);
+  if (st != GI_OK) return st;
+  if (bpc < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE kernel does not fit on a CU");
+  const long long tasks = (long long)(umax > 0 ? umax : 1) * k.Tg;
+  const long long resident = (long long)bpc * device_cu_count();
+  const int grid = (int)(tasks < resident ? tasks : resident);
+  const int total_quads = k.M * (k.H / 4);
+  const int per = (total_quads + grid - 1) / grid;
+  int qpw = 1;
+  while (qpw < per && qpw < T) qpw <<= 1;
+  k.qpw = qpw;
+  *grid_out = grid;
+  return GI_OK;
+}
+
+template <int KBW, int DGW>
+int launch_mfma_variant(Args k, int umax, hipStream_t stream) {
+  const void* fn = (const void*)fused_moe_mfma_kernel<KBW, DGW>;
+  int grid = 0;
+  const int st = launch_grid(fn, kMfmaThreads, k, umax, &grid);
+  if (st != GI_OK) return st;
+  hipLaunchKernelGGL((fused_moe_mfma_kernel<KBW, DGW>), dim3(grid), dim3(kMfmaThreads), 0, stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "fused MoE launch");
+  return GI_OK;
+}
+
+int launch_mfma_shape(const Args& k, int umax, hipStream_t stream) {
+  // (32-k blocks per wave, 64-column down groups per wave) by hidden size
+  if (k.H <= 512) return launch_mfma_variant<2, 1>(k, umax, stream);
+  if (k.H <= 2816) return launch_mfma_variant<11, 6>(k, umax, stream);
+  return launch_mfma_variant<16, 8>(k, umax, stream);
 }
 
 template <int CG, int NT, int JGM, int CPR>
@@ -876,9 +1220,13 @@ int launch_fused_moe(const MoeHostArgs& h) {
   int st = check_moe_shapes(h);
   if (st != GI_OK) return st;
   if (h.M == 0) return GI_OK;
-  const int rows_per = moe_rows_per_launch(h.top_k);
-  if (h.logits && h.M > rows_per)
-    return fail(GI_ERR_UNSUPPORTED, "fused MoE layer: M*top_k must be <= 256");
+  // Matrix-core path when every scale group is whole 32-k blocks and there is
+  // more than one token (one packed word then serves every token of the
+  // expert): launches of up to 8 rows, their activations resident in LDS.
+  // A single token, or other group sizes, take the VALU path.
+  const bool mfma = h.gs % 32 == 0 && h.M > 1;
+  const int rows_vl = moe_rows_per_launch(h.top_k);
+  const int rows_per = mfma ? (rows_vl < kResidentTokens ? rows_vl : kResidentTokens) : rows_vl;
   if (!h.workspace || h.workspace_bytes < moe_workspace_bytes(h.M, h.top_k, h.H, h.I, h.E))
     return fail(GI_ERR_WORKSPACE,
                 "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
@@ -926,8 +1274,11 @@ int launch_fused_moe(const MoeHostArgs& h) {
     k.idx = h.idx ? (const char*)h.idx + (size_t)r0 * h.top_k * idx_es : nullptr;
     k.w = h.w ? (const char*)h.w + (size_t)r0 * h.top_k * w_es : nullptr;
     if (h.logits) k.logits = (const char*)h.logits + (size_t)r0 * h.E * (h.logits_dtype == GI_DTYPE_FP32 ? 4 : 2);
+    k.out_idx = h.out_idx ? h.out_idx + (size_t)r0 * h.top_k : nullptr;
+    k.out_w = h.out_w ? (uint16_t*)h.out_w + (size_t)r0 * h.top_k : nullptr;
     const int umax = k.S < h.E ? k.S : h.E;
-    st = rows == 1 ? launch_shape<kTaskCols, 1>(k, umax, h.stream) : launch_shape<kTaskCols, 2>(k, umax, h.stream);
+    if (mfma) st = launch_mfma_shape(k, umax, h.stream);
+    else st = rows == 1 ? launch_shape<kTaskCols, 1>(k, umax, h.stream) : launch_shape<kTaskCols, 2>(k, umax, h.stream);
     if (st != GI_OK) return st;
   }
   return GI_OK;

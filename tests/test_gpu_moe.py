@@ -122,6 +122,25 @@ def test_fused_small_shapes(small, m):
     assert_bf16_close(out, ref, f"small m={m}")
 
 
+@pytest.mark.parametrize("gs", [8, 16, 24, 32, 96])
+@pytest.mark.parametrize("m", [1, 3, 9])
+def test_fused_group_sizes(gs, m):
+    """Group sizes that are not multiples of 32 take the VALU kernel, the others
+    the matrix-core kernel; 24 and 96 leave a ragged last group (ceil groups)."""
+    W = synth.moe_weights(E=8, H=256, I=128, group_size=gs, seed=gs + m)
+    Wd = _dev(W)
+    x = synth.activations(m, 256, seed=m + 40)
+    logits = synth.router_logits(m, 8, seed=m + 40)
+    idx, _, w = O.route_topk_softmax(np64(logits), 2)
+    idx_t = torch.from_numpy(idx)
+    w_t = torch.from_numpy(w).to(torch.bfloat16)
+    out = torch.zeros(m, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx_t.to(DEV), w_t.to(DEV), out, gs)
+    ref, _ = _oracle_moe(x, W, idx_t, w_t, torch.zeros(m, 256), gs)
+    assert_bf16_close(out, ref, f"gs={gs} m={m}")
+
+
 def test_fused_duplicates_invalid_and_dtypes(small):
     """Duplicate ids within a token are separate slots (pybind.cpp:219-244, no
     MAX_MATCH cap); ids outside [0, E) are skipped (marlin.cu:304,473);
@@ -154,8 +173,9 @@ def test_fused_gemma_shapes_gs128(gemma128, m, noise):
 
 
 def test_layer_from_logits_gemma(gemma128):
+    """Layer mode; 12 and 16 rows take several launches of up to 8 rows each."""
     W, Wd = gemma128
-    for m, noise in ((1, 0.0), (7, 0.5)):
+    for m, noise in ((1, 0.0), (7, 0.5), (12, 0.5), (16, 0.0)):
         x = synth.activations(m, 2816, seed=10 + m)
         logits = synth.router_logits(m, 128, seed=10 + m, verify_noise=noise)
         out, idx, w = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"],
