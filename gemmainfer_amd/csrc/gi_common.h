@@ -206,6 +206,13 @@ __device__ __forceinline__ float4 ld_coherent_f4(__amdgpu_buffer_rsrc_t r, uint3
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Workgroup barrier for LDS data: waits for this wave's LDS (and scalar)
+// accesses and meets the other waves, leaving global loads in flight.
+// __syncthreads() also waits for vmcnt(0) (its workgroup-scope fence), which
+// would drain every prefetched weight load at each barrier.  Global data
+// handed between waves needs wait_vmem() before this barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // ---- counters (agent scope) -------------------------------------------------
 __device__ __forceinline__ int atomic_add_relaxed(int* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -46,6 +46,11 @@ struct MoeHostArgs {
 int moe_rows_per_launch(int top_k);
 size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E);
 int launch_fused_moe(const MoeHostArgs& a);
+// decode/verify kernel (moe_decode.hip): <= 8 rows per launch, no grid barrier
+bool moe_decode_supported(const MoeHostArgs& h);
+int moe_decode_rows_per_launch(int top_k);
+size_t moe_decode_state_bytes();        // epochs + exchange buffers: kept between calls
+int launch_moe_decode(const MoeHostArgs& h, void* state, int* status);
 int launch_moe_align(const void* idx, int is64, int M, int top_k, int E, int32_t* uniq,
                      int32_t* nuniq, int32_t* s2u, int32_t* offsets, int32_t* slots,
                      hipStream_t stream);

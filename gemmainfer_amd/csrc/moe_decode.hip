@@ -1,0 +1,1190 @@
+// Token-Union W4A16 fused MoE for decode and speculative verify on gfx950:
+// at most 8 tokens (64 slots) per launch, one launch per layer, no grid-wide
+// barrier, no partial sums in memory.
+//
+// Reference behaviour restated (paths relative to the GemmaInfer repo):
+//   routing        gemmainfer/models/gemma.py:77-80
+//   dedup          csrc/marlin.cu:285-335 (gate_up) / :453-505 (down)
+//   gate_up + GELU csrc/marlin.cu:337-426
+//   down + combine csrc/marlin.cu:507-586
+//
+// A launch has G workgroups of 512 threads, one per CU, all resident.  Every
+// workgroup routes the tokens (layer mode) or reads the routing, and builds
+// the Token-Union tables in LDS: the unique experts in ascending id order
+// (a bitmap of the selected ids and prefix popcounts), each expert's token
+// mask, and the activation rows in expert order (expert u's tokens, in token
+// order, occupy rows epos[u] .. epos[u+1]).  The number U of unique experts
+// then picks the split of the grid into two roles from a table the host
+// computed for every U (the split that balances the weight bytes per CU):
+//
+//   gate/up  workgroups [0, n_gu).  Item (u, c) is unique expert u times the
+//            32 intermediate columns [32c, 32c+32).  The item's gate and up
+//            words (64 columns over the whole hidden size) are issued at once
+//            as fixed-count 16-byte loads, two items ahead, and multiplied on
+//            the matrix cores against every token's x, which sits in LDS
+//            (one more product against a constant operand gives the offset
+//            term of the int4 decoding).  The waves' sums are reduced in LDS,
+//            then gelu_tanh(gate)*up is rounded to bf16 (where the reference
+//            stores its activation, marlin.cu:421-423) and written to the
+//            exchange buffer at the rows of the tokens routed to u.
+//   down     workgroups [n_gu, n_gu + n_dn).  One or two units of 32 output
+//            columns.  Each wave owns a contiguous range of the (expert,
+//            32-k block) pairs, issues their down words at once and keeps
+//            them in registers, then all 512 threads poll the exchange
+//            buffer and copy its rows into LDS.  The products run on the
+//            matrix cores (rows = tokens), are scaled per group and routing
+//            weight into per-token fp32 sums, reduced over the waves in a
+//            fixed order, and out is written (or added to) once, in bf16.
+//
+// Deterministic: every sum has a fixed order, whatever the timing.  Slots of
+// one token with the same expert (possible only with caller-given ids) are
+// one row whose weight is the sum of theirs, in slot order.
+//
+// Exchange: activations are stored bit-inverted, 16 bytes at a time, into one
+// of two buffers chosen by the parity of the launch epoch.  A stored 16-bit
+// value is never zero (the one bf16 pattern that would invert to zero, a NaN
+// with every bit set, is stored as the canonical NaN), so an all-zero value
+// means "not written yet": the reader polls the data itself, one round trip,
+// no flag to order against it, and a chunk with any zero half-word is simply
+// read again.  Each launch's down workgroups clear the other parity's buffer
+// for the next launch (the workspace starts zero-filled).
+//
+// Launch epochs: the workspace holds kEpochSlots 64-bit epoch words, all
+// equal.  Workgroup b reads word b at launch start, adds one, and stores the
+// result to every word j with j % G == b, so all words advance by one per
+// launch whatever the grid size.  No contended atomics are used anywhere:
+// on this part a returning atomic on one address costs microseconds when 256
+// workgroups issue it.
+//
+// Code shape: the hot loops are straight-line with register indices fixed at
+// compile time, per-expert values are read from registers with readlane (no
+// LDS round trip before a weight load), no integer division in a loop (group
+// sizes are powers of two), and one buffer resource per tensor with a scalar
+// per-expert offset.
+
+#include "../../include/gemmainfer_amd.h"
+#include "gi_common.h"
+#include "gi_internal.h"
+#include "moe_shared.h"
+
+namespace gi {
+
+namespace {
+
+using namespace moe;
+
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kRows = 8;              // tokens per launch (matrix-core rows used)
+constexpr int kSlots = 64;            // slots per launch
+constexpr int kEpochSlots = 1024;     // also the largest grid
+constexpr int kCols = 32;             // intermediate columns per item == down k block
+constexpr int kUnitCols = 32;         // output columns of a down unit
+constexpr int kDefaultSpin = 1 << 20;
+constexpr int kCpolNt = 2;            // non-temporal: weights are read once
+constexpr int kMaxItems = 9;          // gate/up items per workgroup and launch
+constexpr int kDownRegs = 64;         // down-word registers (uint2 units) per wave and batch
+constexpr int kDownKpw = 3;           // down k blocks per wave: Tk <= 24 (I <= 768)
+constexpr int kMaxI = kCols * kDownKpw * kWaves;  // 768
+constexpr size_t kActParity = (size_t)kSlots * kMaxI * 2;  // bytes of one exchange buffer
+constexpr int kScaleLoads = 4;        // 16-byte down-scale chunks per thread (2048 per workgroup)
+constexpr int kMaxStage = 12;         // exchange chunks per thread: 64 rows of I/8 <= 96 chunks
+constexpr uint32_t kOob = 0xFFFFFFF0u;  // buffer offset past any resource: the load returns zeros
+
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+// A value every lane of the wave holds (read from LDS, so the compiler cannot
+// tell): made scalar, so that buffer offsets built from it need no per-lane
+// loop and loop control stays on the scalar unit.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// Orders LDS accesses of this wave before the next instruction (no vmcnt wait).
+__device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+struct DecArgs {
+  const uint16_t* x;
+  const int32_t* gu_packed;
+  const uint16_t* gu_scales;
+  const int32_t* d_packed;
+  const uint16_t* d_scales;
+  const void* idx;
+  const void* w;
+  const void* logits;
+  const float* expert_scale;
+  int32_t* out_idx;
+  uint16_t* out_w;
+  uint16_t* out;
+  unsigned long long* epochs;  // [kEpochSlots]
+  uint16_t* act;               // [2][kSlots][I] (parity stride kActParity bytes): rows in expert
+                               // order, inverted bf16, matrix-core k order
+  int* status;
+  uint32_t gu_bytes, gus_bytes, dn_bytes;  // one expert's packed gate/up, its scales, packed down
+  uint32_t gu_total, gus_total, dn_total;  // whole tensors (buffer resource sizes)
+  uint32_t dsc_total;                      // down scales tensor
+  int idx_is64, w_dtype, logits_dtype;
+  int M, H, I, E, top_k, Ggu, Gd, S;
+  int gsh;      // group_size = 32 << gsh
+  int Tk;       // I / 32: items per expert, k blocks of the down projection
+  int units;    // H / 32 column units of the down projection
+  int overwrite, spin_limit;
+  uint16_t n_gu[kSlots + 1];  // gate/up workgroups when the launch has U unique experts
+  uint16_t n_dn[kSlots + 1];  // down workgroups for U
+};
+
+struct DecPrologue {
+  int slot_e[kSlots];
+  float slot_w[kSlots];
+  uint32_t bm[32];                 // bitmap of the selected expert ids (E <= 1024)
+  uint32_t tm[kSlots];             // token mask of unique expert u
+  int uexp[kSlots];                // expert id of unique expert u
+  int epos[kSlots + 1];            // expert u's rows are [epos[u], epos[u+1])
+  __attribute__((aligned(8))) int8_t rowpos[kSlots][kRows];  // row of (u, token), -1 if none
+  __attribute__((aligned(16))) float roww[kSlots][kRows];    // routing weight of (u, token), 0 if none
+  int n_unique;
+};
+
+// ---------------------------------------------------------------------------
+// prologue: routing, Token-Union tables
+// ---------------------------------------------------------------------------
+// Inclusive prefix sum over the wave: shifts inside each 16-lane row, then
+// the row totals broadcast into the rows above (DPP, no LDS round trip).
+__device__ __forceinline__ int wave_scan_incl(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return v;
+}
+
+__device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int S = a.S;
+  if (tid < 32) P.bm[tid] = 0u;
+  if (tid < kSlots) P.tm[tid] = 0u;
+  (&P.rowpos[0][0])[tid] = -1;  // kSlots * kRows == kThreads entries
+  (&P.roww[0][0])[tid] = 0.f;
+  if (a.logits) {
+    if (wave < a.M) route_token_any(a, wave, lane, P.slot_e + wave * a.top_k, P.slot_w + wave * a.top_k);
+  } else if (tid < S) {
+    const int e = load_expert_id(a.idx, a.idx_is64, tid);
+    P.slot_e[tid] = (e >= 0 && e < a.E) ? e : -1;
+    P.slot_w[tid] = load_weight_as_bf16(a.w, a.w_dtype, tid);
+  }
+  lds_barrier();
+  if (wave == 0) {
+    int e = lane < S ? P.slot_e[lane] : -1;
+    float w = lane < S ? P.slot_w[lane] : 0.f;
+    const int t = lane / a.top_k;
+    if (a.logits) {
+      w = round_to_bf16(w);
+      if (blockIdx.x == 0 && lane < S) {
+        if (a.out_idx) a.out_idx[lane] = e;
+        if (a.out_w) a.out_w[lane] = f32_to_bf16(w);
+      }
+    } else {
+      // a token's slots with one expert: the first keeps the sum of their
+      // weights (in slot order), the others are dropped
+      const int t0 = t * a.top_k;
+      float ws = 0.f;
+      bool first = true;
+      for (int k2 = 0; k2 < a.top_k; ++k2) {
+        const int j = min(t0 + k2, kWave - 1);
+        const int ej = __shfl(e, j, kWave);
+        const float wj = __shfl(w, j, kWave);
+        if (t0 + k2 < S && e >= 0 && ej == e) {
+          ws += wj;
+          if (t0 + k2 < lane) first = false;
+        }
+      }
+      w = ws;
+      if (!first) e = -1;
+    }
+    // unique experts in ascending id order
+    if (e >= 0) __hip_atomic_fetch_or(&P.bm[e >> 5], 1u << (e & 31), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    lds_fence();
+    const uint32_t word = lane < 32 ? P.bm[lane] : 0u;
+    const int cnt = __popc(word);
+    const int incl = wave_scan_incl(cnt);
+    const int U = __shfl(incl, kWave - 1, kWave);
+    const int wi = max(e, 0) >> 5;
+    const int base = __shfl(incl - cnt, wi, kWave);
+    const uint32_t bw = (uint32_t)__shfl((int)word, wi, kWave);
+    const int u = e >= 0 ? base + __popc(bw & ((1u << (e & 31)) - 1u)) : -1;
+    if (u >= 0) {
+      __hip_atomic_fetch_or(&P.tm[u], 1u << t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      P.uexp[u] = e;
+      P.roww[u][t] = w;
+    }
+    lds_fence();
+    // rows in expert order, tokens ascending within an expert
+    const uint32_t tmu = lane < U ? P.tm[lane] : 0u;
+    const int c2 = __popc(tmu);
+    const int inc2 = wave_scan_incl(c2);
+    const int total = __shfl(inc2, kWave - 1, kWave);
+    const int ep0 = inc2 - c2;
+    if (lane < U) {
+      P.epos[lane] = ep0;
+      uint32_t lo = 0u, hi = 0u;
+#pragma unroll
+      for (int t2 = 0; t2 < kRows; ++t2) {
+        const int r = ((tmu >> t2) & 1u) ? ep0 + __popc(tmu & ((1u << t2) - 1u)) : -1;
+        if (t2 < 4) lo |= ((uint32_t)r & 0xffu) << (8 * t2);
+        else hi |= ((uint32_t)r & 0xffu) << (8 * (t2 - 4));
+      }
+      *(uint2*)&P.rowpos[lane][0] = make_uint2(lo, hi);
+    }
+    if (lane == 0) {
+      P.epos[U] = total;
+      P.n_unique = U;
+    }
+  }
+  lds_barrier();
+}
+
+// Launch epoch (see the header).
+__device__ __forceinline__ unsigned long long load_epoch(const DecArgs& a) {
+  return __hip_atomic_load(a.epochs + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void advance_epoch(const DecArgs& a, unsigned long long ep) {
+  for (int j = blockIdx.x; j < kEpochSlots; j += gridDim.x)
+    __hip_atomic_store(a.epochs + j, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// gate/up role
+// ---------------------------------------------------------------------------
+template <int KBW>
+struct GuShape {
+  static constexpr int KPM = 4 * kWaves * KBW;  // packed rows of x staged (>= H/8)
+};
+
+constexpr int kGuScales = 4;  // scale groups a wave's k blocks can span (group size >= 4 k blocks)
+
+// One item in flight: this lane's words and the scales of the (at most four)
+// groups its wave's k blocks fall in.
+template <int KBW>
+struct GuBuf {
+  uint2 s[kGuScales];
+  uint4 w[KBW];
+};
+
+// The item's words of this lane (16 bytes = 4 adjacent columns, gate for
+// lanes 0-7 of each 16, up for 8-15) at packed rows 4kb + lq of this wave's
+// k blocks, and their group scales; scales first, so the first group end
+// does not wait for the words.  Past the last item the resource is empty:
+// the same loads return zeros without touching memory, and the number of
+// loads in flight (with it every wait count) is the same on every path.
+// Rows past H/8 read the next expert's words (or zeros past the tensor),
+// which meet x = 0.
+template <int KBW>
+__device__ __forceinline__ void gu_load(const DecArgs& a, int uexp_v, int item, int n_items, GuBuf<KBW>& b) {
+  const int lane = threadIdx.x & (kWave - 1), wave = uniform(threadIdx.x >> 6);
+  const int lq = lane >> 4, lr = lane & 15;
+  const int twoI = 2 * a.I;
+  const bool real = item < n_items;
+  const int u = real ? item / a.Tk : 0, c = real ? item - u * a.Tk : 0;
+  const int e = __builtin_amdgcn_readlane(uexp_v, u);
+  const int col = (lr < 8 ? 0 : a.I) + kCols * c + 4 * (lr & 7);
+  const int kb0 = wave * KBW;
+  const int g0 = kb0 >> a.gsh;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.gu_scales, real ? a.gus_total : 0u);
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.gu_packed, real ? a.gu_total : 0u);
+  const int so_s = real ? e * (int)a.gus_bytes : 0, so_w = real ? e * (int)a.gu_bytes : 0;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < kGuScales; ++j) {
+    const int g = min(g0 + j, a.Ggu - 1);
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)((g * twoI + col) * 2), so_s, 0);
+    b.s[j] = make_uint2(v.x, v.y);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < KBW; ++j) {
+    const uint32_t row = 4 * (kb0 + j) + lq;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, (row * twoI + col) * 4, so_w, kCpolNt);
+    b.w[j] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+struct GuLds {
+  uint4* xs;       // [kRows][KPM] x in k order (rows >= M and past the scale groups are zero)
+  float4* red;     // [kWaves][M][16] per-wave gate/up sums, 64 task columns
+  uint16_t* sact;  // [M][32] one item's activations in k order
+};
+
+// One item: gate/up product, cross-wave reduction, activation, exchange.
+template <int KBW>
+__device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, int item, const GuBuf<KBW>& b,
+                                        const GuLds& L, uint16_t* act) {
+  constexpr int KPM = GuShape<KBW>::KPM;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int lq = lane >> 4, lr = lane & 15;
+  const int u = item / a.Tk, c = item - u * a.Tk;
+  const int kb0 = wave * KBW;
+  const int kbpg_m1 = (1 << a.gsh) - 1;  // k blocks per scale group - 1
+  const uint32_t m43 = magic43();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  f32x4_t D[4] = {zf, zf, zf, zf};
+  f32x4_t Db = zf;
+  float y[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i][0] = y[i][1] = y[i][2] = y[i][3] = 0.f;
+  // rows 8-15 of the product repeat rows 0-7 (never used); x rows >= M are zero
+  const uint4* xrow = L.xs + (lr & 7) * KPM + lq;
+#pragma unroll
+  for (int j = 0; j < KBW; ++j) {
+    const int kb = kb0 + j;
+    const uint4 A = xrow[4 * kb];
+    const uint4 w = opaque(b.w[j]);
+    D[0] = mfma_bf16(A, q4_operand(w.x, m43), D[0]);
+    D[1] = mfma_bf16(A, q4_operand(w.y, m43), D[1]);
+    D[2] = mfma_bf16(A, q4_operand(w.z, m43), D[2]);
+    D[3] = mfma_bf16(A, q4_operand(w.w, m43), D[3]);
+    Db = mfma_bf16(A, bc, Db);  // -136 * sum of each row's x over the k block
+    if (((kb + 1) & kbpg_m1) == 0 || j == KBW - 1) {  // a scale group ends here
+      const int gi = min(kb >> a.gsh, a.Ggu - 1) - min(kb0 >> a.gsh, a.Ggu - 1);
+      uint2 s2 = opaque(b.s[0]);
+#pragma unroll
+      for (int q = 1; q < kGuScales; ++q)
+        if (gi == q) s2 = opaque(b.s[q]);
+      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (D[i][jj] + Db[jj]);
+        D[i] = zf;
+      }
+      Db = zf;
+    }
+  }
+  // per-wave sums of token rows 4lq+jj, task columns 4lr..4lr+3
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int row = 4 * lq + jj;
+    if (row < a.M) L.red[(wave * a.M + row) * 16 + lr] = make_float4(y[0][jj], y[1][jj], y[2][jj], y[3][jj]);
+  }
+  lds_barrier();
+  const int Iv = min(a.I, a.Gd << (a.gsh + 5));  // activations past the last down group are dropped
+  if (tid < a.M * kCols) {
+    const int t = tid >> 5, ci = tid & 31;
+    float g = 0.f, up = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) {
+      const float* r = (const float*)(L.red + (w2 * a.M + t) * 16);
+      g += r[ci];
+      up += r[32 + ci];
+    }
+    const float av = (kCols * c + ci < Iv) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
+    uint16_t bits = f32_to_bf16(av);
+    if ((bits & 0x7fffu) > 0x7f80u) bits = 0x7fc0u;  // canonical NaN: no stored zero (see header)
+    L.sact[t * kCols + (ci & ~7) + mfma_k_pos(ci & 7)] = bits;
+  }
+  lds_barrier();
+  // publish: 16 bytes per (token, 8 columns), inverted; the data is the signal
+  if (tid < a.M * 4) {
+    const int t = tid >> 2, q = tid & 3;
+    const int row = P.rowpos[u][t];
+    if (row >= 0) {
+      const uint4 v = ((const uint4*)L.sact)[t * 4 + q];
+      u32x4_t vv;
+      vv.x = ~v.x;
+      vv.y = ~v.y;
+      vv.z = ~v.z;
+      vv.w = ~v.w;
+      __builtin_amdgcn_raw_buffer_store_b128(vv, buffer_rsrc(act, kActParity),
+                                             (uint32_t)((row * a.I + kCols * c + 8 * q) * 2), 0, kCpolAgent);
+    }
+  }
+}
+
+// x rows of every token, loaded by the kernel before the routing (they do not
+// depend on it) so that their latency overlaps the router logits'; rows >= M
+// fall outside the resource and read as zero.
+template <int KBW>
+struct XRegs {
+  static constexpr int XPT = (kRows * GuShape<KBW>::KPM + kThreads - 1) / kThreads;
+  uint4 v[XPT];
+};
+template <int KBW>
+__device__ __forceinline__ void load_x(const DecArgs& a, XRegs<KBW>& x) {
+  constexpr int KPM = GuShape<KBW>::KPM;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (uint32_t)a.M * a.H * 2);
+#pragma unroll
+  for (int i = 0; i < XRegs<KBW>::XPT; ++i) {
+    const int id = threadIdx.x + i * kThreads, n = id / KPM, r = id - n * KPM;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, (uint32_t)((n * a.H + 8 * r) * 2), 0, 0);
+    x.v[i] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+}
+
+// Items it0 + K*stride, ... of this workgroup: item K from buffer `cur`, which
+// is then reloaded with item K+2 while item K+1 runs from `nxt`.  Template
+// recursion instead of a loop: a register array carried around a loop is
+// copied at the loop header, which waits for every load in flight.
+template <int KBW, int K>
+__device__ __forceinline__ void gu_items(const DecArgs& a, const DecPrologue& P, const GuLds& L, int uexp_v,
+                                         int it0, int stride, int n_items, GuBuf<KBW>& cur, GuBuf<KBW>& nxt,
+                                         uint16_t* act) {
+  if constexpr (K < kMaxItems) {
+    const int item = it0 + K * stride;
+    if (item >= n_items) return;
+    gu_item<KBW>(a, P, item, cur, L, act);
+    gu_load<KBW>(a, uexp_v, item + 2 * stride, n_items, cur);
+    gu_items<KBW, K + 1>(a, P, L, uexp_v, it0, stride, n_items, nxt, cur, act);
+  }
+}
+
+template <int KBW>
+__device__ __forceinline__ void gate_up_role(const DecArgs& a, const DecPrologue& P, char* lds, const XRegs<KBW>& xr,
+                                             int U, int n_gu, int uexp_v, uint16_t* act) {
+  constexpr int KPM = GuShape<KBW>::KPM;
+  constexpr int XPT = XRegs<KBW>::XPT;
+  const int tid = threadIdx.x;
+  GuLds L;
+  L.xs = (uint4*)lds;
+  L.red = (float4*)(lds + (size_t)kRows * KPM * 16);
+  L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
+  const int n_items = U * a.Tk;
+  const int it0 = blockIdx.x;
+  // zero past the rows that have a scale group (the reference drops them)
+  const int Kv = min(a.H >> 3, a.Ggu << (a.gsh + 2));
+  const int n_my = (n_items - it0 + n_gu - 1) / n_gu;  // items of this workgroup (>= 1)
+  // the first items' words in flight while x is staged; one and two items
+  // have paths of their own, so that no load is issued for nothing
+  GuBuf<KBW> b0, b1;
+  gu_load<KBW>(a, uexp_v, it0, n_items, b0);
+  if (n_my >= 2) gu_load<KBW>(a, uexp_v, it0 + n_gu, n_items, b1);
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int id = tid + i * kThreads;
+    if (id < kRows * KPM) {
+      const int r = id % KPM;
+      const uint4 v = mfma_k_order(xr.v[i]);
+      L.xs[id] = r < Kv ? v : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  lds_barrier();
+  if (n_my == 1) {
+    gu_item<KBW>(a, P, it0, b0, L, act);
+  } else if (n_my == 2) {
+    gu_item<KBW>(a, P, it0, b0, L, act);
+    gu_item<KBW>(a, P, it0 + n_gu, b1, L, act);
+  } else {
+    gu_items<KBW, 0>(a, P, L, uexp_v, it0, n_gu, n_items, b0, b1, act);
+    wait_vmem();  // no load left in flight at exit
+  }
+}
+
+// ---------------------------------------------------------------------------
+// down role
+// ---------------------------------------------------------------------------
+struct DnLds {
+  uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16, k order); row S is zero
+  float* abias;   // [S + 1][I/8] -136 * sum of each chunk's 8 values
+  uint32_t* dsc;  // [U][Gd][16][NU] bf16 scale pairs of each lane's columns
+  float* ored;    // [kWaves][kRows][64] per-wave output sums (aliases sact once it is consumed)
+};
+
+// LDS layout of the down role for S slots (rows), I and the scale chunks.
+struct DnLayout {
+  size_t abias, dsc, total;
+};
+__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, int nu) {
+  const size_t rows = (size_t)S + 1;
+  size_t sact = align16(rows * I * 2);
+  const size_t ored = (size_t)kWaves * kRows * 64 * 4;
+  if (sact < ored) sact = ored;
+  DnLayout l;
+  l.abias = sact;
+  l.dsc = l.abias + align16(rows * (I / 8) * 4);
+  l.total = l.dsc + align16((size_t)S * Gd * 4 * nu * 16);
+  return l;
+}
+
+template <int NU>
+struct DnWord;
+template <>
+struct DnWord<1> {
+  typedef uint2 T;
+};
+template <>
+struct DnWord<2> {
+  typedef uint4 T;
+};
+
+// Every 16-bit half non-zero.
+__device__ __forceinline__ bool chunk_ready(const uint4 v) {
+  const uint32_t a0 = min(v.x & 0xffffu, v.x >> 16), a1 = min(v.y & 0xffffu, v.y >> 16);
+  const uint32_t a2 = min(v.z & 0xffffu, v.z >> 16), a3 = min(v.w & 0xffffu, v.w >> 16);
+  return min(min(a0, a1), min(a2, a3)) != 0u;
+}
+
+// sum of the 8 values of a staged chunk (in matrix-core k order) times 128+q,
+// for one unpacked word: A.x holds (x0, x4), A.y (x2, x6), A.z (x1, x5), A.w
+// (x3, x7), the order of unpack_q4's pairs.
+__device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, float c) {
+  c = fdot2(A.x, q.p0, c);
+  c = fdot2(A.y, q.p1, c);
+  c = fdot2(A.z, q.p2, c);
+  return fdot2(A.w, q.p3, c);
+}
+
+// The k blocks of wave w: [kb_lo(w), kb_lo(w + 1)), kb_lo(w) = w * Tk / 8, so
+// a wave's blocks are contiguous (at most KPW of them) and every wave takes
+// its blocks of every expert of the batch.
+template <int NU, int KPW, int EPB>
+__device__ __forceinline__ void dn_load(const DecArgs& a, int uexp_v, int u0, int ne, int kbw0, int nkb,
+                                        uint32_t col_byte, typename DnWord<NU>::T (&dw)[EPB][KPW]) {
+  const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_packed, a.dn_total);
+  const uint32_t vbase = ((uint32_t)(4 * kbw0 + lq) * a.H) * 4 + col_byte;
+  const uint32_t vstep = (uint32_t)a.H * 16;  // 4 packed rows
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int e = 0; e < EPB; ++e) {
+    if (e >= ne) {
+      // an expert past the batch in the last straight-line block: codes 8, weight 0
+#pragma unroll
+      for (int j = 0; j < KPW; ++j) {
+        if constexpr (NU == 1) dw[e][j] = make_uint2(0x88888888u, 0x88888888u);
+        else dw[e][j] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
+      }
+    }
+    if (e < ne) {
+      const int so = __builtin_amdgcn_readlane(uexp_v, u0 + e) * (int)a.dn_bytes;
+#pragma unroll
+      for (int j = 0; j < KPW; ++j) {
+        if (j < nkb) {
+          if constexpr (NU == 1) {
+            const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, vbase + j * vstep, so, kCpolNt);
+            dw[e][j] = make_uint2(v.x, v.y);
+          } else {
+            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, vbase + j * vstep, so, kCpolNt);
+            dw[e][j] = make_uint4(v.x, v.y, v.z, v.w);
+          }
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Per-expert inputs of a wave's pairs: the LDS chunk index of each token's
+// activation at the wave's first k block (the zero row for tokens not routed
+// to the expert), the routing weights, and the scale pairs of the (at most
+// two) groups the wave's k blocks fall in.
+template <int NU, int NT>
+struct DnExpert {
+  int cb[NT];
+  float wt[NT];
+  uint32_t s1[NU], s2[NU];
+};
+template <int NU, int NT, bool MFMA>
+__device__ __forceinline__ DnExpert<NU, NT> dn_expert(const DecArgs& a, const DecPrologue& P, const DnLds& L,
+                                                      int epos_v, int tm_v, int u, bool valid, int kbw0, int g1,
+                                                      int g2) {
+  const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4, lr = lane & 15;
+  const int cps = a.I >> 3;
+  const int uc = min(u, kSlots - 1);
+  const int ep = __builtin_amdgcn_readlane(epos_v, uc);
+  const uint32_t tmk = valid ? (uint32_t)__builtin_amdgcn_readlane(tm_v, uc) : 0u;
+  DnExpert<NU, NT> x;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    // matrix cores: A row lr is token lr (rows >= M are zero); VALU: token t
+    const int tok = MFMA ? (lr & 7) : t;
+    const bool ok = (!MFMA || lr < a.M) && ((tmk >> tok) & 1u);
+    const int row = ok ? ep + __popc(tmk & ((1u << tok) - 1u)) : a.S;
+    x.cb[t] = row * cps + 4 * kbw0 + lq;
+    x.wt[t] = valid ? P.roww[uc][t] : 0.f;
+  }
+  const uint32_t* sp1 = L.dsc + ((uc * a.Gd + g1) * 16 + lr) * NU;
+  const uint32_t* sp2 = L.dsc + ((uc * a.Gd + g2) * 16 + lr) * NU;
+#pragma unroll
+  for (int i = 0; i < NU; ++i) {
+    x.s1[i] = sp1[i];
+    x.s2[i] = sp2[i];
+  }
+  return x;
+}
+
+constexpr int kDownEg = 2;  // experts per straight-line block of the down products
+
+// One or two tokens: dot products on the VALU.  Lane (lq, lr) takes columns
+// 2NU*lr + h at packed row 4kb + lq, i.e. one 8-value chunk of each token's
+// activation row; the chunk's -136 offset sum comes precomputed from LDS.
+// Experts run kDownEg at a time as straight-line code (an expert past the
+// batch reads the zero row with weight 0), each pair with its own sum so
+// that the dot chains are independent; a wave's KPW k blocks of one expert
+// read the zero row past the wave's count; the first SPLIT of them belong to
+// one scale group, the rest to the next.  The four lq lanes are added at
+// the end.
+template <int NU, int KPW, int EPB, int NT, int SPLIT>
+__device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
+                                        int tm_v, int u0, int ne, int kbw0, int nkb,
+                                        const typename DnWord<NU>::T (&dw)[EPB][KPW], float (&acc)[NT][2 * NU]) {
+  const int cps = a.I >> 3;
+  const uint32_t m43 = magic43();
+  const int g1 = min(kbw0 >> a.gsh, a.Gd - 1), g2 = min((kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
+  const int zc = a.S * cps;  // the zero row
+#pragma unroll
+  for (int e0 = 0; e0 < EPB; e0 += kDownEg) {
+    if (e0 < ne) {
+#pragma unroll
+      for (int ei = 0; ei < kDownEg; ++ei) {
+        const int e = e0 + ei;
+        if (e < EPB) {
+          const bool valid = e < ne;
+          const DnExpert<NU, NT> x = dn_expert<NU, NT, false>(a, P, L, epos_v, tm_v, u0 + e, valid, kbw0, g1, g2);
+          float d[KPW][NT][2 * NU], bsj[KPW][NT];
+#pragma unroll
+          for (int j = 0; j < KPW; ++j) {
+            const typename DnWord<NU>::T w = dw[e][j];
+            Q4Pairs q[2 * NU];
+            q[0] = unpack_q4(w.x, m43);
+            q[1] = unpack_q4(w.y, m43);
+            if constexpr (NU == 2) {
+              q[2] = unpack_q4(w.z, m43);
+              q[3] = unpack_q4(w.w, m43);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+              const int ci = j < nkb ? x.cb[t] + 4 * j : zc;
+              const uint4 A = L.sact[ci];
+              bsj[j][t] = L.abias[ci];
+#pragma unroll
+              for (int h = 0; h < 2 * NU; ++h) d[j][t][h] = dot_chunk(A, q[h], 0.f);
+            }
+          }
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            float b1 = 0.f, b2 = 0.f;
+#pragma unroll
+            for (int j = 0; j < KPW; ++j) (j < SPLIT ? b1 : b2) += bsj[j][t];
+#pragma unroll
+            for (int h = 0; h < 2 * NU; ++h) {
+              const float sa = (h & 1) ? bf16hi(x.s1[h >> 1]) : bf16lo(x.s1[h >> 1]);
+              const float sb = (h & 1) ? bf16hi(x.s2[h >> 1]) : bf16lo(x.s2[h >> 1]);
+              float v1 = b1, v2 = b2;
+#pragma unroll
+              for (int j = 0; j < KPW; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
+              float v = sa * v1;
+              if constexpr (SPLIT < KPW) v += sb * v2;
+              acc[t][h] += x.wt[t] * v;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Three tokens or more: matrix-core products, A rows = tokens (row lr is
+// token lr's chunk when lr < M and the token is routed to the expert, else
+// the zero row), B = the unpacked words (columns 2NU*lr + h), one more
+// product with a constant -136 operand for the int4 offset, accumulated per
+// scale group (the first SPLIT of the wave's k blocks, then the rest) and
+// scaled by the group scale and routing weight into acc[h] (rows 4lq + jj).
+// Experts run kDownEg at a time as straight-line code, as above.
+template <int NU, int KPW, int EPB, int SPLIT>
+__device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
+                                        int tm_v, int u0, int ne, int kbw0, int nkb,
+                                        const typename DnWord<NU>::T (&dw)[EPB][KPW], f32x4_t (&acc)[2 * NU]) {
+  const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
+  const int cps = a.I >> 3;
+  const uint32_t m43 = magic43();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  const int g1 = min(kbw0 >> a.gsh, a.Gd - 1), g2 = min((kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
+  const int zc = a.S * cps;
+#pragma unroll
+  for (int e0 = 0; e0 < EPB; e0 += kDownEg) {
+    if (e0 < ne) {
+#pragma unroll
+      for (int ei = 0; ei < kDownEg; ++ei) {
+        const int e = e0 + ei;
+        if (e < EPB) {
+          const bool valid = e < ne;
+          const DnExpert<NU, 1> x = dn_expert<NU, 1, true>(a, P, L, epos_v, tm_v, u0 + e, valid, kbw0, g1, g2);
+          const float4 wr = *(const float4*)&P.roww[min(u0 + e, kSlots - 1)][4 * (lq & 1)];
+          const float wv[4] = {valid ? wr.x : 0.f, valid ? wr.y : 0.f, valid ? wr.z : 0.f, valid ? wr.w : 0.f};
+          f32x4_t D[2][2 * NU], Db[2];
+#pragma unroll
+          for (int sgi = 0; sgi < 2; ++sgi) {
+            Db[sgi] = zf;
+#pragma unroll
+            for (int h = 0; h < 2 * NU; ++h) D[sgi][h] = zf;
+          }
+#pragma unroll
+          for (int j = 0; j < KPW; ++j) {
+            const int sgi = j < SPLIT ? 0 : 1;
+            const uint4 A = L.sact[j < nkb ? x.cb[0] + 4 * j : zc];
+            const typename DnWord<NU>::T w = dw[e][j];
+            D[sgi][0] = mfma_bf16(A, q4_operand(w.x, m43), D[sgi][0]);
+            D[sgi][1] = mfma_bf16(A, q4_operand(w.y, m43), D[sgi][1]);
+            if constexpr (NU == 2) {
+              D[sgi][2] = mfma_bf16(A, q4_operand(w.z, m43), D[sgi][2]);
+              D[sgi][3] = mfma_bf16(A, q4_operand(w.w, m43), D[sgi][3]);
+            }
+            Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
+          }
+#pragma unroll
+          for (int h = 0; h < 2 * NU; ++h) {
+            const float sa = (h & 1) ? bf16hi(x.s1[h >> 1]) : bf16lo(x.s1[h >> 1]);
+            const float sb = (h & 1) ? bf16hi(x.s2[h >> 1]) : bf16lo(x.s2[h >> 1]);
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+              float v = sa * (D[0][h][jj] + Db[0][jj]);
+              if constexpr (SPLIT < KPW) v += sb * (D[1][h][jj] + Db[1][jj]);
+              acc[h][jj] += wv[jj] * v;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// All 512 threads copy the exchange rows into LDS: thread tid owns chunks
+// tid + 512j, which the load writes straight into LDS (a wave's 64 lanes
+// fill 1 KB in lane order, no registers held); a chunk is complete when no
+// 16-bit half is zero, and is then inverted in place and its offset sum
+// stored.  Each wave repeats its incomplete chunks until none is left
+// (bounded: on timeout the status word is flagged and the wave goes on, so
+// the launch always ends).
+template <int CPT>
+__device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, const uint16_t* act, int nchunks) {
+  const int tid = threadIdx.x, wave = uniform(tid >> 6);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act, kActParity);
+  uint32_t pending = 0u;
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+    if (tid + j * kThreads < nchunks) pending |= 1u << j;
+  int spins = 0;
+  while (true) {
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      if ((pending >> j) & 1u)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(L.sact + j * kThreads + wave * kWave), 16,
+                                                 (uint32_t)(tid + j * kThreads) * 16u, 0, 0, kCpolAgent);
+    }
+    wait_vmem();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+      if ((pending >> j) & 1u) {
+        const uint4 v = L.sact[tid + j * kThreads];
+        if (chunk_ready(v)) {
+          const uint4 x = make_uint4(~v.x, ~v.y, ~v.z, ~v.w);
+          L.sact[tid + j * kThreads] = x;
+          L.abias[tid + j * kThreads] = neg_bias_136(x);
+          pending &= ~(1u << j);
+        }
+      }
+    }
+    if (__ballot(pending != 0u) == 0ull) break;
+    if (++spins >= a.spin_limit) {
+      if ((threadIdx.x & (kWave - 1)) == 0) atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(2);
+    asm volatile("" ::: "memory");  // the next poll reads memory again
+  }
+}
+
+// Down scales of the workgroup's columns for every unique expert, straight
+// into LDS: chunk ch = (u * Gd + g) * 4NU + q holds bf16 columns 8q .. 8q+7
+// of (u, g), so that chunk q of a row is u32 words 4q .. 4q+3 of the
+// [16 lanes][NU] layout (lane lr's NU words = columns 2NU*lr .. 2NU*lr +
+// 2NU - 1).  Complete once the wave has waited for its loads.
+template <int NU>
+__device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int uexp_v, int U, int col0) {
+  const int tid = threadIdx.x, wave = uniform(tid >> 6);
+  constexpr int per = 4 * NU;
+  const int n = U * a.Gd * per;
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_scales, a.dsc_total);
+#pragma unroll
+  for (int j = 0; j < kScaleLoads; ++j) {
+    const int ch = tid + j * kThreads;
+    const int ug = ch / per, q = ch - ug * per;
+    const int u = ug / a.Gd, g = ug - u * a.Gd;
+    const int e = __shfl(uexp_v, min(u, kSlots - 1), kWave);
+    const uint32_t off = (uint32_t)((((size_t)e * a.Gd + g) * a.H + col0 + 8 * q) * 2);
+    if (ch < n)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)((uint4*)L.dsc + j * kThreads + wave * kWave), 16,
+                                               off, 0, 0, 0);
+  }
+}
+
+template <int NU, int MODE, int CPT>
+__device__ __forceinline__ void down_body(const DecArgs& a, const DecPrologue& P, const DnLds& L, int U, int col0,
+                                          int uexp_v, const uint16_t* act) {
+  constexpr int KPW = kDownKpw;
+  constexpr int EPB = kDownRegs / (NU * KPW);  // experts per batch of word registers
+  constexpr int NT = MODE > 0 ? MODE : 1;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int lq = lane >> 4, lr = lane & 15;
+  const int cps = a.I >> 3;
+  const int rows = P.epos[U];
+  const int epos_v = P.epos[lane];
+  const int tm_v = (int)P.tm[lane];
+  const int kbw0 = wave * a.Tk / kWaves, nkb = (wave + 1) * a.Tk / kWaves - kbw0;
+  // the zero row (absent tokens read it)
+  if (tid < cps) {
+    L.sact[a.S * cps + tid] = make_uint4(0u, 0u, 0u, 0u);
+    L.abias[a.S * cps + tid] = 0.f;
+  }
+  // previous output of this thread's (token, column), accumulate mode
+  // (read unconditionally: a load under a per-lane condition is waited for
+  // at the end of the condition)
+  constexpr int ncol = kUnitCols * NU;
+  const bool writer = tid < a.M * ncol;
+  const int wt = tid / ncol, wc = tid - wt * ncol;
+  const uint16_t old = a.out[writer ? (size_t)wt * a.H + col0 + wc : 0];
+
+  float accv[NT][2 * NU];
+  f32x4_t accm[2 * NU];
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int h = 0; h < 2 * NU; ++h) {
+    accm[h] = zf;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) accv[t][h] = 0.f;
+  }
+  const uint32_t col_byte = (uint32_t)(col0 + 2 * NU * lr) * 4u;
+  int u0 = 0;
+  bool first = true;
+  do {
+    const int ne = min(U - u0, EPB);
+    typename DnWord<NU>::T dw[EPB][KPW];
+    dn_load<NU, KPW, EPB>(a, uexp_v, u0, ne, kbw0, nkb, col_byte, dw);
+    if (first) {
+      dsc_load<NU>(a, L, uexp_v, U, col0);
+      stage_acts<CPT>(a, L, act, rows * cps);  // waits for every load of the wave
+      lds_barrier();
+      first = false;
+    }
+    // k blocks of the wave in its first scale group (a group has at least KPW blocks)
+    const int split = min(KPW, (1 << a.gsh) - (kbw0 & ((1 << a.gsh) - 1)));
+    if constexpr (MODE > 0) {
+      if (split == 1) dn_valu<NU, KPW, EPB, NT, 1>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
+      else if (split == 2) dn_valu<NU, KPW, EPB, NT, 2>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
+      else dn_valu<NU, KPW, EPB, NT, KPW>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
+    } else {
+      if (split == 1) dn_mfma<NU, KPW, EPB, 1>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
+      else if (split == 2) dn_mfma<NU, KPW, EPB, 2>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
+      else dn_mfma<NU, KPW, EPB, KPW>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
+    }
+    u0 += ne;
+  } while (u0 < U);
+  // fixed-order reduction over the waves (the sums alias the staged rows)
+  lds_barrier();
+  if constexpr (MODE > 0) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+      for (int h = 0; h < 2 * NU; ++h) {
+        float v = accv[t][h];
+        v += __shfl_xor(v, 16, kWave);
+        v += __shfl_xor(v, 32, kWave);
+        if (lq == 0 && t < a.M) L.ored[(wave * kRows + t) * 64 + 2 * NU * lr + h] = v;
+      }
+    }
+  } else {
+    if (lq < 2) {
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int row = 4 * lq + jj;
+        if (row < a.M) {
+#pragma unroll
+          for (int h = 0; h < 2 * NU; ++h) L.ored[(wave * kRows + row) * 64 + 2 * NU * lr + h] = accm[h][jj];
+        }
+      }
+    }
+  }
+  lds_barrier();
+  if (writer) {
+    float s = 0.f;
+#pragma unroll
+    for (int w2 = 0; w2 < kWaves; ++w2) s += L.ored[(w2 * kRows + wt) * 64 + wc];
+    if (!a.overwrite) s += bf16_to_f32(old);
+    a.out[(size_t)wt * a.H + col0 + wc] = f32_to_bf16(s);
+  }
+}
+
+// Share `part` of `parts` of the next launch's exchange buffer, cleared.
+__device__ __forceinline__ void clear_share(uint16_t* act_next, int part, int parts) {
+  const int nch = (int)(kActParity / 16);
+  const int per = (nch + parts - 1) / parts;
+  const __amdgpu_buffer_rsrc_t nx = buffer_rsrc(act_next, kActParity);
+  const u32x4_t z = {0u, 0u, 0u, 0u};
+  for (int i = threadIdx.x; i < per; i += kThreads) {
+    const int ch = part * per + i;
+    if (ch < nch) __builtin_amdgcn_raw_buffer_store_b128(z, nx, (uint32_t)ch * 16u, 0, kCpolAgent);
+  }
+}
+
+template <int NUMAX, int MODE, int CPT>
+__device__ __forceinline__ void down_role(const DecArgs& a, const DecPrologue& P, char* lds, int U, int d, int n_dn,
+                                          int uexp_v, const uint16_t* act, uint16_t* act_next) {
+  const int unit0 = (int)((long long)d * a.units / n_dn);
+  const int nu = (int)((long long)(d + 1) * a.units / n_dn) - unit0;  // 1 or 2
+  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, NUMAX);
+  DnLds L;
+  L.sact = (uint4*)lds;
+  L.ored = (float*)lds;
+  L.abias = (float*)(lds + ly.abias);
+  L.dsc = (uint32_t*)(lds + ly.dsc);
+  clear_share(act_next, d, n_dn);
+  if (NUMAX == 2 && nu == 2) down_body<NUMAX, MODE, CPT>(a, P, L, U, kUnitCols * unit0, uexp_v, act);
+  else down_body<1, MODE, CPT>(a, P, L, U, kUnitCols * unit0, uexp_v, act);
+}
+
+// ---------------------------------------------------------------------------
+// kernel
+// ---------------------------------------------------------------------------
+template <int KBW, int NUMAX, int MODE, int CPT>
+__global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
+  __shared__ DecPrologue P;
+  extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
+  // the epoch word and x go out first: neither depends on the routing
+  // (every lane reads the word: a load under a per-lane condition would be
+  // waited for at the end of the condition)
+  const unsigned long long ep = load_epoch(a) + 1;
+  XRegs<KBW> xr;
+  load_x<KBW>(a, xr);
+  dec_prologue(a, P);
+  if (threadIdx.x == 0) advance_epoch(a, ep);
+  const int parity = (int)(ep & 1ull);
+  uint16_t* act = a.act + (size_t)parity * (kActParity / 2);
+  uint16_t* act_next = a.act + (size_t)(parity ^ 1) * (kActParity / 2);
+  const int U = uniform(P.n_unique);
+  const int b = blockIdx.x;
+  if (U == 0) {
+    // no valid slot: a layer call still owns (overwrites) out
+    if (a.overwrite)
+      for (int i = b * kThreads + threadIdx.x; i < a.M * a.H; i += gridDim.x * kThreads) a.out[i] = 0;
+    clear_share(act_next, b, gridDim.x);
+    return;
+  }
+  const int n_gu = a.n_gu[U], n_dn = a.n_dn[U];
+  const int uexp_v = P.uexp[threadIdx.x & (kWave - 1)];
+  if (b < n_gu) gate_up_role<KBW>(a, P, dyn_lds, xr, U, n_gu, uexp_v, act);
+  else if (b < n_gu + n_dn) down_role<NUMAX, MODE, CPT>(a, P, dyn_lds, U, b - n_gu, n_dn, uexp_v, act, act_next);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+constexpr size_t kMaxDynLds = 160 * 1024 - 8 * 1024;  // room for the static prologue
+
+template <int KBW>
+size_t gu_lds_bytes() {
+  return (size_t)kRows * GuShape<KBW>::KPM * 16 + (size_t)kWaves * kRows * 16 * 16 + (size_t)kRows * kCols * 2;
+}
+
+int kbw_for(int H) { return H <= 512 ? 2 : 11; }
+
+size_t lds_for(int kbw, int S, int I, int Gd, int nu) {
+  const size_t g = kbw == 2 ? gu_lds_bytes<2>() : gu_lds_bytes<11>();
+  const size_t d = dn_layout(S, I, Gd, nu).total;
+  return g > d ? g : d;
+}
+
+template <int KBW, int NUMAX, int MODE, int CPT>
+int launch_variant(const DecArgs& k, size_t lds, int grid, hipStream_t stream) {
+  static bool attr_set[64];
+  int dev = 0;
+  hipError_t e0 = hipGetDevice(&dev);
+  if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
+  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+    e0 = hipFuncSetAttribute((const void*)moe_decode_kernel<KBW, NUMAX, MODE, CPT>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
+    if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
+    attr_set[dev] = true;
+  }
+  hipLaunchKernelGGL((moe_decode_kernel<KBW, NUMAX, MODE, CPT>), dim3(grid), dim3(kThreads), lds, stream, k);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");
+  return GI_OK;
+}
+
+// Role split for every unique-expert count U: the down workgroups own one or
+// two 32-column units (all U experts, whole k), the gate/up workgroups the
+// U*Tk items; the split minimises the largest weight byte count of one
+// workgroup, with a small extra charge on gate/up bytes (a late item delays
+// every down workgroup by one exchange).
+struct DecodePlan {
+  int grid, nu_max, max_items, cpt;
+  uint16_t n_gu[kSlots + 1], n_dn[kSlots + 1];
+};
+bool decode_plan(int S, int H, int I, int cus, DecodePlan& pl) {
+  const int units = H / kUnitCols, tk = I / kCols;
+  const int G = cus < kEpochSlots ? cus : kEpochSlots;
+  const double item_bytes = (double)H * 32.0;  // 64 columns of int4 over H
+  const double xchg = 16.0 * 1024.0;
+  pl.grid = 1;
+  pl.nu_max = 1;
+  pl.max_items = 0;
+  pl.n_gu[0] = pl.n_dn[0] = 0;
+  for (int U = 1; U <= kSlots; ++U) {
+    const int Uc = U <= S ? U : S;
+    const long long items = (long long)Uc * tk;
+    const double unit_bytes = 16.0 * Uc * I;
+    int best_gu = -1, best_dn = -1;
+    double best = 0.0;
+    // two units per down workgroup only for launches of at most 8 slots
+    const int hi = units < G - 1 ? units : G - 1, lo = S <= kRows ? (units + 1) / 2 : hi;
+    for (int n_dn = hi; n_dn >= lo; --n_dn) {  // ties: more down workgroups
+      long long n_gu = G - n_dn;
+      if (n_gu > items) n_gu = items;
+      if (n_gu < 1) continue;
+      const long long per_gu = (items + n_gu - 1) / n_gu;
+      if (per_gu > kMaxItems) continue;
+      const int per_dn = (units + n_dn - 1) / n_dn;
+      const double gu_cost = per_gu * item_bytes + xchg, dn_cost = per_dn * unit_bytes;
+      const double cost = gu_cost > dn_cost ? gu_cost : dn_cost;
+      if (best_gu < 0 || cost < best) {
+        best = cost;
+        best_gu = (int)n_gu;
+        best_dn = n_dn;
+      }
+    }
+    if (best_gu < 0) return false;
+    pl.n_gu[U] = (uint16_t)best_gu;
+    pl.n_dn[U] = (uint16_t)best_dn;
+    if (U <= S) {
+      if (best_gu + best_dn > pl.grid) pl.grid = best_gu + best_dn;
+      const int per_dn = (units + best_dn - 1) / best_dn;
+      if (per_dn > pl.nu_max) pl.nu_max = per_dn;
+      const int per_gu = (int)((items + best_gu - 1) / best_gu);
+      if (per_gu > pl.max_items) pl.max_items = per_gu;
+    }
+  }
+  const int chunks = S * (I / 8);
+  pl.cpt = (chunks + kThreads - 1) / kThreads;
+  return pl.nu_max <= 2 && pl.cpt <= kMaxStage;
+}
+
+// Variants: one token (VALU down products, two units per down workgroup
+// when the launch has at most 8 slots), two tokens (VALU), three or more
+// (matrix cores).
+template <int KBW>
+int launch_plan(const DecArgs& k, const DecodePlan& pl, hipStream_t stream) {
+  const size_t lds = lds_for(KBW, k.S, k.I, k.Gd, pl.nu_max);
+  if (k.M == 1 && pl.nu_max == 2) return launch_variant<KBW, 2, 1, 2>(k, lds, pl.grid, stream);
+  if (k.M == 1) return launch_variant<KBW, 1, 1, kMaxStage>(k, lds, pl.grid, stream);
+  if (k.M == 2) return launch_variant<KBW, 1, 2, kMaxStage>(k, lds, pl.grid, stream);
+  return launch_variant<KBW, 1, 0, kMaxStage>(k, lds, pl.grid, stream);
+}
+
+int log2_exact(int v) {
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return (1 << s) == v ? s : -1;
+}
+
+}  // namespace
+
+int moe_decode_rows_per_launch(int top_k) {
+  if (top_k <= 0 || top_k > kSlots) return 0;
+  const int r = kSlots / top_k;
+  return r < kRows ? r : kRows;
+}
+
+bool moe_decode_supported(const MoeHostArgs& h) {
+  if (h.H % 32 || h.I % 32 || h.H > 2816 || h.I > kMaxI) return false;
+  if (h.gs % 32 || log2_exact(h.gs / 32) < 0) return false;
+  // a scale group covers at least 4 k blocks: a wave's gate/up blocks span at
+  // most four groups, its down blocks (at most three) at most two
+  if (log2_exact(h.gs / 32) < 2) return false;
+  if ((((uintptr_t)h.gu_scales) | ((uintptr_t)h.d_scales) | ((uintptr_t)h.out)) % 16) return false;
+  if (h.top_k > kSlots || (h.logits && h.top_k > 64) || h.E > kRouteMaxExperts) return false;
+  // whole tensors addressed with 32-bit buffer offsets
+  if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 >= (1LL << 32)) return false;
+  if ((long long)h.E * (h.I / 8) * h.H * 4 >= (1LL << 32)) return false;
+  if ((long long)h.E * h.Gd * h.H * 2 >= (1LL << 32)) return false;
+  const int rows = moe_decode_rows_per_launch(h.top_k);
+  if (rows < 1) return false;
+  const int r1 = h.M < rows ? h.M : rows, S = r1 * h.top_k;
+  DecodePlan pl;
+  if (!decode_plan(S, h.H, h.I, device_cu_count(), pl)) return false;
+  // two units per down workgroup only where a kernel variant has them
+  if (pl.nu_max == 2 && (r1 != 1 || S * (h.I / 8) > 2 * kThreads)) return false;
+  // down scales of the unique experts fit the fixed loads
+  if ((long long)S * h.Gd * 4 * pl.nu_max > (long long)kScaleLoads * kThreads) return false;
+  return lds_for(kbw_for(h.H), S, h.I, h.Gd, pl.nu_max) <= kMaxDynLds;
+}
+
+size_t moe_decode_state_bytes() { return (size_t)kEpochSlots * 8 + 2 * kActParity; }
+
+int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
+  const int rows_per = moe_decode_rows_per_launch(h.top_k);
+  DecArgs k{};
+  k.gu_packed = h.gu_packed;
+  k.gu_scales = (const uint16_t*)h.gu_scales;
+  k.d_packed = h.d_packed;
+  k.d_scales = (const uint16_t*)h.d_scales;
+  k.logits_dtype = h.logits_dtype;
+  k.expert_scale = h.expert_scale;
+  k.idx_is64 = h.idx_is64;
+  k.w_dtype = h.w_dtype;
+  k.H = h.H;
+  k.I = h.I;
+  k.E = h.E;
+  k.top_k = h.top_k;
+  k.gsh = log2_exact(h.gs / 32);
+  k.Ggu = h.Ggu;
+  k.Gd = h.Gd;
+  k.Tk = h.I / kCols;
+  k.units = h.H / kUnitCols;
+  k.gu_bytes = (uint32_t)((h.H / 8) * 2 * h.I * 4);
+  k.gus_bytes = (uint32_t)(h.Ggu * 2 * h.I * 2);
+  k.dn_bytes = (uint32_t)((h.I / 8) * h.H * 4);
+  k.gu_total = (uint32_t)((size_t)h.E * k.gu_bytes);
+  k.gus_total = (uint32_t)((size_t)h.E * k.gus_bytes);
+  k.dn_total = (uint32_t)((size_t)h.E * k.dn_bytes);
+  k.dsc_total = (uint32_t)((size_t)h.E * h.Gd * h.H * 2);
+  k.overwrite = h.overwrite;
+  k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
+  k.status = status;
+  k.epochs = (unsigned long long*)state;
+  k.act = (uint16_t*)((char*)state + (size_t)kEpochSlots * 8);
+
+  const int kbw = kbw_for(h.H);
+  const int cus = device_cu_count();
+  const size_t idx_es = h.idx_is64 ? 8 : 4;
+  const size_t w_es = h.w_dtype == GI_DTYPE_FP32 ? 4 : 2;
+  for (int r0 = 0; r0 < h.M; r0 += rows_per) {
+    const int rows = (h.M - r0) < rows_per ? (h.M - r0) : rows_per;
+    k.M = rows;
+    k.S = rows * h.top_k;
+    DecodePlan pl;
+    if (!decode_plan(k.S, h.H, h.I, cus, pl)) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: no role split");
+    for (int u = 0; u <= kSlots; ++u) {
+      k.n_gu[u] = pl.n_gu[u];
+      k.n_dn[u] = pl.n_dn[u];
+    }
+    k.x = (const uint16_t*)h.x + (size_t)r0 * h.H;
+    k.out = (uint16_t*)h.out + (size_t)r0 * h.H;
+    k.idx = h.idx ? (const char*)h.idx + (size_t)r0 * h.top_k * idx_es : nullptr;
+    k.w = h.w ? (const char*)h.w + (size_t)r0 * h.top_k * w_es : nullptr;
+    k.logits = h.logits ? (const char*)h.logits + (size_t)r0 * h.E * (h.logits_dtype == GI_DTYPE_FP32 ? 4 : 2)
+                        : nullptr;
+    k.out_idx = h.out_idx ? h.out_idx + (size_t)r0 * h.top_k : nullptr;
+    k.out_w = h.out_w ? (uint16_t*)h.out_w + (size_t)r0 * h.top_k : nullptr;
+    const int st = kbw == 2 ? launch_plan<2>(k, pl, h.stream) : launch_plan<11>(k, pl, h.stream);
+    if (st != GI_OK) return st;
+  }
+  return GI_OK;
+}
+
+}  // namespace gi

@@ -40,10 +40,13 @@
 #include "../../include/gemmainfer_amd.h"
 #include "gi_common.h"
 #include "gi_internal.h"
+#include "moe_shared.h"
 
 namespace gi {
 
 namespace {
+
+using namespace moe;
 
 constexpr int kMaxSlots = 256;
 constexpr int kMaxExperts = 1024;
@@ -103,95 +106,6 @@ struct Prologue {
   int n_list;
 };
 
-// ---------------------------------------------------------------------------
-// routing
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint32_t orderable_key(float f) {
-  const uint32_t u = __float_as_uint(f);
-  if (f != f) return 0xffffffffu;  // NaN ranks above every number
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float key_value(uint32_t k) {
-  if (k == 0xffffffffu) return __uint_as_float(0x7fc00000u);
-  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-
-__device__ __forceinline__ uint32_t umax(uint32_t a, uint32_t b) { return a > b ? a : b; }
-
-// Maximum over the wave: DPP inside each 16-lane row (quad swaps, half-row
-// and row mirrors), then the four row results through readlane.
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad_perm [1,0,3,2]
-  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad_perm [2,3,0,1]
-  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));  // row_half_mirror
-  v = umax(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));  // row_mirror
-  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
-  return umax(umax(r0, r1), umax(r2, r3));
-}
-
-// Top-k + softmax of token t by one wave (gemma.py:77-80).  Lane l holds the
-// keys of experts l, l+64, ...  Each round takes the wave maximum of the keys
-// and, among equal keys, the lowest expert index (first set ballot bit in the
-// lowest register), then retires it (key 0; every real value has a non-zero
-// key).  Lane r < top_k ends with the r-th expert and its weight.
-template <int VPL>
-__device__ __forceinline__ void route_token(const Args& a, int t, int lane, int* idx_out,
-                                            float* w_out) {
-  uint32_t keys[VPL];
-  const size_t base = (size_t)t * a.E;
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int e = lane + v * kWave;
-    uint32_t k = 0;
-    if (e < a.E) {
-      const float f = a.logits_dtype == GI_DTYPE_BF16
-                          ? bf16_to_f32(((const uint16_t*)a.logits)[base + e])
-                          : ((const float*)a.logits)[base + e];
-      k = orderable_key(f);
-    }
-    keys[v] = k;
-  }
-  int my_idx = 0;
-  float my_val = 0.f;
-  for (int r = 0; r < a.top_k; ++r) {
-    uint32_t lm = keys[0];
-#pragma unroll
-    for (int v = 1; v < VPL; ++v) lm = umax(lm, keys[v]);
-    const uint32_t m = wave_max_u32(lm);
-    int win = -1;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const unsigned long long b = __ballot(keys[v] == m);
-      if (win < 0 && b) win = v * kWave + (int)__builtin_ctzll(b);
-    }
-#pragma unroll
-    for (int v = 0; v < VPL; ++v)
-      if (lane + v * kWave == win) keys[v] = 0u;
-    if (lane == r) {
-      my_idx = win;
-      my_val = key_value(m);
-    }
-  }
-  const float vmax = __shfl(my_val, 0, kWave);
-  const float ex = lane < a.top_k ? expf(my_val - vmax) : 0.f;
-  float sum = ex;
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-  if (lane < a.top_k) {
-    float p = ex / sum;
-    if (a.expert_scale) p *= a.expert_scale[my_idx];
-    idx_out[lane] = my_idx;
-    w_out[lane] = p;
-  }
-}
-
-__device__ __forceinline__ void route_token_any(const Args& a, int t, int lane, int* idx_out,
-                                                float* w_out) {
-  if (a.E <= 2 * kWave) route_token<2>(a, t, lane, idx_out, w_out);
-  else if (a.E <= 4 * kWave) route_token<4>(a, t, lane, idx_out, w_out);
-  else route_token<kMaxExperts / kWave>(a, t, lane, idx_out, w_out);
-}
 
 // Token-Union alignment of up to 64 slots by one wave, without LDS atomics
 // or barriers: lane s holds slot s's expert id; each round takes the lowest
@@ -736,30 +650,12 @@ __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
 //            64-column output groups [w*DGW, (w+1)*DGW), one word quad per
 //            lane and group, the scale of the task's (single) group.
 // ---------------------------------------------------------------------------
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaThreads = 512;
 constexpr int kMfmaWaves = kMfmaThreads / kWave;
 constexpr int kResidentTokens = 8;   // x rows staged in LDS by the prologue
 constexpr int kChunkRows = 16;       // slots per MFMA pass
-constexpr uint32_t kNeg136Pair = 0xC308C308u;  // bf16 -136, twice
 
-__device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-// 8 bf16 values in the k order of an unpacked word: (0,4) (2,6) (1,5) (3,7)
-__device__ __forceinline__ uint4 mfma_k_order(uint4 d) {
-  const uint4 p = pair_permute(d);
-  return make_uint4(p.x, p.z, p.y, p.w);
-}
-__device__ __forceinline__ uint4 q4_operand(uint32_t w, uint32_t m43) {
-  const Q4Pairs q = unpack_q4(w, m43);
-  return make_uint4(q.p0, q.p1, q.p2, q.p3);
-}
-// position of element p (0..7) of a packed row in that order
-__device__ __forceinline__ int mfma_k_pos(int p) { return (p & 1) * 4 + (p & 2) + (p >> 2); }
 
 template <int KBW, int DGW>
 struct MfmaLds {
@@ -1055,8 +951,10 @@ __global__ __launch_bounds__(256) void route_kernel(Args a, int32_t* out_idx, vo
 constexpr size_t kAlign = 256;
 inline size_t round_up(size_t v, size_t a = kAlign) { return (v + a - 1) / a * a; }
 
+// status word | decode-kernel state (epochs, exchange buffers; fixed offset,
+// kept between calls) | barrier counters | partial slabs
 struct WsLayout {
-  size_t status, ctr, part, total;
+  size_t status, state, ctr, part, total;
 };
 
 // Intermediate columns per task.  32 columns (512-thread workgroups) beat 16
@@ -1068,8 +966,9 @@ int tiles_per_expert(int I, int cg) { return (I + cg - 1) / cg; }
 WsLayout ws_layout(int S, int H, int I, int cg) {
   WsLayout L;
   L.status = 0;
-  L.ctr = kAlign;
-  L.part = kAlign + round_up((size_t)3 * kCtrStride * sizeof(int));
+  L.state = kAlign;
+  L.ctr = L.state + round_up(moe_decode_state_bytes());
+  L.part = L.ctr + round_up((size_t)3 * kCtrStride * sizeof(int));
   L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
   return L;
 }
@@ -1232,6 +1131,13 @@ int launch_fused_moe(const MoeHostArgs& h) {
                 "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
   if (((uintptr_t)h.workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
+  if (moe_decode_supported(h)) {
+    // the same layout as the size query (gi_fused_moe_workspace_bytes)
+    const int per = moe_rows_per_launch(h.top_k);
+    const WsLayout L = ws_layout((h.M < per ? h.M : per) * h.top_k, h.H, h.I, kTaskCols);
+    char* ws0 = (char*)h.workspace;
+    return launch_moe_decode(h, ws0 + L.state, (int*)(ws0 + L.status));
+  }
 
   char* ws = (char*)h.workspace;
   Args k{};
