@@ -119,6 +119,7 @@ struct DecArgs {
   unsigned long long* epochs;  // [kEpochSlots]
   uint16_t* act;               // [2][kSlots][I] (parity stride kActParity bytes): rows in expert
                                // order, inverted bf16, matrix-core k order
+  float* part;                 // [2][units][kPartSlots][kRows][32] partial sums, inverted bits
   int* status;
   uint32_t gu_bytes, gus_bytes, dn_bytes;  // one expert's packed gate/up, its scales, packed down
   uint32_t gu_total, gus_total, dn_total;  // whole tensors (buffer resource sizes)
@@ -129,8 +130,6 @@ struct DecArgs {
   int Tk;       // I / 32: items per expert, k blocks of the down projection
   int units;    // H / 32 column units of the down projection
   int overwrite, spin_limit;
-  uint16_t n_gu[kSlots + 1];  // gate/up workgroups when the launch has U unique experts
-  uint16_t n_dn[kSlots + 1];  // down workgroups for U
 };
 
 struct DecPrologue {
@@ -440,26 +439,15 @@ __device__ __forceinline__ void gu_items(const DecArgs& a, const DecPrologue& P,
   }
 }
 
+// x of every token into LDS in the matrix-core k order (rows >= M and
+// packed rows past the gate/up scale groups are zero: the reference drops
+// them).
 template <int KBW>
-__device__ __forceinline__ void gate_up_role(const DecArgs& a, const DecPrologue& P, char* lds, const XRegs<KBW>& xr,
-                                             int U, int n_gu, int uexp_v, uint16_t* act) {
+__device__ __forceinline__ void stage_x(const DecArgs& a, const GuLds& L, const XRegs<KBW>& xr) {
   constexpr int KPM = GuShape<KBW>::KPM;
   constexpr int XPT = XRegs<KBW>::XPT;
   const int tid = threadIdx.x;
-  GuLds L;
-  L.xs = (uint4*)lds;
-  L.red = (float4*)(lds + (size_t)kRows * KPM * 16);
-  L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
-  const int n_items = U * a.Tk;
-  const int it0 = blockIdx.x;
-  // zero past the rows that have a scale group (the reference drops them)
   const int Kv = min(a.H >> 3, a.Ggu << (a.gsh + 2));
-  const int n_my = (n_items - it0 + n_gu - 1) / n_gu;  // items of this workgroup (>= 1)
-  // the first items' words in flight while x is staged; one and two items
-  // have paths of their own, so that no load is issued for nothing
-  GuBuf<KBW> b0, b1;
-  gu_load<KBW>(a, uexp_v, it0, n_items, b0);
-  if (n_my >= 2) gu_load<KBW>(a, uexp_v, it0 + n_gu, n_items, b1);
 #pragma unroll
   for (int i = 0; i < XPT; ++i) {
     const int id = tid + i * kThreads;
@@ -470,53 +458,46 @@ __device__ __forceinline__ void gate_up_role(const DecArgs& a, const DecPrologue
     }
   }
   lds_barrier();
-  if (n_my == 1) {
-    gu_item<KBW>(a, P, it0, b0, L, act);
-  } else if (n_my == 2) {
-    gu_item<KBW>(a, P, it0, b0, L, act);
-    gu_item<KBW>(a, P, it0 + n_gu, b1, L, act);
-  } else {
-    gu_items<KBW, 0>(a, P, L, uexp_v, it0, n_gu, n_items, b0, b1, act);
-    wait_vmem();  // no load left in flight at exit
-  }
 }
 
 // ---------------------------------------------------------------------------
-// down role
+// down projection: blocks (unit d, unique expert u), b = d * U + u
 // ---------------------------------------------------------------------------
+constexpr int kMaxUnits = 88;          // H <= 2816
+constexpr int kPartSlots = 8;          // workgroups sharing one unit
+constexpr size_t kPartParity = (size_t)kMaxUnits * kPartSlots * kRows * kUnitCols * 4;  // bytes
+
+// Workgroup w owns blocks [blk_lo(w), blk_lo(w + 1)); the workgroup holding
+// block b is the largest w with blk_lo(w) <= b.
+__host__ __device__ inline int blk_lo(int w, int NB, int G) { return (int)((long long)w * NB / G); }
+__host__ __device__ inline int blk_owner(int b, int NB, int G) {
+  return (int)(((long long)(b + 1) * G - 1) / NB);
+}
+
 struct DnLds {
   uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16, k order); row S is zero
   float* abias;   // [S + 1][I/8] -136 * sum of each chunk's 8 values
-  uint32_t* dsc;  // [U][Gd][16][NU] bf16 scale pairs of each lane's columns
-  float* ored;    // [kWaves][kRows][64] per-wave output sums (aliases sact once it is consumed)
+  uint32_t* dsc;  // [block of the workgroup][Gd][16] bf16 scale pairs of each lane's two columns
+  float* red;     // [2][kWaves][kRows][32] per-wave output sums (aliases sact once it is consumed)
+  float* pbuf;    // [kPartSlots][kRows][32] partial sums of a unit's other workgroups (after red)
 };
 
-// LDS layout of the down role for S slots (rows), I and the scale chunks.
+// LDS layout of the down phase.
 struct DnLayout {
   size_t abias, dsc, total;
 };
-__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, int nu) {
+__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, int bpw) {
   const size_t rows = (size_t)S + 1;
   size_t sact = align16(rows * I * 2);
-  const size_t ored = (size_t)kWaves * kRows * 64 * 4;
-  if (sact < ored) sact = ored;
+  const size_t red = (size_t)2 * kWaves * kRows * 32 * 4 + (size_t)kPartSlots * kRows * 32 * 4;
+  if (sact < red) sact = red;
   DnLayout l;
   l.abias = sact;
   l.dsc = l.abias + align16(rows * (I / 8) * 4);
-  l.total = l.dsc + align16((size_t)S * Gd * 4 * nu * 16);
+  (void)bpw;
+  l.total = l.dsc + align16((size_t)S * Gd * 64);  // a workgroup holds at most U <= S blocks
   return l;
 }
-
-template <int NU>
-struct DnWord;
-template <>
-struct DnWord<1> {
-  typedef uint2 T;
-};
-template <>
-struct DnWord<2> {
-  typedef uint4 T;
-};
 
 // Every 16-bit half non-zero.
 __device__ __forceinline__ bool chunk_ready(const uint4 v) {
@@ -535,145 +516,152 @@ __device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, floa
   return fdot2(A.w, q.p3, c);
 }
 
-// The k blocks of wave w: [kb_lo(w), kb_lo(w + 1)), kb_lo(w) = w * Tk / 8, so
-// a wave's blocks are contiguous (at most KPW of them) and every wave takes
-// its blocks of every expert of the batch.
-template <int NU, int KPW, int EPB>
-__device__ __forceinline__ void dn_load(const DecArgs& a, int uexp_v, int u0, int ne, int kbw0, int nkb,
-                                        uint32_t col_byte, typename DnWord<NU>::T (&dw)[EPB][KPW]) {
-  const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
+// The workgroup's down blocks and the wave's k blocks: wave w takes blocks
+// [kb_lo(w), kb_lo(w + 1)) of the 32-k blocks, kb_lo(w) = w * Tk / 8 (at most
+// KPW), of every block of the workgroup.
+struct DnPlan {
+  int blo, nb;  // first block of the batch, blocks held in registers (<= BPW)
+  int d_a;      // unit of the batch's first block
+  int n0;       // blocks of unit d_a
+  int e_off;    // blocks of the workgroup before the batch (scales are indexed from the workgroup's first)
+  int kbw0, nkb;
+};
+
+// Down words of the workgroup's blocks: lane (lq, lr) loads the 8 bytes of
+// columns 32d + 2lr, 32d + 2lr + 1 at packed row 4kb + lq for the wave's k
+// blocks.  A fixed number of loads (blocks past nb or k blocks past nkb read
+// an offset past the resource: zeros, no memory access), so that the wait
+// counts of the gate/up loads issued before them stay exact.
+template <int BPW>
+__device__ __forceinline__ void dn_load(const DecArgs& a, int uexp_v, int U, const DnPlan& dp,
+                                        uint2 (&dw)[BPW][kDownKpw]) {
+  const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4, lr = lane & 15;
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_packed, a.dn_total);
-  const uint32_t vbase = ((uint32_t)(4 * kbw0 + lq) * a.H) * 4 + col_byte;
+  const uint32_t vbase = ((uint32_t)(4 * dp.kbw0 + lq) * a.H) * 4 + (uint32_t)(2 * lr) * 4;
   const uint32_t vstep = (uint32_t)a.H * 16;  // 4 packed rows
+  int d = dp.d_a, u = dp.blo - dp.d_a * U;
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int e = 0; e < EPB; ++e) {
-    if (e >= ne) {
-      // an expert past the batch in the last straight-line block: codes 8, weight 0
+  for (int e = 0; e < BPW; ++e) {
+    const bool real = e < dp.nb;
+    const int ex = __builtin_amdgcn_readlane(uexp_v, min(u, kSlots - 1));
+    const int so = real ? ex * (int)a.dn_bytes : 0;
 #pragma unroll
-      for (int j = 0; j < KPW; ++j) {
-        if constexpr (NU == 1) dw[e][j] = make_uint2(0x88888888u, 0x88888888u);
-        else dw[e][j] = make_uint4(0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u);
-      }
+    for (int j = 0; j < kDownKpw; ++j) {
+      const uint32_t off = real && j < dp.nkb ? vbase + j * vstep + (uint32_t)(kUnitCols * d) * 4 : kOob;
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, so, kCpolNt);
+      dw[e][j] = make_uint2(v.x, v.y);
     }
-    if (e < ne) {
-      const int so = __builtin_amdgcn_readlane(uexp_v, u0 + e) * (int)a.dn_bytes;
-#pragma unroll
-      for (int j = 0; j < KPW; ++j) {
-        if (j < nkb) {
-          if constexpr (NU == 1) {
-            const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, vbase + j * vstep, so, kCpolNt);
-            dw[e][j] = make_uint2(v.x, v.y);
-          } else {
-            const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, vbase + j * vstep, so, kCpolNt);
-            dw[e][j] = make_uint4(v.x, v.y, v.z, v.w);
-          }
-        }
-      }
+    if (++u == U) {
+      u = 0;
+      ++d;
     }
   }
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Per-expert inputs of a wave's pairs: the LDS chunk index of each token's
-// activation at the wave's first k block (the zero row for tokens not routed
-// to the expert), the routing weights, and the scale pairs of the (at most
-// two) groups the wave's k blocks fall in.
-template <int NU, int NT>
-struct DnExpert {
-  int cb[NT];
+// Per-block inputs: the chunk index of each token's activation at the wave's
+// first k block (the zero row for tokens not routed to the expert), the
+// routing weights, and the scale pairs of the (at most two) groups the
+// wave's k blocks fall in.
+template <int NT>
+struct DnBlock {
+  uint32_t ci[NT];
   float wt[NT];
-  uint32_t s1[NU], s2[NU];
+  uint32_t s1, s2;
 };
-template <int NU, int NT, bool MFMA>
-__device__ __forceinline__ DnExpert<NU, NT> dn_expert(const DecArgs& a, const DecPrologue& P, const DnLds& L,
-                                                      int epos_v, int tm_v, int u, bool valid, int kbw0, int g1,
-                                                      int g2) {
+template <int NT, bool MFMA>
+__device__ __forceinline__ DnBlock<NT> dn_block(const DecArgs& a, const DecPrologue& P, const DnLds& L,
+                                                int epos_v, int tm_v, int u, int e, bool valid, int kbw0, int g1,
+                                                int g2) {
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4, lr = lane & 15;
   const int cps = a.I >> 3;
   const int uc = min(u, kSlots - 1);
   const int ep = __builtin_amdgcn_readlane(epos_v, uc);
   const uint32_t tmk = valid ? (uint32_t)__builtin_amdgcn_readlane(tm_v, uc) : 0u;
-  DnExpert<NU, NT> x;
+  DnBlock<NT> x;
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     // matrix cores: A row lr is token lr (rows >= M are zero); VALU: token t
     const int tok = MFMA ? (lr & 7) : t;
     const bool ok = (!MFMA || lr < a.M) && ((tmk >> tok) & 1u);
     const int row = ok ? ep + __popc(tmk & ((1u << tok) - 1u)) : a.S;
-    x.cb[t] = row * cps + 4 * kbw0 + lq;
+    x.ci[t] = (uint32_t)(row * cps + 4 * kbw0 + lq);
     x.wt[t] = valid ? P.roww[uc][t] : 0.f;
   }
-  const uint32_t* sp1 = L.dsc + ((uc * a.Gd + g1) * 16 + lr) * NU;
-  const uint32_t* sp2 = L.dsc + ((uc * a.Gd + g2) * 16 + lr) * NU;
-#pragma unroll
-  for (int i = 0; i < NU; ++i) {
-    x.s1[i] = sp1[i];
-    x.s2[i] = sp2[i];
-  }
+  x.s1 = L.dsc[(e * a.Gd + g1) * 16 + lr];
+  x.s2 = L.dsc[(e * a.Gd + g2) * 16 + lr];  // e counts from the workgroup's first block
   return x;
 }
 
-constexpr int kDownEg = 2;  // experts per straight-line block of the down products
+// Chunk j of a wave's k blocks (the zero row past the wave's count unless
+// every wave has KPW blocks).
+template <bool FULL>
+__device__ __forceinline__ uint32_t dn_chunk(uint32_t ci, int j, int nkb, uint32_t zc) {
+  if constexpr (FULL) return ci + 4 * j;
+  else return j < nkb ? ci + 4 * j : zc;
+}
 
-// One or two tokens: dot products on the VALU.  Lane (lq, lr) takes columns
-// 2NU*lr + h at packed row 4kb + lq, i.e. one 8-value chunk of each token's
-// activation row; the chunk's -136 offset sum comes precomputed from LDS.
-// Experts run kDownEg at a time as straight-line code (an expert past the
-// batch reads the zero row with weight 0), each pair with its own sum so
-// that the dot chains are independent; a wave's KPW k blocks of one expert
-// read the zero row past the wave's count; the first SPLIT of them belong to
-// one scale group, the rest to the next.  The four lq lanes are added at
-// the end.
-template <int NU, int KPW, int EPB, int NT, int SPLIT>
+constexpr int kDownEg = 2;  // blocks per straight-line run of the VALU down products
+
+// One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
+// workgroup (all of one unit).  Lane (lq, lr) takes columns 2lr, 2lr+1 at
+// packed row 4kb + lq, i.e. one 8-value chunk of each token's activation
+// row; the chunk's -136 offset sum comes precomputed from LDS.  Blocks run
+// kDownEg at a time as straight-line code, each pair with its own sum so that
+// the dot chains are independent; the first SPLIT of a wave's k blocks
+// belong to one scale group, the rest to the next.  The four lq lanes are
+// added at the end.
+template <int BPW, int NT, int SPLIT, bool FULL>
 __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
-                                        int tm_v, int u0, int ne, int kbw0, int nkb,
-                                        const typename DnWord<NU>::T (&dw)[EPB][KPW], float (&acc)[NT][2 * NU]) {
+                                        int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
+                                        const uint2 (&dw)[BPW][kDownKpw], float (&acc)[NT][2]) {
+  constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
   const uint32_t m43 = magic43();
-  const int g1 = min(kbw0 >> a.gsh, a.Gd - 1), g2 = min((kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
-  const int zc = a.S * cps;  // the zero row
+  const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
+  const uint32_t zc = (uint32_t)(a.S * cps);  // the zero row
+  const int u_base = dp.blo - dp.d_a * U;     // expert of block 0
 #pragma unroll
-  for (int e0 = 0; e0 < EPB; e0 += kDownEg) {
-    if (e0 < ne) {
+  for (int e0 = 0; e0 < BPW; e0 += kDownEg) {
+    if (e0 < e_hi && e0 + kDownEg > e_lo) {
 #pragma unroll
       for (int ei = 0; ei < kDownEg; ++ei) {
         const int e = e0 + ei;
-        if (e < EPB) {
-          const bool valid = e < ne;
-          const DnExpert<NU, NT> x = dn_expert<NU, NT, false>(a, P, L, epos_v, tm_v, u0 + e, valid, kbw0, g1, g2);
-          float d[KPW][NT][2 * NU], bsj[KPW][NT];
+        if (e < BPW) {
+          const bool valid = e >= e_lo && e < e_hi;
+          int u = u_base + e;
+          if (u >= U) u -= U;
+          const DnBlock<NT> x =
+              dn_block<NT, false>(a, P, L, epos_v, tm_v, u, dp.e_off + e, valid, dp.kbw0, g1, g2);
+          float d[KPW][NT][2];
 #pragma unroll
           for (int j = 0; j < KPW; ++j) {
-            const typename DnWord<NU>::T w = dw[e][j];
-            Q4Pairs q[2 * NU];
+            const uint2 w = dw[e][j];
+            Q4Pairs q[2];
             q[0] = unpack_q4(w.x, m43);
             q[1] = unpack_q4(w.y, m43);
-            if constexpr (NU == 2) {
-              q[2] = unpack_q4(w.z, m43);
-              q[3] = unpack_q4(w.w, m43);
-            }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-              const int ci = j < nkb ? x.cb[t] + 4 * j : zc;
+              const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
               const uint4 A = L.sact[ci];
-              bsj[j][t] = L.abias[ci];
+              const float b = L.abias[ci];
 #pragma unroll
-              for (int h = 0; h < 2 * NU; ++h) d[j][t][h] = dot_chunk(A, q[h], 0.f);
+              for (int h = 0; h < 2; ++h) d[j][t][h] = dot_chunk(A, q[h], b);
             }
           }
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
-            float b1 = 0.f, b2 = 0.f;
 #pragma unroll
-            for (int j = 0; j < KPW; ++j) (j < SPLIT ? b1 : b2) += bsj[j][t];
+            for (int h = 0; h < 2; ++h) {
+              const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
+              const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
+              // segment sums: k block 0 is always in the first group, block
+              // KPW-1 in the second unless SPLIT == KPW
+              float v1 = d[0][t][h], v2 = d[KPW - 1][t][h];
 #pragma unroll
-            for (int h = 0; h < 2 * NU; ++h) {
-              const float sa = (h & 1) ? bf16hi(x.s1[h >> 1]) : bf16lo(x.s1[h >> 1]);
-              const float sb = (h & 1) ? bf16hi(x.s2[h >> 1]) : bf16lo(x.s2[h >> 1]);
-              float v1 = b1, v2 = b2;
-#pragma unroll
-              for (int j = 0; j < KPW; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
+              for (int j = 1; j < KPW - 1; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
+              if constexpr (SPLIT == KPW) v1 += v2;
               float v = sa * v1;
               if constexpr (SPLIT < KPW) v += sb * v2;
               acc[t][h] += x.wt[t] * v;
@@ -687,105 +675,129 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 
 // Three tokens or more: matrix-core products, A rows = tokens (row lr is
 // token lr's chunk when lr < M and the token is routed to the expert, else
-// the zero row), B = the unpacked words (columns 2NU*lr + h), one more
-// product with a constant -136 operand for the int4 offset, accumulated per
-// scale group (the first SPLIT of the wave's k blocks, then the rest) and
-// scaled by the group scale and routing weight into acc[h] (rows 4lq + jj).
-// Experts run kDownEg at a time as straight-line code, as above.
-template <int NU, int KPW, int EPB, int SPLIT>
+// the zero row), B = the unpacked words (columns 2lr + h), one more product
+// with a constant -136 operand for the int4 offset, accumulated per scale
+// group (the first SPLIT of the wave's k blocks, then the rest) and scaled
+// by the group scale and routing weight into acc[h] (rows 4lq + jj).
+template <int BPW, int SPLIT, bool FULL>
 __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
-                                        int tm_v, int u0, int ne, int kbw0, int nkb,
-                                        const typename DnWord<NU>::T (&dw)[EPB][KPW], f32x4_t (&acc)[2 * NU]) {
+                                        int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
+                                        const uint2 (&dw)[BPW][kDownKpw], f32x4_t (&acc)[2]) {
+  constexpr int KPW = kDownKpw;
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
   const int cps = a.I >> 3;
   const uint32_t m43 = magic43();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
-  const int g1 = min(kbw0 >> a.gsh, a.Gd - 1), g2 = min((kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
-  const int zc = a.S * cps;
+  const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
+  const uint32_t zc = (uint32_t)(a.S * cps);
+  const int u_base = dp.blo - dp.d_a * U;
 #pragma unroll
-  for (int e0 = 0; e0 < EPB; e0 += kDownEg) {
-    if (e0 < ne) {
+  for (int e = 0; e < BPW; ++e) {
+    if (e >= e_lo && e < e_hi) {
+      int u = u_base + e;
+      if (u >= U) u -= U;
+      const DnBlock<1> x = dn_block<1, true>(a, P, L, epos_v, tm_v, u, dp.e_off + e, true, dp.kbw0, g1, g2);
+      const float4 wr = *(const float4*)&P.roww[u][4 * (lq & 1)];
+      const float wv[4] = {wr.x, wr.y, wr.z, wr.w};
+      f32x4_t D[2][2], Db[2];
 #pragma unroll
-      for (int ei = 0; ei < kDownEg; ++ei) {
-        const int e = e0 + ei;
-        if (e < EPB) {
-          const bool valid = e < ne;
-          const DnExpert<NU, 1> x = dn_expert<NU, 1, true>(a, P, L, epos_v, tm_v, u0 + e, valid, kbw0, g1, g2);
-          const float4 wr = *(const float4*)&P.roww[min(u0 + e, kSlots - 1)][4 * (lq & 1)];
-          const float wv[4] = {valid ? wr.x : 0.f, valid ? wr.y : 0.f, valid ? wr.z : 0.f, valid ? wr.w : 0.f};
-          f32x4_t D[2][2 * NU], Db[2];
+      for (int sgi = 0; sgi < 2; ++sgi) {
+        Db[sgi] = zf;
+        D[sgi][0] = zf;
+        D[sgi][1] = zf;
+      }
 #pragma unroll
-          for (int sgi = 0; sgi < 2; ++sgi) {
-            Db[sgi] = zf;
+      for (int j = 0; j < KPW; ++j) {
+        const int sgi = j < SPLIT ? 0 : 1;
+        const uint4 A = L.sact[dn_chunk<FULL>(x.ci[0], j, dp.nkb, zc)];
+        const uint2 w = dw[e][j];
+        D[sgi][0] = mfma_bf16(A, q4_operand(w.x, m43), D[sgi][0]);
+        D[sgi][1] = mfma_bf16(A, q4_operand(w.y, m43), D[sgi][1]);
+        Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
+      }
 #pragma unroll
-            for (int h = 0; h < 2 * NU; ++h) D[sgi][h] = zf;
-          }
+      for (int h = 0; h < 2; ++h) {
+        const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
+        const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
 #pragma unroll
-          for (int j = 0; j < KPW; ++j) {
-            const int sgi = j < SPLIT ? 0 : 1;
-            const uint4 A = L.sact[j < nkb ? x.cb[0] + 4 * j : zc];
-            const typename DnWord<NU>::T w = dw[e][j];
-            D[sgi][0] = mfma_bf16(A, q4_operand(w.x, m43), D[sgi][0]);
-            D[sgi][1] = mfma_bf16(A, q4_operand(w.y, m43), D[sgi][1]);
-            if constexpr (NU == 2) {
-              D[sgi][2] = mfma_bf16(A, q4_operand(w.z, m43), D[sgi][2]);
-              D[sgi][3] = mfma_bf16(A, q4_operand(w.w, m43), D[sgi][3]);
-            }
-            Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
-          }
-#pragma unroll
-          for (int h = 0; h < 2 * NU; ++h) {
-            const float sa = (h & 1) ? bf16hi(x.s1[h >> 1]) : bf16lo(x.s1[h >> 1]);
-            const float sb = (h & 1) ? bf16hi(x.s2[h >> 1]) : bf16lo(x.s2[h >> 1]);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-              float v = sa * (D[0][h][jj] + Db[0][jj]);
-              if constexpr (SPLIT < KPW) v += sb * (D[1][h][jj] + Db[1][jj]);
-              acc[h][jj] += wv[jj] * v;
-            }
-          }
+        for (int jj = 0; jj < 4; ++jj) {
+          float v = sa * (D[0][h][jj] + Db[0][jj]);
+          if constexpr (SPLIT < KPW) v += sb * (D[1][h][jj] + Db[1][jj]);
+          acc[h][jj] += wv[jj] * v;
         }
       }
     }
   }
 }
 
+// Blocks [e_lo, e_hi) with the wave's variant: k blocks in its first scale
+// group (1, 2 or all KPW; a group has at least KPW blocks) and whether the
+// wave has all KPW k blocks.
+template <int BPW, int MODE, int SPLIT>
+__device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
+                                             int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
+                                             const uint2 (&dw)[BPW][kDownKpw], float (&accv)[MODE > 0 ? MODE : 1][2],
+                                             f32x4_t (&accm)[2]) {
+  constexpr int NT = MODE > 0 ? MODE : 1;
+  if (dp.nkb == kDownKpw) {
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, true>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv);
+    else dn_mfma<BPW, SPLIT, true>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
+  } else {
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv);
+    else dn_mfma<BPW, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
+  }
+}
+template <int BPW, int MODE>
+__device__ __forceinline__ void dn_run(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v, int tm_v,
+                                       int U, const DnPlan& dp, int e_lo, int e_hi, const uint2 (&dw)[BPW][kDownKpw],
+                                       float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
+  const int split = min(kDownKpw, (1 << a.gsh) - (dp.kbw0 & ((1 << a.gsh) - 1)));
+  if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
+  else if (split == 2) dn_run_split<BPW, MODE, 2>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
+  else dn_run_split<BPW, MODE, kDownKpw>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
-// All 512 threads copy the exchange rows into LDS: thread tid owns chunks
-// tid + 512j, which the load writes straight into LDS (a wave's 64 lanes
-// fill 1 KB in lane order, no registers held); a chunk is complete when no
-// 16-bit half is zero, and is then inverted in place and its offset sum
-// stored.  Each wave repeats its incomplete chunks until none is left
+// All 512 threads copy exchange rows into LDS: chunks g = base + tid + 512j
+// of the rows [r0, r1) (less the rows [x0, x1), which no block of the
+// workgroup reads), written straight into LDS at their own index (a wave's
+// 64 lanes fill 1 KB in lane order, no registers held).  A chunk is complete
+// when no 16-bit half is zero, and is then inverted in place and its offset
+// sum stored.  Each wave repeats its incomplete chunks until none is left
 // (bounded: on timeout the status word is flagged and the wave goes on, so
 // the launch always ends).
 template <int CPT>
-__device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, const uint16_t* act, int nchunks) {
+__device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, const uint16_t* act, int c0, int c1,
+                                           int x0, int x1) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act, kActParity);
   uint32_t pending = 0u;
 #pragma unroll
-  for (int j = 0; j < CPT; ++j)
-    if (tid + j * kThreads < nchunks) pending |= 1u << j;
+  for (int j = 0; j < CPT; ++j) {
+    const int g = c0 + tid + j * kThreads;
+    if (g < c1 && (g < x0 || g >= x1)) pending |= 1u << j;
+  }
   int spins = 0;
   while (true) {
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       if ((pending >> j) & 1u)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(L.sact + j * kThreads + wave * kWave), 16,
-                                                 (uint32_t)(tid + j * kThreads) * 16u, 0, 0, kCpolAgent);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(L.sact + c0 + j * kThreads + wave * kWave), 16,
+                                                 (uint32_t)(c0 + tid + j * kThreads) * 16u, 0, 0, kCpolAgent);
     }
     wait_vmem();
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       if ((pending >> j) & 1u) {
-        const uint4 v = L.sact[tid + j * kThreads];
+        const int g = c0 + tid + j * kThreads;
+        const uint4 v = L.sact[g];
         if (chunk_ready(v)) {
           const uint4 x = make_uint4(~v.x, ~v.y, ~v.z, ~v.w);
-          L.sact[tid + j * kThreads] = x;
-          L.abias[tid + j * kThreads] = neg_bias_136(x);
+          L.sact[g] = x;
+          L.abias[g] = neg_bias_136(x);
           pending &= ~(1u << j);
         }
       }
@@ -800,131 +812,34 @@ __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, con
   }
 }
 
-// Down scales of the workgroup's columns for every unique expert, straight
-// into LDS: chunk ch = (u * Gd + g) * 4NU + q holds bf16 columns 8q .. 8q+7
-// of (u, g), so that chunk q of a row is u32 words 4q .. 4q+3 of the
-// [16 lanes][NU] layout (lane lr's NU words = columns 2NU*lr .. 2NU*lr +
-// 2NU - 1).  Complete once the wave has waited for its loads.
-template <int NU>
-__device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int uexp_v, int U, int col0) {
+// Down scales of the workgroup's blocks (all batches), straight into LDS: chunk ch =
+// (e * Gd + g) * 4 + q holds bf16 columns 8q .. 8q+7 of block e's unit for
+// group g, so that lane lr's pair (columns 2lr, 2lr+1) is u32 word
+// (e * Gd + g) * 16 + lr.  Complete once the wave has waited for its loads.
+__device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int uexp_v, int U, int blo, int nb) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
-  constexpr int per = 4 * NU;
-  const int n = U * a.Gd * per;
+  const int n = nb * a.Gd * 4;
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_scales, a.dsc_total);
 #pragma unroll
   for (int j = 0; j < kScaleLoads; ++j) {
     const int ch = tid + j * kThreads;
-    const int ug = ch / per, q = ch - ug * per;
-    const int u = ug / a.Gd, g = ug - u * a.Gd;
-    const int e = __shfl(uexp_v, min(u, kSlots - 1), kWave);
-    const uint32_t off = (uint32_t)((((size_t)e * a.Gd + g) * a.H + col0 + 8 * q) * 2);
+    const int eg = ch >> 2, q = ch & 3;
+    const int e = eg / a.Gd, g = eg - e * a.Gd;
+    const int b = blo + e;
+    const int d = b / U, u = b - d * U;
+    const int ex = __shfl(uexp_v, min(u, kSlots - 1), kWave);
+    const uint32_t off = (uint32_t)((((size_t)ex * a.Gd + g) * a.H + kUnitCols * d + 8 * q) * 2);
     if (ch < n)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)((uint4*)L.dsc + j * kThreads + wave * kWave), 16,
                                                off, 0, 0, 0);
   }
 }
 
-template <int NU, int MODE, int CPT>
-__device__ __forceinline__ void down_body(const DecArgs& a, const DecPrologue& P, const DnLds& L, int U, int col0,
-                                          int uexp_v, const uint16_t* act) {
-  constexpr int KPW = kDownKpw;
-  constexpr int EPB = kDownRegs / (NU * KPW);  // experts per batch of word registers
-  constexpr int NT = MODE > 0 ? MODE : 1;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
-  const int lq = lane >> 4, lr = lane & 15;
-  const int cps = a.I >> 3;
-  const int rows = P.epos[U];
-  const int epos_v = P.epos[lane];
-  const int tm_v = (int)P.tm[lane];
-  const int kbw0 = wave * a.Tk / kWaves, nkb = (wave + 1) * a.Tk / kWaves - kbw0;
-  // the zero row (absent tokens read it)
-  if (tid < cps) {
-    L.sact[a.S * cps + tid] = make_uint4(0u, 0u, 0u, 0u);
-    L.abias[a.S * cps + tid] = 0.f;
-  }
-  // previous output of this thread's (token, column), accumulate mode
-  // (read unconditionally: a load under a per-lane condition is waited for
-  // at the end of the condition)
-  constexpr int ncol = kUnitCols * NU;
-  const bool writer = tid < a.M * ncol;
-  const int wt = tid / ncol, wc = tid - wt * ncol;
-  const uint16_t old = a.out[writer ? (size_t)wt * a.H + col0 + wc : 0];
-
-  float accv[NT][2 * NU];
-  f32x4_t accm[2 * NU];
-  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int h = 0; h < 2 * NU; ++h) {
-    accm[h] = zf;
-#pragma unroll
-    for (int t = 0; t < NT; ++t) accv[t][h] = 0.f;
-  }
-  const uint32_t col_byte = (uint32_t)(col0 + 2 * NU * lr) * 4u;
-  int u0 = 0;
-  bool first = true;
-  do {
-    const int ne = min(U - u0, EPB);
-    typename DnWord<NU>::T dw[EPB][KPW];
-    dn_load<NU, KPW, EPB>(a, uexp_v, u0, ne, kbw0, nkb, col_byte, dw);
-    if (first) {
-      dsc_load<NU>(a, L, uexp_v, U, col0);
-      stage_acts<CPT>(a, L, act, rows * cps);  // waits for every load of the wave
-      lds_barrier();
-      first = false;
-    }
-    // k blocks of the wave in its first scale group (a group has at least KPW blocks)
-    const int split = min(KPW, (1 << a.gsh) - (kbw0 & ((1 << a.gsh) - 1)));
-    if constexpr (MODE > 0) {
-      if (split == 1) dn_valu<NU, KPW, EPB, NT, 1>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
-      else if (split == 2) dn_valu<NU, KPW, EPB, NT, 2>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
-      else dn_valu<NU, KPW, EPB, NT, KPW>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accv);
-    } else {
-      if (split == 1) dn_mfma<NU, KPW, EPB, 1>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
-      else if (split == 2) dn_mfma<NU, KPW, EPB, 2>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
-      else dn_mfma<NU, KPW, EPB, KPW>(a, P, L, epos_v, tm_v, u0, ne, kbw0, nkb, dw, accm);
-    }
-    u0 += ne;
-  } while (u0 < U);
-  // fixed-order reduction over the waves (the sums alias the staged rows)
-  lds_barrier();
-  if constexpr (MODE > 0) {
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-#pragma unroll
-      for (int h = 0; h < 2 * NU; ++h) {
-        float v = accv[t][h];
-        v += __shfl_xor(v, 16, kWave);
-        v += __shfl_xor(v, 32, kWave);
-        if (lq == 0 && t < a.M) L.ored[(wave * kRows + t) * 64 + 2 * NU * lr + h] = v;
-      }
-    }
-  } else {
-    if (lq < 2) {
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const int row = 4 * lq + jj;
-        if (row < a.M) {
-#pragma unroll
-          for (int h = 0; h < 2 * NU; ++h) L.ored[(wave * kRows + row) * 64 + 2 * NU * lr + h] = accm[h][jj];
-        }
-      }
-    }
-  }
-  lds_barrier();
-  if (writer) {
-    float s = 0.f;
-#pragma unroll
-    for (int w2 = 0; w2 < kWaves; ++w2) s += L.ored[(w2 * kRows + wt) * 64 + wc];
-    if (!a.overwrite) s += bf16_to_f32(old);
-    a.out[(size_t)wt * a.H + col0 + wc] = f32_to_bf16(s);
-  }
-}
-
-// Share `part` of `parts` of the next launch's exchange buffer, cleared.
-__device__ __forceinline__ void clear_share(uint16_t* act_next, int part, int parts) {
-  const int nch = (int)(kActParity / 16);
+// Share `part` of `parts` of a buffer of `bytes`, cleared.
+__device__ __forceinline__ void clear_share(void* buf, size_t bytes, int part, int parts) {
+  const int nch = (int)(bytes / 16);
   const int per = (nch + parts - 1) / parts;
-  const __amdgpu_buffer_rsrc_t nx = buffer_rsrc(act_next, kActParity);
+  const __amdgpu_buffer_rsrc_t nx = buffer_rsrc(buf, (uint32_t)bytes);
   const u32x4_t z = {0u, 0u, 0u, 0u};
   for (int i = threadIdx.x; i < per; i += kThreads) {
     const int ch = part * per + i;
@@ -932,26 +847,231 @@ __device__ __forceinline__ void clear_share(uint16_t* act_next, int part, int pa
   }
 }
 
-template <int NUMAX, int MODE, int CPT>
-__device__ __forceinline__ void down_role(const DecArgs& a, const DecPrologue& P, char* lds, int U, int d, int n_dn,
-                                          int uexp_v, const uint16_t* act, uint16_t* act_next) {
-  const int unit0 = (int)((long long)d * a.units / n_dn);
-  const int nu = (int)((long long)(d + 1) * a.units / n_dn) - unit0;  // 1 or 2
-  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, NUMAX);
+__device__ __forceinline__ uint32_t f32_signal_bits(float v) {
+  uint32_t b = __float_as_uint(v);
+  if ((b & 0x7fffffffu) > 0x7f800000u) b = 0x7fc00000u;  // canonical NaN: no stored zero
+  return ~b;
+}
+
+// The down phase of one workgroup: stage the activation rows its blocks
+// read, the products, the sums over the waves, then per unit either the
+// output (a unit held whole, or the unit's first workgroup once the others'
+// partial sums are in) or this workgroup's partial sum for the first one.
+template <int BPW, int MODE, int CPT>
+__device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& P, char* lds, int U, int uexp_v,
+                                           const uint16_t* act, float* part, int blo, int bhi, DnPlan dp,
+                                           const uint2 (&dw0)[BPW][kDownKpw]) {
+  constexpr int NT = MODE > 0 ? MODE : 1;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int lq = lane >> 4, lr = lane & 15;
+  const int cps = a.I >> 3;
+  const int G = gridDim.x, NB = a.units * U;
+  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, BPW);
   DnLds L;
   L.sact = (uint4*)lds;
-  L.ored = (float*)lds;
+  L.red = (float*)lds;
+  L.pbuf = L.red + 2 * kWaves * kRows * 32;
   L.abias = (float*)(lds + ly.abias);
   L.dsc = (uint32_t*)(lds + ly.dsc);
-  clear_share(act_next, d, n_dn);
-  if (NUMAX == 2 && nu == 2) down_body<NUMAX, MODE, CPT>(a, P, L, U, kUnitCols * unit0, uexp_v, act);
-  else down_body<1, MODE, CPT>(a, P, L, U, kUnitCols * unit0, uexp_v, act);
+  const int epos_v = P.epos[lane];
+  const int tm_v = (int)P.tm[lane];
+  const int nb_all = bhi - blo, d_first = blo / U;
+  const int n_units = (bhi - 1) / U > d_first ? 2 : 1;  // at most two: a workgroup has at most U blocks
+  // previous output of the writer thread's (token, column) of each unit
+  // (read unconditionally: a load under a per-lane condition is waited for
+  // at the end of the condition)
+  const bool writer = tid < a.M * kUnitCols;
+  const int wt = tid >> 5, wc = tid & 31;
+  uint16_t old[2];
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int d = min(d_first + p, a.units - 1);
+    old[p] = a.out[writer ? (size_t)wt * a.H + kUnitCols * d + wc : 0];
+  }
+  lds_barrier();  // the gate/up phase's LDS is free
+  // the zero row (absent tokens and missing k blocks read it)
+  if (tid < cps) {
+    L.sact[a.S * cps + tid] = make_uint4(0u, 0u, 0u, 0u);
+    L.abias[a.S * cps + tid] = 0.f;
+  }
+  dsc_load(a, L, uexp_v, U, blo, nb_all);
+  // rows of the experts the blocks read: expert u_a.. of the first unit, and
+  // 0..u_b of the second
+  const int u_a = blo - d_first * U;
+  int c0, c1, x0 = 0, x1 = 0;
+  if (n_units == 1) {
+    c0 = P.epos[u_a] * cps;
+    c1 = P.epos[u_a + nb_all] * cps;
+  } else {
+    const int u_b = bhi - 1 - (d_first + 1) * U;
+    c0 = 0;
+    c1 = P.epos[U] * cps;
+    if (u_b + 1 < u_a) {
+      x0 = P.epos[u_b + 1] * cps;
+      x1 = P.epos[u_a] * cps;
+    }
+  }
+  c0 = uniform(c0);
+  c1 = uniform(c1);
+  x0 = uniform(x0);
+  x1 = uniform(x1);
+  stage_acts<CPT>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
+  lds_barrier();
+
+  float accv[2][NT][2];
+  f32x4_t accm[2][2];
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int p = 0; p < 2; ++p)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      accm[p][h] = zf;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) accv[p][t][h] = 0.f;
+    }
+  // batch 0 from the words loaded with the gate/up items, then any further
+  // batches (more blocks than the registers hold)
+  dp.blo = blo;
+  dp.e_off = 0;
+  dp.nb = min(nb_all, BPW);
+  dp.d_a = d_first;
+  dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
+  dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, accv[0], accm[0]);
+  if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, accv[1], accm[1]);
+  for (int b0 = blo + BPW; b0 < bhi; b0 += BPW) {
+    dp.blo = b0;
+    dp.e_off = b0 - blo;
+    dp.nb = min(bhi - b0, BPW);
+    dp.d_a = b0 / U;
+    dp.n0 = max(0, min(dp.nb, (d_first + 1) * U - b0));
+    uint2 dw[BPW][kDownKpw];
+    dn_load<BPW>(a, uexp_v, U, dp, dw);
+    if (dp.n0 > 0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw, accv[1], accm[1]);
+  }
+  // sums over the waves, fixed order (the per-wave sums alias the staged rows)
+  lds_barrier();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    float* red = L.red + (size_t)p * kWaves * kRows * 32;
+    if constexpr (MODE > 0) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float v = accv[p][t][h];
+          v += __shfl_xor(v, 16, kWave);
+          v += __shfl_xor(v, 32, kWave);
+          if (lq == 0 && t < a.M) red[(wave * kRows + t) * 32 + 2 * lr + h] = v;
+        }
+      }
+    } else {
+      if (lq < 2) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int row = 4 * lq + jj;
+          if (row < a.M) {
+            red[(wave * kRows + row) * 32 + 2 * lr] = accm[p][0][jj];
+            red[(wave * kRows + row) * 32 + 2 * lr + 1] = accm[p][1][jj];
+          }
+        }
+      }
+    }
+  }
+  lds_barrier();
+  for (int p = 0; p < n_units; ++p) {
+    const int d = d_first + p;
+    const int wf = blk_owner(d * U, NB, G), wl = blk_owner(d * U + U - 1, NB, G);
+    const int ns = wl - wf + 1, slot = (int)blockIdx.x - wf;
+    float s = 0.f;
+    if (writer) {
+      const float* red = L.red + (size_t)p * kWaves * kRows * 32;
+#pragma unroll
+      for (int w2 = 0; w2 < kWaves; ++w2) s += red[(w2 * kRows + wt) * 32 + wc];
+    }
+    const __amdgpu_buffer_rsrc_t pr = buffer_rsrc(part, kPartParity);
+    if (slot > 0) {
+      // a partial sum for the unit's first workgroup: 16 bytes per (token, 4 columns)
+      if (writer) L.pbuf[wt * 32 + wc] = s;
+      lds_barrier();
+      if (tid < a.M * 8) {
+        const int t = tid >> 3, q = tid & 7;
+        const float4 v = *(const float4*)&L.pbuf[t * 32 + 4 * q];
+        u32x4_t vv;
+        vv.x = f32_signal_bits(v.x);
+        vv.y = f32_signal_bits(v.y);
+        vv.z = f32_signal_bits(v.z);
+        vv.w = f32_signal_bits(v.w);
+        __builtin_amdgcn_raw_buffer_store_b128(
+            vv, pr, (uint32_t)((((d * kPartSlots + slot) * kRows + t) * kUnitCols + 4 * q) * 4), 0, kCpolAgent);
+      }
+      lds_barrier();
+      continue;
+    }
+    if (ns > 1) {
+      // the unit's first workgroup: the others' partial sums, polled
+      const int nch = (ns - 1) * a.M * 8;
+      if (tid < nch) {
+        const int sl = 1 + tid / (a.M * 8), r = tid - (sl - 1) * a.M * 8;
+        const int t = r >> 3, q = r & 7;
+        const uint32_t off = (uint32_t)((((d * kPartSlots + sl) * kRows + t) * kUnitCols + 4 * q) * 4);
+        int spins = 0;
+        u32x4_t v;
+        while (true) {
+          v = __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, kCpolAgent);
+          if (v.x != 0u && v.y != 0u && v.z != 0u && v.w != 0u) break;
+          if (++spins >= a.spin_limit) {
+            atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+          asm volatile("" ::: "memory");
+        }
+        *(float4*)&L.pbuf[((sl - 1) * kRows + t) * 32 + 4 * q] =
+            make_float4(__uint_as_float(~v.x), __uint_as_float(~v.y), __uint_as_float(~v.z), __uint_as_float(~v.w));
+      }
+      lds_barrier();
+      if (writer)
+        for (int sl = 1; sl < ns; ++sl) s += L.pbuf[((sl - 1) * kRows + wt) * 32 + wc];
+      lds_barrier();
+    }
+    if (writer) {
+      if (!a.overwrite) s += bf16_to_f32(old[p]);
+      a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_bf16(s);
+    }
+  }
+}
+
+// The workgroup's gate/up items (it0, it0 + G, ...) and the issue of its down
+// words: the first items' words go out first, then the down words, so that
+// every wait of the gate/up products has an exact count; NI = 1 and 2 have
+// paths of their own (no load is issued for nothing), NI = 3 is the general
+// path (two items in flight, the next one loaded as each finishes), which
+// issues the down words after its items (registers: a rare case).
+template <int KBW, int NI, int BPW>
+__device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P, const GuLds& L, int U,
+                                         int uexp_v, uint16_t* act, const DnPlan& dp, int n_items,
+                                         uint2 (&dw)[BPW][kDownKpw]) {
+  const int it0 = blockIdx.x, G = gridDim.x;
+  GuBuf<KBW> b0, b1;
+  gu_load<KBW>(a, uexp_v, it0, n_items, b0);
+  if constexpr (NI >= 2) gu_load<KBW>(a, uexp_v, it0 + G, n_items, b1);
+  if constexpr (NI <= 2) dn_load<BPW>(a, uexp_v, U, dp, dw);
+  if constexpr (NI == 1) {
+    gu_item<KBW>(a, P, it0, b0, L, act);
+  } else if constexpr (NI == 2) {
+    gu_item<KBW>(a, P, it0, b0, L, act);
+    gu_item<KBW>(a, P, it0 + G, b1, L, act);
+  } else {
+    gu_items<KBW, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
+    dn_load<BPW>(a, uexp_v, U, dp, dw);
+  }
 }
 
 // ---------------------------------------------------------------------------
 // kernel
 // ---------------------------------------------------------------------------
-template <int KBW, int NUMAX, int MODE, int CPT>
+template <int KBW, int MODE, int BPW, int CPT>
 __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   __shared__ DecPrologue P;
   extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
@@ -966,19 +1086,47 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   const int parity = (int)(ep & 1ull);
   uint16_t* act = a.act + (size_t)parity * (kActParity / 2);
   uint16_t* act_next = a.act + (size_t)(parity ^ 1) * (kActParity / 2);
+  float* part = a.part + (size_t)parity * (kPartParity / 4);
+  float* part_next = a.part + (size_t)(parity ^ 1) * (kPartParity / 4);
   const int U = uniform(P.n_unique);
-  const int b = blockIdx.x;
+  const int b = blockIdx.x, G = gridDim.x;
+  // this workgroup's share of the next launch's exchange buffers
+  clear_share(act_next, kActParity, b, G);
+  clear_share(part_next, kPartParity, b, G);
   if (U == 0) {
     // no valid slot: a layer call still owns (overwrites) out
     if (a.overwrite)
-      for (int i = b * kThreads + threadIdx.x; i < a.M * a.H; i += gridDim.x * kThreads) a.out[i] = 0;
-    clear_share(act_next, b, gridDim.x);
+      for (int i = b * kThreads + threadIdx.x; i < a.M * a.H; i += G * kThreads) a.out[i] = 0;
     return;
   }
-  const int n_gu = a.n_gu[U], n_dn = a.n_dn[U];
   const int uexp_v = P.uexp[threadIdx.x & (kWave - 1)];
-  if (b < n_gu) gate_up_role<KBW>(a, P, dyn_lds, xr, U, n_gu, uexp_v, act);
-  else if (b < n_gu + n_dn) down_role<NUMAX, MODE, CPT>(a, P, dyn_lds, U, b - n_gu, n_dn, uexp_v, act, act_next);
+  const int n_items = U * a.Tk;
+  const int NB = a.units * U;
+  const int n_my = b < n_items ? (n_items - b + G - 1) / G : 0;
+  // down blocks of this workgroup, at most BPW at a time
+  const int blo = blk_lo(b, NB, G), bhi = blk_lo(b + 1, NB, G);
+  const int wave = uniform(threadIdx.x >> 6);
+  GuLds L;
+  constexpr int KPM = GuShape<KBW>::KPM;
+  L.xs = (uint4*)dyn_lds;
+  L.red = (float4*)(dyn_lds + (size_t)kRows * KPM * 16);
+  L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
+  // x into LDS first: its registers are free before the word buffers fill
+  if (n_my > 0) stage_x<KBW>(a, L, xr);
+  DnPlan dp;
+  dp.blo = blo;
+  dp.e_off = 0;
+  dp.nb = min(bhi - blo, BPW);
+  dp.d_a = blo / U;
+  dp.n0 = min(dp.nb, (dp.d_a + 1) * U - blo);
+  dp.kbw0 = wave * a.Tk / kWaves;
+  dp.nkb = (wave + 1) * a.Tk / kWaves - dp.kbw0;
+  uint2 dw[BPW][kDownKpw];
+  if (n_my == 0) dn_load<BPW>(a, uexp_v, U, dp, dw);
+  else if (n_my == 1) up_phase<KBW, 1, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  else if (n_my == 2) up_phase<KBW, 2, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  else up_phase<KBW, 3, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  if (bhi > blo) down_phase<BPW, MODE, CPT>(a, P, dyn_lds, U, uexp_v, act, part, blo, bhi, dp, dw);
 }
 
 // ---------------------------------------------------------------------------
@@ -993,97 +1141,57 @@ size_t gu_lds_bytes() {
 
 int kbw_for(int H) { return H <= 512 ? 2 : 11; }
 
-size_t lds_for(int kbw, int S, int I, int Gd, int nu) {
+size_t lds_for(int kbw, int S, int I, int Gd, int bpw) {
   const size_t g = kbw == 2 ? gu_lds_bytes<2>() : gu_lds_bytes<11>();
-  const size_t d = dn_layout(S, I, Gd, nu).total;
+  const size_t d = dn_layout(S, I, Gd, bpw).total;
   return g > d ? g : d;
 }
 
-template <int KBW, int NUMAX, int MODE, int CPT>
+template <int KBW, int MODE, int BPW, int CPT>
 int launch_variant(const DecArgs& k, size_t lds, int grid, hipStream_t stream) {
   static bool attr_set[64];
   int dev = 0;
   hipError_t e0 = hipGetDevice(&dev);
   if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
   if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    e0 = hipFuncSetAttribute((const void*)moe_decode_kernel<KBW, NUMAX, MODE, CPT>,
+    e0 = hipFuncSetAttribute((const void*)moe_decode_kernel<KBW, MODE, BPW, CPT>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
     if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((moe_decode_kernel<KBW, NUMAX, MODE, CPT>), dim3(grid), dim3(kThreads), lds, stream, k);
+  hipLaunchKernelGGL((moe_decode_kernel<KBW, MODE, BPW, CPT>), dim3(grid), dim3(kThreads), lds, stream, k);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");
   return GI_OK;
 }
 
-// Role split for every unique-expert count U: the down workgroups own one or
-// two 32-column units (all U experts, whole k), the gate/up workgroups the
-// U*Tk items; the split minimises the largest weight byte count of one
-// workgroup, with a small extra charge on gate/up bytes (a late item delays
-// every down workgroup by one exchange).
+// Grid and variant of a launch of S slots: one workgroup per CU, fewer when
+// the down units are few (at most kPartSlots workgroups share one unit), and
+// enough that no workgroup gets more than kMaxItems gate/up items.
 struct DecodePlan {
-  int grid, nu_max, max_items, cpt;
-  uint16_t n_gu[kSlots + 1], n_dn[kSlots + 1];
+  int grid, bpw, cpt, mode;
 };
-bool decode_plan(int S, int H, int I, int cus, DecodePlan& pl) {
+bool decode_plan(int M, int S, int H, int I, int cus, DecodePlan& pl) {
   const int units = H / kUnitCols, tk = I / kCols;
-  const int G = cus < kEpochSlots ? cus : kEpochSlots;
-  const double item_bytes = (double)H * 32.0;  // 64 columns of int4 over H
-  const double xchg = 16.0 * 1024.0;
-  pl.grid = 1;
-  pl.nu_max = 1;
-  pl.max_items = 0;
-  pl.n_gu[0] = pl.n_dn[0] = 0;
-  for (int U = 1; U <= kSlots; ++U) {
-    const int Uc = U <= S ? U : S;
-    const long long items = (long long)Uc * tk;
-    const double unit_bytes = 16.0 * Uc * I;
-    int best_gu = -1, best_dn = -1;
-    double best = 0.0;
-    // two units per down workgroup only for launches of at most 8 slots
-    const int hi = units < G - 1 ? units : G - 1, lo = S <= kRows ? (units + 1) / 2 : hi;
-    for (int n_dn = hi; n_dn >= lo; --n_dn) {  // ties: more down workgroups
-      long long n_gu = G - n_dn;
-      if (n_gu > items) n_gu = items;
-      if (n_gu < 1) continue;
-      const long long per_gu = (items + n_gu - 1) / n_gu;
-      if (per_gu > kMaxItems) continue;
-      const int per_dn = (units + n_dn - 1) / n_dn;
-      const double gu_cost = per_gu * item_bytes + xchg, dn_cost = per_dn * unit_bytes;
-      const double cost = gu_cost > dn_cost ? gu_cost : dn_cost;
-      if (best_gu < 0 || cost < best) {
-        best = cost;
-        best_gu = (int)n_gu;
-        best_dn = n_dn;
-      }
-    }
-    if (best_gu < 0) return false;
-    pl.n_gu[U] = (uint16_t)best_gu;
-    pl.n_dn[U] = (uint16_t)best_dn;
-    if (U <= S) {
-      if (best_gu + best_dn > pl.grid) pl.grid = best_gu + best_dn;
-      const int per_dn = (units + best_dn - 1) / best_dn;
-      if (per_dn > pl.nu_max) pl.nu_max = per_dn;
-      const int per_gu = (int)((items + best_gu - 1) / best_gu);
-      if (per_gu > pl.max_items) pl.max_items = per_gu;
-    }
-  }
-  const int chunks = S * (I / 8);
-  pl.cpt = (chunks + kThreads - 1) / kThreads;
-  return pl.nu_max <= 2 && pl.cpt <= kMaxStage;
+  // U consecutive blocks meet at most ceil(G / units) + 1 workgroups
+  int G = cus < kEpochSlots ? cus : kEpochSlots;
+  if (G > (kPartSlots - 1) * units) G = (kPartSlots - 1) * units;
+  if (G < 1 || ((long long)S * tk + G - 1) / G > kMaxItems) return false;
+  pl.grid = G;
+  pl.mode = M == 1 ? 1 : M == 2 ? 2 : 0;
+  const int max_blocks = (units * S + G - 1) / G;
+  pl.bpw = S <= kRows && max_blocks <= 4 ? 4 : 8;
+  pl.cpt = S * (I / 8) <= 2 * kThreads ? 2 : kMaxStage;
+  return true;
 }
 
-// Variants: one token (VALU down products, two units per down workgroup
-// when the launch has at most 8 slots), two tokens (VALU), three or more
-// (matrix cores).
 template <int KBW>
 int launch_plan(const DecArgs& k, const DecodePlan& pl, hipStream_t stream) {
-  const size_t lds = lds_for(KBW, k.S, k.I, k.Gd, pl.nu_max);
-  if (k.M == 1 && pl.nu_max == 2) return launch_variant<KBW, 2, 1, 2>(k, lds, pl.grid, stream);
-  if (k.M == 1) return launch_variant<KBW, 1, 1, kMaxStage>(k, lds, pl.grid, stream);
-  if (k.M == 2) return launch_variant<KBW, 1, 2, kMaxStage>(k, lds, pl.grid, stream);
-  return launch_variant<KBW, 1, 0, kMaxStage>(k, lds, pl.grid, stream);
+  const size_t lds = lds_for(KBW, k.S, k.I, k.Gd, pl.bpw);
+  if (pl.mode == 1 && pl.bpw == 4 && pl.cpt == 2) return launch_variant<KBW, 1, 4, 2>(k, lds, pl.grid, stream);
+  if (pl.mode == 1) return launch_variant<KBW, 1, 8, kMaxStage>(k, lds, pl.grid, stream);
+  if (pl.mode == 2) return launch_variant<KBW, 2, 8, kMaxStage>(k, lds, pl.grid, stream);
+  return launch_variant<KBW, 0, 8, kMaxStage>(k, lds, pl.grid, stream);
 }
 
 int log2_exact(int v) {
@@ -1101,7 +1209,7 @@ int moe_decode_rows_per_launch(int top_k) {
 }
 
 bool moe_decode_supported(const MoeHostArgs& h) {
-  if (h.H % 32 || h.I % 32 || h.H > 2816 || h.I > kMaxI) return false;
+  if (h.H % 32 || h.I % 32 || h.H > kMaxUnits * kUnitCols || h.I > kMaxI) return false;
   if (h.gs % 32 || log2_exact(h.gs / 32) < 0) return false;
   // a scale group covers at least 4 k blocks: a wave's gate/up blocks span at
   // most four groups, its down blocks (at most three) at most two
@@ -1116,15 +1224,12 @@ bool moe_decode_supported(const MoeHostArgs& h) {
   if (rows < 1) return false;
   const int r1 = h.M < rows ? h.M : rows, S = r1 * h.top_k;
   DecodePlan pl;
-  if (!decode_plan(S, h.H, h.I, device_cu_count(), pl)) return false;
-  // two units per down workgroup only where a kernel variant has them
-  if (pl.nu_max == 2 && (r1 != 1 || S * (h.I / 8) > 2 * kThreads)) return false;
-  // down scales of the unique experts fit the fixed loads
-  if ((long long)S * h.Gd * 4 * pl.nu_max > (long long)kScaleLoads * kThreads) return false;
-  return lds_for(kbw_for(h.H), S, h.I, h.Gd, pl.nu_max) <= kMaxDynLds;
+  if (!decode_plan(r1, S, h.H, h.I, device_cu_count(), pl)) return false;
+  if (pl.cpt > kMaxStage || S * (h.I / 8) > kMaxStage * kThreads) return false;
+  return lds_for(kbw_for(h.H), S, h.I, h.Gd, pl.bpw) <= kMaxDynLds;
 }
 
-size_t moe_decode_state_bytes() { return (size_t)kEpochSlots * 8 + 2 * kActParity; }
+size_t moe_decode_state_bytes() { return (size_t)kEpochSlots * 8 + 2 * kActParity + 2 * kPartParity; }
 
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   const int rows_per = moe_decode_rows_per_launch(h.top_k);
@@ -1158,6 +1263,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   k.status = status;
   k.epochs = (unsigned long long*)state;
   k.act = (uint16_t*)((char*)state + (size_t)kEpochSlots * 8);
+  k.part = (float*)((char*)state + (size_t)kEpochSlots * 8 + 2 * kActParity);
 
   const int kbw = kbw_for(h.H);
   const int cus = device_cu_count();
@@ -1168,11 +1274,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
     k.M = rows;
     k.S = rows * h.top_k;
     DecodePlan pl;
-    if (!decode_plan(k.S, h.H, h.I, cus, pl)) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: no role split");
-    for (int u = 0; u <= kSlots; ++u) {
-      k.n_gu[u] = pl.n_gu[u];
-      k.n_dn[u] = pl.n_dn[u];
-    }
+    if (!decode_plan(rows, k.S, h.H, h.I, cus, pl)) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: no grid");
     k.x = (const uint16_t*)h.x + (size_t)r0 * h.H;
     k.out = (uint16_t*)h.out + (size_t)r0 * h.H;
     k.idx = h.idx ? (const char*)h.idx + (size_t)r0 * h.top_k * idx_es : nullptr;
