@@ -469,10 +469,9 @@ constexpr size_t kPartParity = (size_t)kMaxUnits * kPartSlots * kRows * kUnitCol
 
 // Workgroup w owns blocks [blk_lo(w), blk_lo(w + 1)); the workgroup holding
 // block b is the largest w with blk_lo(w) <= b.
-__host__ __device__ inline int blk_lo(int w, int NB, int G) { return (int)((long long)w * NB / G); }
-__host__ __device__ inline int blk_owner(int b, int NB, int G) {
-  return (int)(((long long)(b + 1) * G - 1) / NB);
-}
+// (products stay below 2^31: w, G <= 1024, NB <= 88 * 64)
+__host__ __device__ inline int blk_lo(int w, int NB, int G) { return w * NB / G; }
+__host__ __device__ inline int blk_owner(int b, int NB, int G) { return ((b + 1) * G - 1) / NB; }
 
 struct DnLds {
   uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16, k order); row S is zero
@@ -604,6 +603,20 @@ __device__ __forceinline__ uint32_t dn_chunk(uint32_t ci, int j, int nkb, uint32
 
 constexpr int kDownEg = 2;  // blocks per straight-line run of the VALU down products
 
+// A down word (columns 2lr, 2lr+1) as the products take it: packed (unpacked
+// where it is used) or already unpacked into bf16 pairs 128 + q.
+struct DnQ {
+  Q4Pairs q[2];
+};
+__device__ __forceinline__ void dn_unpack(const uint2 w, uint32_t m43, Q4Pairs (&q)[2]) {
+  q[0] = unpack_q4(w.x, m43);
+  q[1] = unpack_q4(w.y, m43);
+}
+__device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2]) {
+  q[0] = w.q[0];
+  q[1] = w.q[1];
+}
+
 // One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
 // workgroup (all of one unit).  Lane (lq, lr) takes columns 2lr, 2lr+1 at
 // packed row 4kb + lq, i.e. one 8-value chunk of each token's activation
@@ -612,10 +625,10 @@ constexpr int kDownEg = 2;  // blocks per straight-line run of the VALU down pro
 // the dot chains are independent; the first SPLIT of a wave's k blocks
 // belong to one scale group, the rest to the next.  The four lq lanes are
 // added at the end.
-template <int BPW, int NT, int SPLIT, bool FULL>
+template <int BPW, int NT, int SPLIT, bool FULL, class W>
 __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                         int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                        const uint2 (&dw)[BPW][kDownKpw], float (&acc)[NT][2]) {
+                                        const W (&dw)[BPW][kDownKpw], float (&acc)[NT][2]) {
   constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
   const uint32_t m43 = magic43();
@@ -637,10 +650,8 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
           float d[KPW][NT][2];
 #pragma unroll
           for (int j = 0; j < KPW; ++j) {
-            const uint2 w = dw[e][j];
             Q4Pairs q[2];
-            q[0] = unpack_q4(w.x, m43);
-            q[1] = unpack_q4(w.y, m43);
+            dn_unpack(dw[e][j], m43, q);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
               const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
@@ -679,10 +690,10 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 // with a constant -136 operand for the int4 offset, accumulated per scale
 // group (the first SPLIT of the wave's k blocks, then the rest) and scaled
 // by the group scale and routing weight into acc[h] (rows 4lq + jj).
-template <int BPW, int SPLIT, bool FULL>
+template <int BPW, int SPLIT, bool FULL, class W>
 __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                         int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                        const uint2 (&dw)[BPW][kDownKpw], f32x4_t (&acc)[2]) {
+                                        const W (&dw)[BPW][kDownKpw], f32x4_t (&acc)[2]) {
   constexpr int KPW = kDownKpw;
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
   const int cps = a.I >> 3;
@@ -711,9 +722,10 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
       for (int j = 0; j < KPW; ++j) {
         const int sgi = j < SPLIT ? 0 : 1;
         const uint4 A = L.sact[dn_chunk<FULL>(x.ci[0], j, dp.nkb, zc)];
-        const uint2 w = dw[e][j];
-        D[sgi][0] = mfma_bf16(A, q4_operand(w.x, m43), D[sgi][0]);
-        D[sgi][1] = mfma_bf16(A, q4_operand(w.y, m43), D[sgi][1]);
+        Q4Pairs q[2];
+        dn_unpack(dw[e][j], m43, q);
+        D[sgi][0] = mfma_bf16(A, make_uint4(q[0].p0, q[0].p1, q[0].p2, q[0].p3), D[sgi][0]);
+        D[sgi][1] = mfma_bf16(A, make_uint4(q[1].p0, q[1].p1, q[1].p2, q[1].p3), D[sgi][1]);
         Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
       }
 #pragma unroll
@@ -734,10 +746,10 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
 // Blocks [e_lo, e_hi) with the wave's variant: k blocks in its first scale
 // group (1, 2 or all KPW; a group has at least KPW blocks) and whether the
 // wave has all KPW k blocks.
-template <int BPW, int MODE, int SPLIT>
+template <int BPW, int MODE, int SPLIT, class W>
 __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                              int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                             const uint2 (&dw)[BPW][kDownKpw], float (&accv)[MODE > 0 ? MODE : 1][2],
+                                             const W (&dw)[BPW][kDownKpw], float (&accv)[MODE > 0 ? MODE : 1][2],
                                              f32x4_t (&accm)[2]) {
   constexpr int NT = MODE > 0 ? MODE : 1;
   if (dp.nkb == kDownKpw) {
@@ -748,9 +760,9 @@ __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue
     else dn_mfma<BPW, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
   }
 }
-template <int BPW, int MODE>
+template <int BPW, int MODE, class W>
 __device__ __forceinline__ void dn_run(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v, int tm_v,
-                                       int U, const DnPlan& dp, int e_lo, int e_hi, const uint2 (&dw)[BPW][kDownKpw],
+                                       int U, const DnPlan& dp, int e_lo, int e_hi, const W (&dw)[BPW][kDownKpw],
                                        float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   const int split = min(kDownKpw, (1 << a.gsh) - (dp.kbw0 & ((1 << a.gsh) - 1)));
   if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
@@ -820,13 +832,16 @@ __device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int u
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
   const int n = nb * a.Gd * 4;
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_scales, a.dsc_total);
+  // quotients from float reciprocals: the operands are below 2^13, so the
+  // rounding error of (n + 0.5) * (1/m) is far from the next integer
+  const float inv_gd = 1.0f / (float)a.Gd, inv_u = 1.0f / (float)U;
 #pragma unroll
   for (int j = 0; j < kScaleLoads; ++j) {
     const int ch = tid + j * kThreads;
     const int eg = ch >> 2, q = ch & 3;
-    const int e = eg / a.Gd, g = eg - e * a.Gd;
+    const int e = (int)(((float)eg + 0.5f) * inv_gd), g = eg - e * a.Gd;
     const int b = blo + e;
-    const int d = b / U, u = b - d * U;
+    const int d = (int)(((float)b + 0.5f) * inv_u), u = b - d * U;
     const int ex = __shfl(uexp_v, min(u, kSlots - 1), kWave);
     const uint32_t off = (uint32_t)((((size_t)ex * a.Gd + g) * a.H + kUnitCols * d + 8 * q) * 2);
     if (ch < n)
@@ -857,7 +872,7 @@ __device__ __forceinline__ uint32_t f32_signal_bits(float v) {
 // read, the products, the sums over the waves, then per unit either the
 // output (a unit held whole, or the unit's first workgroup once the others'
 // partial sums are in) or this workgroup's partial sum for the first one.
-template <int BPW, int MODE, int CPT>
+template <int BPW, int MODE, int CPT, bool PRE>
 __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& P, char* lds, int U, int uexp_v,
                                            const uint16_t* act, float* part, int blo, int bhi, DnPlan dp,
                                            const uint2 (&dw0)[BPW][kDownKpw]) {
@@ -915,6 +930,23 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   c1 = uniform(c1);
   x0 = uniform(x0);
   x1 = uniform(x1);
+  // the first batch's words unpacked while the activations are on their way
+  // (where the registers allow: one token, few blocks)
+  DnQ dq[PRE ? BPW : 1][kDownKpw];
+  if constexpr (PRE) {
+    const uint32_t m43 = magic43();
+#pragma unroll
+    for (int e = 0; e < BPW; ++e)
+#pragma unroll
+      for (int j = 0; j < kDownKpw; ++j) {
+        dn_unpack(dw0[e][j], m43, dq[e][j].q);
+        // here, not next to the products: the unpacking overlaps the wait
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+          asm volatile("" : "+v"(dq[e][j].q[h].p0), "+v"(dq[e][j].q[h].p1), "+v"(dq[e][j].q[h].p2),
+                       "+v"(dq[e][j].q[h].p3));
+      }
+  }
   stage_acts<CPT>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
   lds_barrier();
 
@@ -936,8 +968,13 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   dp.nb = min(nb_all, BPW);
   dp.d_a = d_first;
   dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
-  dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, accv[0], accm[0]);
-  if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, accv[1], accm[1]);
+  if constexpr (PRE) {
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, accv[1], accm[1]);
+  } else {
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, accv[1], accm[1]);
+  }
   for (int b0 = blo + BPW; b0 < bhi; b0 += BPW) {
     dp.blo = b0;
     dp.e_off = b0 - blo;
@@ -1126,7 +1163,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   else if (n_my == 1) up_phase<KBW, 1, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
   else if (n_my == 2) up_phase<KBW, 2, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
   else up_phase<KBW, 3, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
-  if (bhi > blo) down_phase<BPW, MODE, CPT>(a, P, dyn_lds, U, uexp_v, act, part, blo, bhi, dp, dw);
+  if (bhi > blo) down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4>(a, P, dyn_lds, U, uexp_v, act, part, blo, bhi, dp, dw);
 }
 
 // ---------------------------------------------------------------------------
