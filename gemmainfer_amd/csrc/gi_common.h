@@ -20,6 +20,7 @@ constexpr int kWave = 64;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load (non-temporal hint: weights are read once).
 __device__ __forceinline__ uint4 load_nt_u4(const void* p) {

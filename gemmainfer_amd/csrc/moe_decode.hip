@@ -83,7 +83,6 @@ constexpr int kUnitCols = 32;         // output columns of a down unit
 constexpr int kDefaultSpin = 1 << 20;
 constexpr int kCpolNt = 2;            // non-temporal: weights are read once
 constexpr int kMaxItems = 9;          // gate/up items per workgroup and launch
-constexpr int kDownRegs = 64;         // down-word registers (uint2 units) per wave and batch
 constexpr int kDownKpw = 3;           // down k blocks per wave: Tk <= 24 (I <= 768)
 constexpr int kMaxI = kCols * kDownKpw * kWaves;  // 768
 constexpr size_t kActParity = (size_t)kSlots * kMaxI * 2;  // bytes of one exchange buffer
@@ -91,7 +90,6 @@ constexpr int kScaleLoads = 4;        // 16-byte down-scale chunks per thread (2
 constexpr int kMaxStage = 12;         // exchange chunks per thread: 64 rows of I/8 <= 96 chunks
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // buffer offset past any resource: the load returns zeros
 
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // A value every lane of the wave holds (read from LDS, so the compiler cannot
 // tell): made scalar, so that buffer offsets built from it need no per-lane
@@ -159,7 +157,37 @@ __device__ __forceinline__ int wave_scan_incl(int v) {
   return v;
 }
 
-__device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
+// Loads of the routing inputs, issued before anything else: with router
+// logits, wave w takes token min(w, M - 1)'s row; otherwise lane s of wave 0
+// takes slot s's expert id and weight (zeros past S: the resource ends there).
+template <int VPL>
+struct DecIn {
+  RouteIn<VPL> r;
+  uint32_t id_lo, id_hi, wb;
+};
+template <int VPL>
+__device__ __forceinline__ void dec_issue(const DecArgs& a, DecIn<VPL>& in) {
+  const int lane = threadIdx.x & (kWave - 1), wave = uniform(threadIdx.x >> 6);
+  in.id_lo = in.id_hi = in.wb = 0u;
+  if (a.logits) {
+    route_issue<VPL>(a, min(wave, a.M - 1), lane, in.r);
+  } else if (wave == 0) {
+    if (a.idx_is64) {
+      const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(a.idx, (uint32_t)a.S * 8u), lane * 8u, 0, 0);
+      in.id_lo = v.x;
+      in.id_hi = v.y;
+    } else {
+      in.id_lo = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(a.idx, (uint32_t)a.S * 4u), lane * 4u, 0, 0);
+    }
+    if (a.w_dtype == GI_DTYPE_FP32)
+      in.wb = __builtin_amdgcn_raw_buffer_load_b32(buffer_rsrc(a.w, (uint32_t)a.S * 4u), lane * 4u, 0, 0);
+    else
+      in.wb = __builtin_amdgcn_raw_buffer_load_b16(buffer_rsrc(a.w, (uint32_t)a.S * 2u), lane * 2u, 0, 0);
+  }
+}
+
+template <int VPL>
+__device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, const DecIn<VPL>& in) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int S = a.S;
   if (tid < 32) P.bm[tid] = 0u;
@@ -167,11 +195,18 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
   (&P.rowpos[0][0])[tid] = -1;  // kSlots * kRows == kThreads entries
   (&P.roww[0][0])[tid] = 0.f;
   if (a.logits) {
-    if (wave < a.M) route_token_any(a, wave, lane, P.slot_e + wave * a.top_k, P.slot_w + wave * a.top_k);
-  } else if (tid < S) {
-    const int e = load_expert_id(a.idx, a.idx_is64, tid);
-    P.slot_e[tid] = (e >= 0 && e < a.E) ? e : -1;
-    P.slot_w[tid] = load_weight_as_bf16(a.w, a.w_dtype, tid);
+    if (wave < a.M) route_finish<VPL>(a, lane, in.r, P.slot_e + wave * a.top_k, P.slot_w + wave * a.top_k);
+  } else if (wave == 0 && lane < S) {
+    int e = (int)in.id_lo;
+    if (a.idx_is64) {
+      const long long v = (long long)(((unsigned long long)in.id_hi << 32) | in.id_lo);
+      e = (v < -2147483647LL || v > 2147483647LL) ? -1 : (int)v;
+    }
+    P.slot_e[lane] = (e >= 0 && e < a.E) ? e : -1;
+    const float wv = a.w_dtype == GI_DTYPE_FP32   ? __uint_as_float(in.wb)
+                     : a.w_dtype == GI_DTYPE_FP16 ? fp16_to_f32((uint16_t)in.wb)
+                                                  : bf16_to_f32(in.wb);
+    P.slot_w[lane] = round_to_bf16(wv);
   }
   lds_barrier();
   if (wave == 0) {
@@ -180,10 +215,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
     const int t = lane / a.top_k;
     if (a.logits) {
       w = round_to_bf16(w);
-      if (blockIdx.x == 0 && lane < S) {
-        if (a.out_idx) a.out_idx[lane] = e;
-        if (a.out_w) a.out_w[lane] = f32_to_bf16(w);
-      }
+      if (lane < S) P.slot_w[lane] = w;  // reported by workgroup 0 at the end
     } else {
       // a token's slots with one expert: the first keeps the sum of their
       // weights (in slot order), the others are dropped
@@ -208,7 +240,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
     const uint32_t word = lane < 32 ? P.bm[lane] : 0u;
     const int cnt = __popc(word);
     const int incl = wave_scan_incl(cnt);
-    const int U = __shfl(incl, kWave - 1, kWave);
+    const int U = __builtin_amdgcn_readlane(incl, kWave - 1);
     const int wi = max(e, 0) >> 5;
     const int base = __shfl(incl - cnt, wi, kWave);
     const uint32_t bw = (uint32_t)__shfl((int)word, wi, kWave);
@@ -223,7 +255,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
     const uint32_t tmu = lane < U ? P.tm[lane] : 0u;
     const int c2 = __popc(tmu);
     const int inc2 = wave_scan_incl(c2);
-    const int total = __shfl(inc2, kWave - 1, kWave);
+    const int total = __builtin_amdgcn_readlane(inc2, kWave - 1);
     const int ep0 = inc2 - c2;
     if (lane < U) {
       P.epos[lane] = ep0;
@@ -245,8 +277,9 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P) {
 }
 
 // Launch epoch (see the header).
-__device__ __forceinline__ unsigned long long load_epoch(const DecArgs& a) {
-  return __hip_atomic_load(a.epochs + blockIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ u32x2_t load_epoch(const DecArgs& a) {
+  return __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(a.epochs, (uint32_t)kEpochSlots * 8u), blockIdx.x * 8u, 0,
+                                              kCpolAgent);
 }
 __device__ __forceinline__ void advance_epoch(const DecArgs& a, unsigned long long ep) {
   for (int j = blockIdx.x; j < kEpochSlots; j += gridDim.x)
@@ -315,6 +348,10 @@ struct GuLds {
   float4* red;     // [kWaves][M][16] per-wave gate/up sums, 64 task columns
   uint16_t* sact;  // [M][32] one item's activations in k order
 };
+template <int KBW>
+__host__ __device__ constexpr size_t gu_lds_bytes() {
+  return (size_t)kRows * GuShape<KBW>::KPM * 16 + (size_t)kWaves * kRows * 16 * 16 + (size_t)kRows * kCols * 2;
+}
 
 // One item: gate/up product, cross-wave reduction, activation, exchange.
 template <int KBW>
@@ -481,11 +518,13 @@ struct DnLds {
   float* pbuf;    // [kPartSlots][kRows][32] partial sums of a unit's other workgroups (after red)
 };
 
-// LDS layout of the down phase.
+// LDS layout of the down phase.  The down scales sit past both the gate/up
+// phase's LDS (gu bytes) and the down phase's data: they are staged before
+// the weight loads go out.
 struct DnLayout {
   size_t abias, dsc, total;
 };
-__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, int bpw) {
+__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, size_t gu) {
   const size_t rows = (size_t)S + 1;
   size_t sact = align16(rows * I * 2);
   const size_t red = (size_t)2 * kWaves * kRows * 32 * 4 + (size_t)kPartSlots * kRows * 32 * 4;
@@ -493,7 +532,7 @@ __host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, int bpw) {
   DnLayout l;
   l.abias = sact;
   l.dsc = l.abias + align16(rows * (I / 8) * 4);
-  (void)bpw;
+  if (l.dsc < gu) l.dsc = align16(gu);
   l.total = l.dsc + align16((size_t)S * Gd * 64);  // a workgroup holds at most U <= S blocks
   return l;
 }
@@ -601,7 +640,6 @@ __device__ __forceinline__ uint32_t dn_chunk(uint32_t ci, int j, int nkb, uint32
   else return j < nkb ? ci + 4 * j : zc;
 }
 
-constexpr int kDownEg = 2;  // blocks per straight-line run of the VALU down products
 
 // A down word (columns 2lr, 2lr+1) as the products take it: packed (unpacked
 // where it is used) or already unpacked into bf16 pairs 128 + q.
@@ -620,9 +658,8 @@ __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2
 // One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
 // workgroup (all of one unit).  Lane (lq, lr) takes columns 2lr, 2lr+1 at
 // packed row 4kb + lq, i.e. one 8-value chunk of each token's activation
-// row; the chunk's -136 offset sum comes precomputed from LDS.  Blocks run
-// kDownEg at a time as straight-line code, each pair with its own sum so that
-// the dot chains are independent; the first SPLIT of a wave's k blocks
+// row; the chunk's -136 offset sum comes precomputed from LDS.  Each k block
+// and token has its own dot chain; the first SPLIT of a wave's k blocks
 // belong to one scale group, the rest to the next.  The four lq lanes are
 // added at the end.
 template <int BPW, int NT, int SPLIT, bool FULL, class W>
@@ -636,48 +673,40 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
   const uint32_t zc = (uint32_t)(a.S * cps);  // the zero row
   const int u_base = dp.blo - dp.d_a * U;     // expert of block 0
 #pragma unroll
-  for (int e0 = 0; e0 < BPW; e0 += kDownEg) {
-    if (e0 < e_hi && e0 + kDownEg > e_lo) {
+  for (int e = 0; e < BPW; ++e) {
+    if (e >= e_lo && e < e_hi) {
+      int u = u_base + e;
+      if (u >= U) u -= U;
+      const DnBlock<NT> x = dn_block<NT, false>(a, P, L, epos_v, tm_v, u, dp.e_off + e, true, dp.kbw0, g1, g2);
+      float d[KPW][NT][2];
 #pragma unroll
-      for (int ei = 0; ei < kDownEg; ++ei) {
-        const int e = e0 + ei;
-        if (e < BPW) {
-          const bool valid = e >= e_lo && e < e_hi;
-          int u = u_base + e;
-          if (u >= U) u -= U;
-          const DnBlock<NT> x =
-              dn_block<NT, false>(a, P, L, epos_v, tm_v, u, dp.e_off + e, valid, dp.kbw0, g1, g2);
-          float d[KPW][NT][2];
+      for (int j = 0; j < KPW; ++j) {
+        Q4Pairs q[2];
+        dn_unpack(dw[e][j], m43, q);
 #pragma unroll
-          for (int j = 0; j < KPW; ++j) {
-            Q4Pairs q[2];
-            dn_unpack(dw[e][j], m43, q);
+        for (int t = 0; t < NT; ++t) {
+          const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
+          const uint4 A = L.sact[ci];
+          const float b = L.abias[ci];
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-              const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
-              const uint4 A = L.sact[ci];
-              const float b = L.abias[ci];
+          for (int h = 0; h < 2; ++h) d[j][t][h] = dot_chunk(A, q[h], b);
+        }
+      }
 #pragma unroll
-              for (int h = 0; h < 2; ++h) d[j][t][h] = dot_chunk(A, q[h], b);
-            }
-          }
+      for (int t = 0; t < NT; ++t) {
 #pragma unroll
-          for (int t = 0; t < NT; ++t) {
+        for (int h = 0; h < 2; ++h) {
+          const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
+          const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
+          // segment sums: k block 0 is always in the first group, block
+          // KPW-1 in the second unless SPLIT == KPW
+          float v1 = d[0][t][h], v2 = d[KPW - 1][t][h];
 #pragma unroll
-            for (int h = 0; h < 2; ++h) {
-              const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
-              const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
-              // segment sums: k block 0 is always in the first group, block
-              // KPW-1 in the second unless SPLIT == KPW
-              float v1 = d[0][t][h], v2 = d[KPW - 1][t][h];
-#pragma unroll
-              for (int j = 1; j < KPW - 1; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
-              if constexpr (SPLIT == KPW) v1 += v2;
-              float v = sa * v1;
-              if constexpr (SPLIT < KPW) v += sb * v2;
-              acc[t][h] += x.wt[t] * v;
-            }
-          }
+          for (int j = 1; j < KPW - 1; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
+          if constexpr (SPLIT == KPW) v1 += v2;
+          float v = sa * v1;
+          if constexpr (SPLIT < KPW) v += sb * v2;
+          acc[t][h] += x.wt[t] * v;
         }
       }
     }
@@ -780,7 +809,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // sum stored.  Each wave repeats its incomplete chunks until none is left
 // (bounded: on timeout the status word is flagged and the wave goes on, so
 // the launch always ends).
-template <int CPT>
+template <int CPT, bool BIAS>
 __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, const uint16_t* act, int c0, int c1,
                                            int x0, int x1) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
@@ -809,7 +838,7 @@ __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, con
         if (chunk_ready(v)) {
           const uint4 x = make_uint4(~v.x, ~v.y, ~v.z, ~v.w);
           L.sact[g] = x;
-          L.abias[g] = neg_bias_136(x);
+          if constexpr (BIAS) L.abias[g] = neg_bias_136(x);
           pending &= ~(1u << j);
         }
       }
@@ -828,13 +857,16 @@ __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, con
 // (e * Gd + g) * 4 + q holds bf16 columns 8q .. 8q+7 of block e's unit for
 // group g, so that lane lr's pair (columns 2lr, 2lr+1) is u32 word
 // (e * Gd + g) * 16 + lr.  Complete once the wave has waited for its loads.
-__device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int uexp_v, int U, int blo, int nb) {
+__device__ __forceinline__ void dsc_load(const DecArgs& a, uint32_t* dsc, int uexp_v, int U, int blo, int nb) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
   const int n = nb * a.Gd * 4;
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.d_scales, a.dsc_total);
   // quotients from float reciprocals: the operands are below 2^13, so the
   // rounding error of (n + 0.5) * (1/m) is far from the next integer
   const float inv_gd = 1.0f / (float)a.Gd, inv_u = 1.0f / (float)U;
+  int ex[kScaleLoads];
+  uint32_t off[kScaleLoads];
+  // the expert ids of all chunks first (one LDS round trip for all of them)
 #pragma unroll
   for (int j = 0; j < kScaleLoads; ++j) {
     const int ch = tid + j * kThreads;
@@ -842,11 +874,16 @@ __device__ __forceinline__ void dsc_load(const DecArgs& a, const DnLds& L, int u
     const int e = (int)(((float)eg + 0.5f) * inv_gd), g = eg - e * a.Gd;
     const int b = blo + e;
     const int d = (int)(((float)b + 0.5f) * inv_u), u = b - d * U;
-    const int ex = __shfl(uexp_v, min(u, kSlots - 1), kWave);
-    const uint32_t off = (uint32_t)((((size_t)ex * a.Gd + g) * a.H + kUnitCols * d + 8 * q) * 2);
+    ex[j] = __shfl(uexp_v, min(u, kSlots - 1), kWave);
+    off[j] = (uint32_t)((g * a.H + kUnitCols * d + 8 * q) * 2);
+  }
+#pragma unroll
+  for (int j = 0; j < kScaleLoads; ++j) {
+    const int ch = tid + j * kThreads;
+    const uint32_t o = off[j] + (uint32_t)ex[j] * (uint32_t)(a.Gd * a.H * 2);
     if (ch < n)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)((uint4*)L.dsc + j * kThreads + wave * kWave), 16,
-                                               off, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)((uint4*)dsc + j * kThreads + wave * kWave), 16,
+                                               o, 0, 0, 0);
   }
 }
 
@@ -873,15 +910,14 @@ __device__ __forceinline__ uint32_t f32_signal_bits(float v) {
 // output (a unit held whole, or the unit's first workgroup once the others'
 // partial sums are in) or this workgroup's partial sum for the first one.
 template <int BPW, int MODE, int CPT, bool PRE>
-__device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& P, char* lds, int U, int uexp_v,
-                                           const uint16_t* act, float* part, int blo, int bhi, DnPlan dp,
-                                           const uint2 (&dw0)[BPW][kDownKpw]) {
+__device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& P, char* lds, const DnLayout& ly,
+                                           int U, int uexp_v, const uint16_t* act, float* part, int blo, int bhi,
+                                           DnPlan dp, const uint2 (&dw0)[BPW][kDownKpw]) {
   constexpr int NT = MODE > 0 ? MODE : 1;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int lq = lane >> 4, lr = lane & 15;
   const int cps = a.I >> 3;
   const int G = gridDim.x, NB = a.units * U;
-  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, BPW);
   DnLds L;
   L.sact = (uint4*)lds;
   L.red = (float*)lds;
@@ -892,16 +928,18 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   const int tm_v = (int)P.tm[lane];
   const int nb_all = bhi - blo, d_first = blo / U;
   const int n_units = (bhi - 1) / U > d_first ? 2 : 1;  // at most two: a workgroup has at most U blocks
-  // previous output of the writer thread's (token, column) of each unit
-  // (read unconditionally: a load under a per-lane condition is waited for
-  // at the end of the condition)
+  // previous output of the writer thread's (token, column) of each unit when
+  // accumulating: the 4-byte word holding it, loaded by every thread (no
+  // memory access past the resource), so that no wait is placed here
   const bool writer = tid < a.M * kUnitCols;
   const int wt = tid >> 5, wc = tid & 31;
-  uint16_t old[2];
+  const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(a.out, a.overwrite ? 0u : (uint32_t)a.M * a.H * 2u);
+  uint32_t old[2];
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     const int d = min(d_first + p, a.units - 1);
-    old[p] = a.out[writer ? (size_t)wt * a.H + kUnitCols * d + wc : 0];
+    const uint32_t off = writer ? (uint32_t)(wt * a.H + kUnitCols * d + (wc & ~1)) * 2u : kOob;
+    old[p] = __builtin_amdgcn_raw_buffer_load_b32(ro, off, 0, 0);
   }
   lds_barrier();  // the gate/up phase's LDS is free
   // the zero row (absent tokens and missing k blocks read it)
@@ -909,7 +947,6 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     L.sact[a.S * cps + tid] = make_uint4(0u, 0u, 0u, 0u);
     L.abias[a.S * cps + tid] = 0.f;
   }
-  dsc_load(a, L, uexp_v, U, blo, nb_all);
   // rows of the experts the blocks read: expert u_a.. of the first unit, and
   // 0..u_b of the second
   const int u_a = blo - d_first * U;
@@ -947,7 +984,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
                        "+v"(dq[e][j].q[h].p3));
       }
   }
-  stage_acts<CPT>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
+  stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
   lds_barrier();
 
   float accv[2][NT][2];
@@ -1073,7 +1110,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
       lds_barrier();
     }
     if (writer) {
-      if (!a.overwrite) s += bf16_to_f32(old[p]);
+      if (!a.overwrite) s += bf16_to_f32((old[p] >> (16 * (wc & 1))) & 0xffffu);
       a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_bf16(s);
     }
   }
@@ -1108,32 +1145,59 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
 // ---------------------------------------------------------------------------
 // kernel
 // ---------------------------------------------------------------------------
+// The start of every workgroup: the routing inputs go out first, then the
+// epoch word and x behind them (neither depends on the routing), then the
+// routing and the Token-Union tables.  The epoch is read after the routing:
+// a value needed in scalar registers is otherwise read right after its load,
+// and the routing would wait for it.
+template <int KBW, int VPL>
+__device__ __forceinline__ u32x2_t dec_start(const DecArgs& a, DecPrologue& P, XRegs<KBW>& xr) {
+  DecIn<VPL> in;
+  dec_issue<VPL>(a, in);
+  u32x2_t ep = load_epoch(a);
+  load_x<KBW>(a, xr);
+  dec_prologue<VPL>(a, P, in);
+  asm volatile("" : "+v"(ep));
+  return ep;
+}
+
+// The end of every workgroup: the stores that no part of this launch waits
+// for, left to the end so that no wait of the launch counts them (a store
+// counts in the same in-order counter as the loads): the next launch's epoch,
+// this workgroup's share of the next launch's exchange buffers, and the
+// routing report of workgroup 0.
+__device__ __forceinline__ void dec_end(const DecArgs& a, const DecPrologue& P, unsigned long long ep,
+                                        int parity) {
+  const int b = blockIdx.x, G = gridDim.x;
+  if (threadIdx.x == 0) advance_epoch(a, ep);
+  clear_share(a.act + (size_t)(parity ^ 1) * (kActParity / 2), kActParity, b, G);
+  clear_share(a.part + (size_t)(parity ^ 1) * (kPartParity / 4), kPartParity, b, G);
+  if (b == 0 && a.logits && threadIdx.x < a.S) {
+    if (a.out_idx) a.out_idx[threadIdx.x] = P.slot_e[threadIdx.x];
+    if (a.out_w) a.out_w[threadIdx.x] = f32_to_bf16(P.slot_w[threadIdx.x]);
+  }
+}
+
 template <int KBW, int MODE, int BPW, int CPT>
 __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   __shared__ DecPrologue P;
   extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
-  // the epoch word and x go out first: neither depends on the routing
-  // (every lane reads the word: a load under a per-lane condition would be
-  // waited for at the end of the condition)
-  const unsigned long long ep = load_epoch(a) + 1;
   XRegs<KBW> xr;
-  load_x<KBW>(a, xr);
-  dec_prologue(a, P);
-  if (threadIdx.x == 0) advance_epoch(a, ep);
+  u32x2_t epr;
+  if (a.E <= 2 * kWave) epr = dec_start<KBW, 2>(a, P, xr);
+  else if (a.E <= 4 * kWave) epr = dec_start<KBW, 4>(a, P, xr);
+  else epr = dec_start<KBW, kRouteMaxExperts / kWave>(a, P, xr);
+  const unsigned long long ep = (((unsigned long long)epr.y << 32) | epr.x) + 1ull;
   const int parity = (int)(ep & 1ull);
   uint16_t* act = a.act + (size_t)parity * (kActParity / 2);
-  uint16_t* act_next = a.act + (size_t)(parity ^ 1) * (kActParity / 2);
   float* part = a.part + (size_t)parity * (kPartParity / 4);
-  float* part_next = a.part + (size_t)(parity ^ 1) * (kPartParity / 4);
   const int U = uniform(P.n_unique);
   const int b = blockIdx.x, G = gridDim.x;
-  // this workgroup's share of the next launch's exchange buffers
-  clear_share(act_next, kActParity, b, G);
-  clear_share(part_next, kPartParity, b, G);
   if (U == 0) {
     // no valid slot: a layer call still owns (overwrites) out
     if (a.overwrite)
       for (int i = b * kThreads + threadIdx.x; i < a.M * a.H; i += G * kThreads) a.out[i] = 0;
+    dec_end(a, P, ep, parity);
     return;
   }
   const int uexp_v = P.uexp[threadIdx.x & (kWave - 1)];
@@ -1150,6 +1214,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
   // x into LDS first: its registers are free before the word buffers fill
   if (n_my > 0) stage_x<KBW>(a, L, xr);
+  // the down scales of every block of the workgroup, ahead of the weights
+  // (older than every weight load, they leave the weight waits exact)
+  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, gu_lds_bytes<KBW>());
+  dsc_load(a, (uint32_t*)(dyn_lds + ly.dsc), uexp_v, U, blo, bhi - blo);
   DnPlan dp;
   dp.blo = blo;
   dp.e_off = 0;
@@ -1163,7 +1231,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   else if (n_my == 1) up_phase<KBW, 1, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
   else if (n_my == 2) up_phase<KBW, 2, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
   else up_phase<KBW, 3, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
-  if (bhi > blo) down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4>(a, P, dyn_lds, U, uexp_v, act, part, blo, bhi, dp, dw);
+  if (bhi > blo)
+    down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4>(a, P, dyn_lds, ly, U, uexp_v, act, part, blo, bhi, dp, dw);
+  dec_end(a, P, ep, parity);
 }
 
 // ---------------------------------------------------------------------------
@@ -1171,17 +1241,13 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
 // ---------------------------------------------------------------------------
 constexpr size_t kMaxDynLds = 160 * 1024 - 8 * 1024;  // room for the static prologue
 
-template <int KBW>
-size_t gu_lds_bytes() {
-  return (size_t)kRows * GuShape<KBW>::KPM * 16 + (size_t)kWaves * kRows * 16 * 16 + (size_t)kRows * kCols * 2;
-}
 
 int kbw_for(int H) { return H <= 512 ? 2 : 11; }
 
 size_t lds_for(int kbw, int S, int I, int Gd, int bpw) {
+  (void)bpw;
   const size_t g = kbw == 2 ? gu_lds_bytes<2>() : gu_lds_bytes<11>();
-  const size_t d = dn_layout(S, I, Gd, bpw).total;
-  return g > d ? g : d;
+  return dn_layout(S, I, Gd, g).total;
 }
 
 template <int KBW, int MODE, int BPW, int CPT>
@@ -1214,6 +1280,7 @@ bool decode_plan(int M, int S, int H, int I, int cus, DecodePlan& pl) {
   int G = cus < kEpochSlots ? cus : kEpochSlots;
   if (G > (kPartSlots - 1) * units) G = (kPartSlots - 1) * units;
   if (G < 1 || ((long long)S * tk + G - 1) / G > kMaxItems) return false;
+  if (G < units) return false;  // at most U blocks per workgroup (the scale staging holds S)
   pl.grid = G;
   pl.mode = M == 1 ? 1 : M == 2 ? 2 : 0;
   const int max_blocks = (units * S + G - 1) / G;

@@ -42,75 +42,154 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return umax(umax(r0, r1), umax(r2, r3));
 }
 
-// Top-k + softmax of token t by one wave (gemma.py:77-80).  Lane l holds the
-// keys of experts l, l+64, ...  Each round takes the wave maximum of the keys
-// and, among equal keys, the lowest expert index (first set ballot bit in the
-// lowest register), then retires it (key 0; every real value has a non-zero
-// key).  Lane r < top_k ends with the r-th expert and its weight.
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = min(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return min(min(r0, r1), min(r2, r3));
+}
+
+// Router inputs of one token held by one wave: lane l has experts l + 64v.
+template <int VPL>
+struct RouteIn {
+  uint32_t raw[VPL];  // logit bits: bf16 (zero-extended) or fp32
+  uint32_t es[VPL];   // expert_scale bits (zero without a scale tensor)
+};
+
+// The loads of token t's logits and of the expert scales, issued before any
+// other work so that later loads queue behind them; past E (or without a
+// scale tensor) the buffer resource returns zeros without a memory access.
 template <int VPL, class A>
-__device__ __forceinline__ void route_token(const A& a, int t, int lane, int* idx_out,
-                                            float* w_out) {
-  // All VPL loads go out before any is used (clamped indices, no branch
-  // around a load: a load under a per-lane condition is waited for at the
-  // end of the condition), one dtype path per launch.
-  uint32_t keys[VPL];
-  float f[VPL], es[VPL];
-  const size_t base = (size_t)t * a.E;
-  // expert_scale goes out with the logits, so the winners' scales need no
-  // load of their own
+__device__ __forceinline__ void route_issue(const A& a, int t, int lane, RouteIn<VPL>& r) {
+  const bool bf = a.logits_dtype == GI_DTYPE_BF16;
+  const uint32_t rowb = (uint32_t)a.E * (bf ? 2u : 4u);
+  const __amdgpu_buffer_rsrc_t rl = buffer_rsrc((const char*)a.logits + (size_t)t * rowb, rowb);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.expert_scale, a.expert_scale ? (uint32_t)a.E * 4u : 0u);
+  if (bf) {
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) es[v] = a.expert_scale ? a.expert_scale[min(lane + v * kWave, a.E - 1)] : 1.f;
-  if (a.logits_dtype == GI_DTYPE_BF16) {
-    const uint16_t* row = (const uint16_t*)a.logits + base;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) f[v] = bf16_to_f32(row[min(lane + v * kWave, a.E - 1)]);
+    for (int v = 0; v < VPL; ++v)
+      r.raw[v] = __builtin_amdgcn_raw_buffer_load_b16(rl, (uint32_t)(lane + v * kWave) * 2u, 0, 0);
   } else {
-    const float* row = (const float*)a.logits + base;
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) f[v] = row[min(lane + v * kWave, a.E - 1)];
+    for (int v = 0; v < VPL; ++v)
+      r.raw[v] = __builtin_amdgcn_raw_buffer_load_b32(rl, (uint32_t)(lane + v * kWave) * 4u, 0, 0);
   }
+#pragma unroll
+  for (int v = 0; v < VPL; ++v)
+    r.es[v] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(lane + v * kWave) * 4u, 0, 0);
+}
+
+// Top-k + softmax of one token by one wave (gemma.py:77-80) from the loaded
+// inputs.  Each round takes the largest remaining key and, among equal keys,
+// the lowest expert index, then retires it (key 0; every real value has a
+// non-zero key).  Lane r < top_k ends with the r-th expert and its weight.
+// With two experts per lane (E <= 128) each lane keeps its pair ordered, so
+// a round is one wave maximum, one ballot and a pop on the winning lane.
+template <int VPL, class A>
+__device__ __forceinline__ void route_finish(const A& a, int lane, const RouteIn<VPL>& r, int* idx_out,
+                                             float* w_out) {
+  const bool bf = a.logits_dtype == GI_DTYPE_BF16;
+  uint32_t keys[VPL];
+  float es[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int e = lane + v * kWave;
-    keys[v] = e < a.E ? orderable_key(f[v]) : 0u;
+    const float f = __uint_as_float(bf ? r.raw[v] << 16 : r.raw[v]);
+    keys[v] = e < a.E ? orderable_key(f) : 0u;
+    es[v] = a.expert_scale ? __uint_as_float(r.es[v]) : 1.f;
   }
   int my_idx = 0;
-  float my_val = 0.f, my_es = 1.f;
-  for (int r = 0; r < a.top_k; ++r) {
-    uint32_t lm = keys[0];
-#pragma unroll
-    for (int v = 1; v < VPL; ++v) lm = umax(lm, keys[v]);
-    const uint32_t m = wave_max_u32(lm);
-    int win = -1;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const unsigned long long b = __ballot(keys[v] == m);
-      if (win < 0 && b) win = v * kWave + (int)__builtin_ctzll(b);
+  uint32_t my_key = 0u;
+  float my_es = 1.f;
+  if constexpr (VPL == 2) {
+    const bool sw = keys[1] > keys[0];  // on a tie the lower expert (lane) stays first
+    uint32_t hi = sw ? keys[1] : keys[0], lo = sw ? keys[0] : keys[1];
+    int hi_i = sw ? lane + kWave : lane;
+    const int lo_i = sw ? lane : lane + kWave;
+    float hi_s = sw ? es[1] : es[0];
+    const float lo_s = sw ? es[0] : es[1];
+    bool popped = false;
+    for (int rr = 0; rr < a.top_k; ++rr) {
+      const uint32_t m = wave_max_u32(hi);
+      const unsigned long long b = __ballot(hi == m);
+      int w = (int)__builtin_ctzll(b);
+      // equal maxima on several lanes: the lowest expert index among them
+      // (a lane's second key equal to m has a larger index than its first)
+      if (__popcll(b) > 1) w = (int)(wave_min_u32(hi == m ? (uint32_t)hi_i : 0xffffffffu) & (kWave - 1));
+      const int wi = __builtin_amdgcn_readlane(hi_i, w);
+      const float ws = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(hi_s), w));
+      if (lane == w) {
+        hi = popped ? 0u : lo;
+        hi_i = lo_i;
+        hi_s = lo_s;
+        popped = true;
+      }
+      if (lane == rr) {
+        my_idx = wi;
+        my_key = m;
+        my_es = ws;
+      }
     }
+  } else {
+    for (int rr = 0; rr < a.top_k; ++rr) {
+      uint32_t lm = keys[0];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v)
-      if (lane + v * kWave == win) keys[v] = 0u;
-    float ew = 0.f;
+      for (int v = 1; v < VPL; ++v) lm = umax(lm, keys[v]);
+      const uint32_t m = wave_max_u32(lm);
+      int win = -1;
 #pragma unroll
-    for (int v = 0; v < VPL; ++v)
-      if ((win >> 6) == v) ew = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(es[v]), win & (kWave - 1)));
-    if (lane == r) {
-      my_idx = win;
-      my_val = key_value(m);
-      my_es = ew;
+      for (int v = 0; v < VPL; ++v) {
+        const unsigned long long b = __ballot(keys[v] == m);
+        if (win < 0 && b) win = v * kWave + (int)__builtin_ctzll(b);
+      }
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        if (lane + v * kWave == win) keys[v] = 0u;
+      float ew = 0.f;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+        if ((win >> 6) == v) ew = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(es[v]), win & (kWave - 1)));
+      if (lane == rr) {
+        my_idx = win;
+        my_key = m;
+        my_es = ew;
+      }
     }
   }
-  const float vmax = __shfl(my_val, 0, kWave);
+  const float my_val = key_value(my_key);
+  const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), 0));
   const float ex = lane < a.top_k ? expf(my_val - vmax) : 0.f;
-  float sum = ex;
+  // sum of the weights in the order of a butterfly over xor 32, 16, .., 1;
+  // with top_k <= 8 every lane past 7 holds zero and the first three steps
+  // add exact zeros, so lanes 0-3 need only lane + 4, then the quad swaps
+  float sum;
+  if (a.top_k <= 8) {
+    float s = ex + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ex), 0x104, 0xF, 0xF, false));  // row_shl:4
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  } else {
+    sum = ex;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  }
   if (lane < a.top_k) {
     float p = ex / sum;
     p *= my_es;
     idx_out[lane] = my_idx;
     w_out[lane] = p;
   }
+}
+
+// Loads and selection in one step (kernels with nothing to overlap).
+template <int VPL, class A>
+__device__ __forceinline__ void route_token(const A& a, int t, int lane, int* idx_out, float* w_out) {
+  RouteIn<VPL> r;
+  route_issue<VPL>(a, t, lane, r);
+  route_finish<VPL>(a, lane, r, idx_out, w_out);
 }
 
 template <class A>
