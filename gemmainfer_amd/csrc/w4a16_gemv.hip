@@ -23,6 +23,7 @@
 #include "../../include/gemmainfer_amd.h"
 #include "gi_common.h"
 #include "gi_internal.h"
+#include "moe_shared.h"
 
 namespace gi {
 
@@ -183,6 +184,140 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
   if (tid == 0) store_relaxed(&a.ctr[tile], 0);
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path for a few token rows and a wide N (lm_head): with 3..16
+// rows the VALU dot products of the path above cost more than the weight
+// stream, so the products run on v_mfma_f32_16x16x32_bf16 with A = the token
+// rows (zero rows past M) and B = the unpacked int4 words (128 + q), plus one
+// product with a constant -136 operand per k block for the offset.  A
+// workgroup owns 256 columns over all of K (wave w: 64 of them; lane
+// (lq, lr) loads the 16 bytes of columns 4lr..4lr+3 at packed row 4kb + lq,
+// i.e. the B operands of four 16-column products).  The weights stream
+// through a ring of kMfRing register slots (the load for k block kb + ring
+// goes out as kb is consumed).  The k blocks of a pass are straight-line
+// code (kMfPass of them, the tail past K reads zeros from the buffer
+// resource), so that every wait has an exact count: a ring carried around a
+// loop is drained at the loop header.  x and the scales of the workgroup's
+// columns sit in LDS.  Groups end every KPG = gs/32 k blocks:
+// y += scale * (D + Db); groups at or past G (a floor-size scales tensor)
+// are dropped like the reference's kernels (marlin.cu:128).
+// ---------------------------------------------------------------------------
+using moe::f32x4_t;
+constexpr int kMfThreads = 256;
+constexpr int kMfCols = 256;  // output columns per workgroup (64 per wave)
+constexpr int kMfRing = 8;    // k blocks in flight per wave
+constexpr int kMfPass = 96;   // k blocks per straight-line pass (K <= 3072 in one pass)
+constexpr int kMfMaxM = 16;
+
+struct MfArgs {
+  const uint16_t* A;  // [M, K] bf16
+  const int32_t* B;   // [K/8, N]
+  const uint16_t* S;  // [G, N] bf16
+  uint16_t* C;        // [M, N] bf16
+  int M, K, N, G;
+  uint32_t b_bytes;
+  float cap;
+};
+
+template <int KPG>
+__global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
+  extern __shared__ uint4 mf_lds[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lq = lane >> 4, lr = lane & 15;
+  const int Kp = a.K >> 3, KB = a.K >> 5;
+  const int col0 = blockIdx.x * kMfCols;
+  uint4* xs = mf_lds;                                     // [M + 1][Kp], row M zero
+  uint2* ss = (uint2*)(mf_lds + (size_t)(a.M + 1) * Kp);  // [G][64]: scales of column quad c
+  // x rows in the matrix-core k order, and this workgroup's scales
+  for (int i = tid; i < (a.M + 1) * Kp; i += kMfThreads) {
+    const int n = i / Kp, r = i - n * Kp;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (n < a.M) v = moe::mfma_k_order(*(const uint4*)(a.A + (size_t)n * a.K + 8 * r));
+    xs[i] = v;
+  }
+  for (int i = tid; i < a.G * (kMfCols / 4); i += kMfThreads) {
+    const int g = i >> 6, c = i & 63;
+    ss[i] = *(const uint2*)(a.S + (size_t)g * a.N + col0 + 4 * c);
+  }
+  __syncthreads();
+
+  const uint32_t m43 = magic43();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(moe::kNeg136Pair, moe::kNeg136Pair, moe::kNeg136Pair, moe::kNeg136Pair);
+  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
+  const uint2* srow = ss + wave * 16 + lr;
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
+  const uint32_t rstep = (uint32_t)a.N * 16u;  // 4 packed rows
+  const uint32_t voff = (uint32_t)lq * (uint32_t)a.N * 4u + (uint32_t)(col0 + wave * 64 + 4 * lr) * 4u;
+  f32x4_t y[4] = {zf, zf, zf, zf};
+  for (int kp = 0; kp < KB; kp += kMfPass) {
+    uint4 w[kMfRing];
+#pragma unroll
+    for (int s = 0; s < kMfRing; ++s) {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, voff + (uint32_t)(kp + s) * rstep, 0, 2);
+      w[s] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+    f32x4_t D[4] = {zf, zf, zf, zf};
+    f32x4_t Db = zf;
+#pragma unroll
+    for (int j = 0; j < kMfPass; ++j) {
+      const int kb = kp + j;
+      if (kb < KB) {
+        const uint4 A = xrow[4 * kb];
+        const uint4 wv = w[j % kMfRing];
+        D[0] = moe::mfma_bf16(A, moe::q4_operand(wv.x, m43), D[0]);
+        D[1] = moe::mfma_bf16(A, moe::q4_operand(wv.y, m43), D[1]);
+        D[2] = moe::mfma_bf16(A, moe::q4_operand(wv.z, m43), D[2]);
+        D[3] = moe::mfma_bf16(A, moe::q4_operand(wv.w, m43), D[3]);
+        Db = moe::mfma_bf16(A, bc, Db);
+        // a group ends after k block kb (kMfPass is a multiple of KPG, so
+        // groups never straddle passes), or K ends
+        if ((j + 1) % KPG == 0 || kb == KB - 1) {
+          const int g = kb / KPG;
+          if (g < a.G) {
+            const uint2 sv = srow[g * 64];
+            const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) y[q][jj] += sc[q] * (D[q][jj] + Db[jj]);
+          }
+#pragma unroll
+          for (int q = 0; q < 4; ++q) D[q] = zf;
+          Db = zf;
+        }
+      }
+      if (j + kMfRing < kMfPass) {
+        const u32x4_t v =
+            __builtin_amdgcn_raw_buffer_load_b128(rb, voff + (uint32_t)(kb + kMfRing) * rstep, 0, 2);
+        w[j % kMfRing] = make_uint4(v.x, v.y, v.z, v.w);
+      }
+    }
+  }
+  // token rows 4lq + jj, columns col0 + 64 wave + 4 lr + q
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int t = 4 * lq + jj;
+    if (t < a.M) {
+      uint32_t o[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        o[h] = (uint32_t)f32_to_bf16(epilogue(y[2 * h][jj], a.cap)) |
+               ((uint32_t)f32_to_bf16(epilogue(y[2 * h + 1][jj], a.cap)) << 16);
+      *(uint2*)(a.C + (size_t)t * a.N + col0 + wave * 64 + 4 * lr) = make_uint2(o[0], o[1]);
+    }
+  }
+}
+
+bool mfma_path(int M, int K, int N, int gs, int G) {
+  if (M < 3 || M > kMfMaxM || K % 32 || (gs != 64 && gs != 128) || N % kMfCols || N / kMfCols < 256) return false;
+  // 32-bit buffer offsets, including reads past the last row of a pass
+  const long long kb_pad = (long long)(K / 32 + kMfPass - 1) / kMfPass * kMfPass;
+  if (kb_pad * 4 * N * 4 >= (1LL << 32)) return false;
+  const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)G * (kMfCols / 4) * 8;
+  return lds <= 64 * 1024;
+}
+
 constexpr size_t kAlign = 256;
 inline size_t round_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
@@ -240,6 +375,27 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     return fail(GI_ERR_INVALID_ARG, "w4a16: A and B_packed must be 16-byte aligned");
   if (((uintptr_t)scales) % 8) return fail(GI_ERR_INVALID_ARG, "w4a16: scales must be 8-byte aligned");
   if (M == 0) return GI_OK;
+  if (mfma_path(M, K, N, gs, n_groups)) {
+    MfArgs k{};
+    k.A = (const uint16_t*)A;
+    k.B = B;
+    k.S = (const uint16_t*)scales;
+    k.C = (uint16_t*)C;
+    k.M = M;
+    k.K = K;
+    k.N = N;
+    k.G = n_groups;
+    k.b_bytes = (uint32_t)((size_t)(K / 8) * N * 4);
+    k.cap = softcap;
+    const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)n_groups * (kMfCols / 4) * 8;
+    if (gs == 64)
+      hipLaunchKernelGGL(w4a16_mfma_kernel<2>, dim3(N / kMfCols), dim3(kMfThreads), lds, stream, k);
+    else
+      hipLaunchKernelGGL(w4a16_mfma_kernel<4>, dim3(N / kMfCols), dim3(kMfThreads), lds, stream, k);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "w4a16 matrix-core launch");
+    return GI_OK;
+  }
   const Plan p = make_plan(M, K, N);
   if (p.ks > 1) {
     if (!workspace || workspace_bytes < p.total)

@@ -61,6 +61,32 @@ def test_lm_head_softcap_column_subset():
     assert float(C.float().abs().max()) <= 30.0
 
 
+@pytest.mark.parametrize("m,gs,floor_groups,cap", [
+    (3, 128, False, None),   # fewest rows on the matrix-core path
+    (6, 64, False, 30.0),    # two k blocks per group, softcap
+    (16, 128, False, None),  # a full 16-row operand
+    (7, 128, True, None),    # floor-size scales: rows past the last group dropped
+])
+def test_w4a16_matrix_core_path(m, gs, floor_groups, cap):
+    """3 <= M <= 16 with N >= 65536 runs the matrix-core kernel: checked against
+    the float64 oracle on 1024 random columns of every 256-column tile shape."""
+    k, n = 2816 if not floor_groups else 2880, 65536
+    g = torch.Generator(device=DEV)
+    g.manual_seed(m * 7 + gs)
+    B = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), generator=g, device=DEV,
+                      dtype=torch.int64).to(torch.int32)
+    n_groups = k // gs if floor_groups else -(-k // gs)
+    S = (torch.randn((n_groups, n), generator=g, device=DEV).abs() * 0.02).to(torch.bfloat16)
+    A = synth.activations(m, k, seed=m).to(DEV)
+    C = ops.w4a16_linear(A, B, S, gs, softcap=cap) if cap else ops.w4a16_linear(A, B, S, gs)
+    cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:1024].sort().values
+    Bs, Ss = B[:, cols.to(DEV)].cpu(), S[:, cols.to(DEV)].cpu()
+    ref = O.w4a16_linear(np64(A), Bs.numpy(), np64(Ss), gs)
+    if cap:
+        ref = O.softcap(ref, cap)
+    assert_bf16_close(C[:, cols.to(DEV)], ref, f"matrix-core m={m} gs={gs} floor={floor_groups}")
+
+
 def test_companions_match_cpu_semantics():
     x = torch.randn(3, 2816).to(torch.bfloat16)
     w = torch.randn(2816).to(torch.bfloat16)
