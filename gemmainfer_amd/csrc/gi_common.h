@@ -77,14 +77,14 @@ __device__ __forceinline__ uint4 pair_permute(uint4 d) {
   return p;
 }
 
-// -136 * sum of the 8 bf16 values in d: the bias that turns sum x*(128+q)
+// -24 * sum of the 8 bf16 values in d: the bias that turns sum x*(16+q)
 // into sum x*(q-8) (see dot8_q4).
-__device__ __forceinline__ float neg_bias_136(uint4 d) {
+__device__ __forceinline__ float q4_bias(uint4 d) {
   float s = bf16_to_f32(d.x & 0xffffu) + bf16_to_f32(d.x >> 16) +
             bf16_to_f32(d.y & 0xffffu) + bf16_to_f32(d.y >> 16) +
             bf16_to_f32(d.z & 0xffffu) + bf16_to_f32(d.z >> 16) +
             bf16_to_f32(d.w & 0xffffu) + bf16_to_f32(d.w >> 16);
-  return -136.0f * s;
+  return -24.0f * s;
 }
 
 __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
@@ -93,32 +93,40 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
 }
 
 // sum_{i<8} x_i * (q_i - 8) for one packed word, given pair-permuted x and
-// bias = -136 * sum x_i.  A bf16 whose high byte is 0x43 and low byte is a
-// code q is exactly 128 + q (bf16 128.0 has unit spacing), so v_perm_b32 can
-// assemble two dequantised codes per instruction from the masked nibble bytes
-// and a register holding 0x43 bytes; each pair feeds one v_dot2_f32_bf16 and
-// the bias removes the 136 = 128 + 8 offset.  11 VALU ops per word.
-//   lo = w & 0x0F0F0F0F holds codes (q0, q2, q4, q6) in its bytes,
-//   hi = (w >> 4) & 0x0F0F0F0F holds (q1, q3, q5, q7).
-__device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias, uint32_t m43) {
-  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-  float d = fdot2(xp.x, __builtin_amdgcn_perm(m43, lo, 0x04020400u), bias);  // (q0, q4)
-  d = fdot2(xp.z, __builtin_amdgcn_perm(m43, lo, 0x04030401u), d);           // (q2, q6)
-  d = fdot2(xp.y, __builtin_amdgcn_perm(m43, hi, 0x04020400u), d);           // (q1, q5)
-  d = fdot2(xp.w, __builtin_amdgcn_perm(m43, hi, 0x04030401u), d);           // (q3, q7)
+// bias = -24 * sum x_i.  A bf16 whose high byte is 0x41 and low byte is
+// 0x80 | (q << 3) is exactly 16 + q (exponent 2^4, q in the top four mantissa
+// bits: unit spacing from 16 to 32), so v_perm_b32 can assemble two
+// dequantised codes per instruction from bytes holding 0x80 | q << 3 and a
+// register holding 0x41 bytes; each pair feeds one v_dot2_f32_bf16 and the
+// bias removes the 24 = 16 + 8 offset.  (A larger base such as 128 + q costs
+// precision: the fp32 sums carry base * sum x, which cancels.)
+//   lo = (w << 3) & 0x78787878 | 0x80808080 holds codes (q0, q2, q4, q6),
+//   hi = (w >> 1) & 0x78787878 | 0x80808080 holds (q1, q3, q5, q7).
+__device__ __forceinline__ void q4_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
+  lo = ((w << 3) & 0x78787878u) | 0x80808080u;
+  hi = ((w >> 1) & 0x78787878u) | 0x80808080u;
+}
+__device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias, uint32_t mq) {
+  uint32_t lo, hi;
+  q4_bytes(w, lo, hi);
+  float d = fdot2(xp.x, __builtin_amdgcn_perm(mq, lo, 0x04020400u), bias);  // (q0, q4)
+  d = fdot2(xp.z, __builtin_amdgcn_perm(mq, lo, 0x04030401u), d);           // (q2, q6)
+  d = fdot2(xp.y, __builtin_amdgcn_perm(mq, hi, 0x04020400u), d);           // (q1, q5)
+  d = fdot2(xp.w, __builtin_amdgcn_perm(mq, hi, 0x04030401u), d);           // (q3, q7)
   return d;
 }
 
 // The same product split in two, so that one unpacked word serves several
-// activation rows: unpack_q4 gives the four bf16 pairs (128+q) of dot8_q4,
+// activation rows: unpack_q4 gives the four bf16 pairs (16+q) of dot8_q4,
 // dot_unpacked takes them with one row's pair-permuted x and bias.
 struct Q4Pairs {
   uint32_t p0, p1, p2, p3;  // (q0,q4) (q2,q6) (q1,q5) (q3,q7)
 };
-__device__ __forceinline__ Q4Pairs unpack_q4(uint32_t w, uint32_t m43) {
-  const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-  return Q4Pairs{__builtin_amdgcn_perm(m43, lo, 0x04020400u), __builtin_amdgcn_perm(m43, lo, 0x04030401u),
-                 __builtin_amdgcn_perm(m43, hi, 0x04020400u), __builtin_amdgcn_perm(m43, hi, 0x04030401u)};
+__device__ __forceinline__ Q4Pairs unpack_q4(uint32_t w, uint32_t mq) {
+  uint32_t lo, hi;
+  q4_bytes(w, lo, hi);
+  return Q4Pairs{__builtin_amdgcn_perm(mq, lo, 0x04020400u), __builtin_amdgcn_perm(mq, lo, 0x04030401u),
+                 __builtin_amdgcn_perm(mq, hi, 0x04020400u), __builtin_amdgcn_perm(mq, hi, 0x04030401u)};
 }
 __device__ __forceinline__ float dot_unpacked(const Q4Pairs& d, uint4 xp, float bias) {
   float r = fdot2(xp.x, d.p0, bias);
@@ -127,9 +135,9 @@ __device__ __forceinline__ float dot_unpacked(const Q4Pairs& d, uint4 xp, float 
   return fdot2(xp.w, d.p3, r);
 }
 
-// 0x43434343 held in a VGPR (v_perm_b32 may read only one scalar operand).
-__device__ __forceinline__ uint32_t magic43() {
-  uint32_t v = 0x43434343u;
+// 0x41414141 held in a VGPR (v_perm_b32 may read only one scalar operand).
+__device__ __forceinline__ uint32_t q4_magic() {
+  uint32_t v = 0x41414141u;
   asm volatile("" : "+v"(v));
   return v;
 }

@@ -51,6 +51,11 @@ bool moe_decode_supported(const MoeHostArgs& h);
 int moe_decode_rows_per_launch(int top_k);
 size_t moe_decode_state_bytes();        // epochs + exchange buffers: kept between calls
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status);
+// prefill (moe_prefill.hip): sorted-by-expert grouped GEMM for M >= kPrefillMinRows
+constexpr int kPrefillMinRows = 64;
+bool moe_prefill_supported(const MoeHostArgs& h);
+size_t moe_prefill_workspace_bytes(int M, int top_k, int H, int I, int E);
+int launch_moe_prefill(const MoeHostArgs& h, void* ws, size_t ws_bytes);
 int launch_moe_align(const void* idx, int is64, int M, int top_k, int E, int32_t* uniq,
                      int32_t* nuniq, int32_t* s2u, int32_t* offsets, int32_t* slots,
                      hipStream_t stream);

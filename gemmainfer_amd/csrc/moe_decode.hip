@@ -363,9 +363,9 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
   const int u = item / a.Tk, c = item - u * a.Tk;
   const int kb0 = wave * KBW;
   const int kbpg_m1 = (1 << a.gsh) - 1;  // k blocks per scale group - 1
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 bc = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   f32x4_t D[4] = {zf, zf, zf, zf};
   f32x4_t Db = zf;
   float y[4][4];
@@ -378,11 +378,11 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
     const int kb = kb0 + j;
     const uint4 A = xrow[4 * kb];
     const uint4 w = opaque(b.w[j]);
-    D[0] = mfma_bf16(A, q4_operand(w.x, m43), D[0]);
-    D[1] = mfma_bf16(A, q4_operand(w.y, m43), D[1]);
-    D[2] = mfma_bf16(A, q4_operand(w.z, m43), D[2]);
-    D[3] = mfma_bf16(A, q4_operand(w.w, m43), D[3]);
-    Db = mfma_bf16(A, bc, Db);  // -136 * sum of each row's x over the k block
+    D[0] = mfma_bf16(A, q4_operand(w.x, mq), D[0]);
+    D[1] = mfma_bf16(A, q4_operand(w.y, mq), D[1]);
+    D[2] = mfma_bf16(A, q4_operand(w.z, mq), D[2]);
+    D[3] = mfma_bf16(A, q4_operand(w.w, mq), D[3]);
+    Db = mfma_bf16(A, bc, Db);  // -24 * sum of each row's x over the k block
     if (((kb + 1) & kbpg_m1) == 0 || j == KBW - 1) {  // a scale group ends here
       const int gi = min(kb >> a.gsh, a.Ggu - 1) - min(kb0 >> a.gsh, a.Ggu - 1);
       uint2 s2 = opaque(b.s[0]);
@@ -512,7 +512,7 @@ __host__ __device__ inline int blk_owner(int b, int NB, int G) { return ((b + 1)
 
 struct DnLds {
   uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16, k order); row S is zero
-  float* abias;   // [S + 1][I/8] -136 * sum of each chunk's 8 values
+  float* abias;   // [S + 1][I/8] -24 * sum of each chunk's 8 values
   uint32_t* dsc;  // [block of the workgroup][Gd][16] bf16 scale pairs of each lane's two columns
   float* red;     // [2][kWaves][kRows][32] per-wave output sums (aliases sact once it is consumed)
   float* pbuf;    // [kPartSlots][kRows][32] partial sums of a unit's other workgroups (after red)
@@ -544,7 +544,7 @@ __device__ __forceinline__ bool chunk_ready(const uint4 v) {
   return min(min(a0, a1), min(a2, a3)) != 0u;
 }
 
-// sum of the 8 values of a staged chunk (in matrix-core k order) times 128+q,
+// sum of the 8 values of a staged chunk (in matrix-core k order) times 16+q,
 // for one unpacked word: A.x holds (x0, x4), A.y (x2, x6), A.z (x1, x5), A.w
 // (x3, x7), the order of unpack_q4's pairs.
 __device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, float c) {
@@ -642,13 +642,13 @@ __device__ __forceinline__ uint32_t dn_chunk(uint32_t ci, int j, int nkb, uint32
 
 
 // A down word (columns 2lr, 2lr+1) as the products take it: packed (unpacked
-// where it is used) or already unpacked into bf16 pairs 128 + q.
+// where it is used) or already unpacked into bf16 pairs 16 + q.
 struct DnQ {
   Q4Pairs q[2];
 };
-__device__ __forceinline__ void dn_unpack(const uint2 w, uint32_t m43, Q4Pairs (&q)[2]) {
-  q[0] = unpack_q4(w.x, m43);
-  q[1] = unpack_q4(w.y, m43);
+__device__ __forceinline__ void dn_unpack(const uint2 w, uint32_t mq, Q4Pairs (&q)[2]) {
+  q[0] = unpack_q4(w.x, mq);
+  q[1] = unpack_q4(w.y, mq);
 }
 __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2]) {
   q[0] = w.q[0];
@@ -658,7 +658,7 @@ __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2
 // One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
 // workgroup (all of one unit).  Lane (lq, lr) takes columns 2lr, 2lr+1 at
 // packed row 4kb + lq, i.e. one 8-value chunk of each token's activation
-// row; the chunk's -136 offset sum comes precomputed from LDS.  Each k block
+// row; the chunk's -24 offset sum comes precomputed from LDS.  Each k block
 // and token has its own dot chain; the first SPLIT of a wave's k blocks
 // belong to one scale group, the rest to the next.  The four lq lanes are
 // added at the end.
@@ -668,7 +668,7 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
                                         const W (&dw)[BPW][kDownKpw], float (&acc)[NT][2]) {
   constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
   const uint32_t zc = (uint32_t)(a.S * cps);  // the zero row
   const int u_base = dp.blo - dp.d_a * U;     // expert of block 0
@@ -682,7 +682,7 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
         Q4Pairs q[2];
-        dn_unpack(dw[e][j], m43, q);
+        dn_unpack(dw[e][j], mq, q);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
@@ -716,7 +716,7 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 // Three tokens or more: matrix-core products, A rows = tokens (row lr is
 // token lr's chunk when lr < M and the token is routed to the expert, else
 // the zero row), B = the unpacked words (columns 2lr + h), one more product
-// with a constant -136 operand for the int4 offset, accumulated per scale
+// with a constant -24 operand for the int4 offset, accumulated per scale
 // group (the first SPLIT of the wave's k blocks, then the rest) and scaled
 // by the group scale and routing weight into acc[h] (rows 4lq + jj).
 template <int BPW, int SPLIT, bool FULL, class W>
@@ -726,9 +726,9 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
   constexpr int KPW = kDownKpw;
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
   const int cps = a.I >> 3;
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 bc = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
   const uint32_t zc = (uint32_t)(a.S * cps);
   const int u_base = dp.blo - dp.d_a * U;
@@ -752,7 +752,7 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
         const int sgi = j < SPLIT ? 0 : 1;
         const uint4 A = L.sact[dn_chunk<FULL>(x.ci[0], j, dp.nkb, zc)];
         Q4Pairs q[2];
-        dn_unpack(dw[e][j], m43, q);
+        dn_unpack(dw[e][j], mq, q);
         D[sgi][0] = mfma_bf16(A, make_uint4(q[0].p0, q[0].p1, q[0].p2, q[0].p3), D[sgi][0]);
         D[sgi][1] = mfma_bf16(A, make_uint4(q[1].p0, q[1].p1, q[1].p2, q[1].p3), D[sgi][1]);
         Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
@@ -838,7 +838,7 @@ __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, con
         if (chunk_ready(v)) {
           const uint4 x = make_uint4(~v.x, ~v.y, ~v.z, ~v.w);
           L.sact[g] = x;
-          if constexpr (BIAS) L.abias[g] = neg_bias_136(x);
+          if constexpr (BIAS) L.abias[g] = q4_bias(x);
           pending &= ~(1u << j);
         }
       }
@@ -971,12 +971,12 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   // (where the registers allow: one token, few blocks)
   DnQ dq[PRE ? BPW : 1][kDownKpw];
   if constexpr (PRE) {
-    const uint32_t m43 = magic43();
+    const uint32_t mq = q4_magic();
 #pragma unroll
     for (int e = 0; e < BPW; ++e)
 #pragma unroll
       for (int j = 0; j < kDownKpw; ++j) {
-        dn_unpack(dw0[e][j], m43, dq[e][j].q);
+        dn_unpack(dw0[e][j], mq, dq[e][j].q);
         // here, not next to the products: the unpacking overlaps the wait
 #pragma unroll
         for (int h = 0; h < 2; ++h)

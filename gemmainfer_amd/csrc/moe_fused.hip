@@ -85,10 +85,10 @@ template <int CG, int NT, int JGM, int CPR>
 struct TaskLds {
   static constexpr int T = 16 * CG, W = T / 64, DR = CG / 8, KPM = 32 * JGM;
   uint4* xs;        // [NT][KPM] pair-permuted x words
-  float* xb;        // [NT][KPM] -136 * sum of each x word
+  float* xb;        // [NT][KPM] -24 * sum of each x word
   float* red;       // [W][NT][2*CG] per-wave gate/up sums
   uint16_t* actp;   // [NT][DR][8] pair-permuted bf16 activations
-  float* actb;      // [NT][DR] -136 * sum of each activation row
+  float* actb;      // [NT][DR] -24 * sum of each activation row
 };
 
 struct Prologue {
@@ -353,7 +353,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
     __builtin_amdgcn_sched_barrier(0);
   };
   load_weights();
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
 
   // One chunk of NC (1..NT) of the expert's slots, straight-line for each NC.
   // The first chunk is peeled out of the loop below, so that its waits stay
@@ -369,7 +369,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
           const bool v = n < nch && r < Kv;
           const uint4 d = v ? xr[i] : make_uint4(0u, 0u, 0u, 0u);
           xs[n * KPM + r] = pair_permute(d);
-          xb[n * KPM + r] = neg_bias_136(d);
+          xb[n * KPM + r] = q4_bias(d);
         }
       }
     } else {
@@ -381,7 +381,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
           d = *(const uint4*)(a.x + (size_t)tok * a.H + 8 * r);
         }
         xs[n * KPM + r] = pair_permute(d);
-        xb[n * KPM + r] = neg_bias_136(d);
+        xb[n * KPM + r] = q4_bias(d);
       }
     }
     __syncthreads();
@@ -399,8 +399,8 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
       const uint2 s2 = opaque(sg[j]);
       const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
       const uint4 w = opaque(wv[j]);
-      const Q4Pairs d[4] = {unpack_q4(w.x, m43), unpack_q4(w.y, m43), unpack_q4(w.z, m43),
-                            unpack_q4(w.w, m43)};
+      const Q4Pairs d[4] = {unpack_q4(w.x, mq), unpack_q4(w.y, mq), unpack_q4(w.z, mq),
+                            unpack_q4(w.w, mq)};
 #pragma unroll
       for (int n = 0; n < NC; ++n) {
         const uint4 xp = xs[n * KPM + r];
@@ -440,7 +440,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
       s8 += __shfl_xor(s8, 4, kWave);
       const int r8 = ci >> 3, p = ci & 7;
       actp[(n * DR + r8) * 8 + 2 * (p & 3) + (p >> 2)] = f32_to_bf16(av);
-      if (p == 0) actb[n * DR + r8] = -136.0f * s8;
+      if (p == 0) actb[n * DR + r8] = -24.0f * s8;
     }
     __syncthreads();
 
@@ -462,8 +462,8 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
         }
         const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
         const uint4 w = opaque(dw[m][r]);
-        const Q4Pairs dq[4] = {unpack_q4(w.x, m43), unpack_q4(w.y, m43), unpack_q4(w.z, m43),
-                               unpack_q4(w.w, m43)};
+        const Q4Pairs dq[4] = {unpack_q4(w.x, mq), unpack_q4(w.y, mq), unpack_q4(w.z, mq),
+                               unpack_q4(w.w, mq)};
 #pragma unroll
         for (int n = 0; n < NC; ++n) {
           const uint4 xp = actq[n * DR + r];
@@ -632,10 +632,10 @@ __global__ __launch_bounds__(16 * CG) void fused_moe_kernel(Args a) {
 // Both projections run on v_mfma_f32_16x16x32_bf16, D[16x16] += A[16x32] *
 // B[32x16], lane l holding A[l%16][8(l/16)..+8), B[8(l/16)..+8][l%16] and
 // D[4(l/16)..+4][l%16].  B is the weights: one packed word per lane is
-// exactly 8 consecutive k of one output column, unpacked to bf16 (128+q)
+// exactly 8 consecutive k of one output column, unpacked to bf16 (16+q)
 // pairs in the order (0,4)(2,6)(1,5)(3,7).  A is the activations of up to 16
 // slots (rows), kept in LDS in that same k order.  A second product against a
-// constant -136 matrix supplies -136*sum(a), so D + Db = sum a*(q-8) exactly
+// constant -24 matrix supplies -24*sum(a), so D + Db = sum a*(q-8) exactly
 // as the fp32 accumulation of bf16 products; the group scale multiplies that
 // when a scale group ends.  Per packed word this is 7 VALU (the unpack),
 // whatever the number of tokens.
@@ -742,9 +742,9 @@ __device__ void run_task_mfma(const Args& a, Prologue& P, int u, int c, const ui
     __builtin_amdgcn_sched_barrier(0);
   };
   load_weights();
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const uint4 zero4 = make_uint4(0u, 0u, 0u, 0u);
-  const uint4 bneg = make_uint4(kNeg136Pair, kNeg136Pair, kNeg136Pair, kNeg136Pair);
+  const uint4 bneg = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = 0; c0 < nmatch; c0 += kChunkRows) {
@@ -768,10 +768,10 @@ __device__ void run_task_mfma(const Args& a, Prologue& P, int u, int c, const ui
       const int kb = kb0 + j;
       const uint4 A = a_ok ? xrow[4 * kb + lq] : zero4;
       const uint4 w = opaque(wv[j]);
-      D[0] = mfma_bf16(A, q4_operand(w.x, m43), D[0]);
-      D[1] = mfma_bf16(A, q4_operand(w.y, m43), D[1]);
-      D[2] = mfma_bf16(A, q4_operand(w.z, m43), D[2]);
-      D[3] = mfma_bf16(A, q4_operand(w.w, m43), D[3]);
+      D[0] = mfma_bf16(A, q4_operand(w.x, mq), D[0]);
+      D[1] = mfma_bf16(A, q4_operand(w.y, mq), D[1]);
+      D[2] = mfma_bf16(A, q4_operand(w.z, mq), D[2]);
+      D[3] = mfma_bf16(A, q4_operand(w.w, mq), D[3]);
       Db = mfma_bf16(A, bneg, Db);
       if (kb + 1 == next_end || j == KBW - 1) {  // a scale group ends here
         if (!sc_staged) {  // first group end of the wave: its scale loads (issued first) are in
@@ -836,10 +836,10 @@ __device__ void run_task_mfma(const Args& a, Prologue& P, int u, int c, const ui
       const int gc = wave * DGW + m;
       if (gc >= HG) break;
       const uint4 w = opaque(dw[m]);
-      const f32x4_t D0 = mfma_bf16(Ad, q4_operand(w.x, m43), zf);
-      const f32x4_t D1 = mfma_bf16(Ad, q4_operand(w.y, m43), zf);
-      const f32x4_t D2 = mfma_bf16(Ad, q4_operand(w.z, m43), zf);
-      const f32x4_t D3 = mfma_bf16(Ad, q4_operand(w.w, m43), zf);
+      const f32x4_t D0 = mfma_bf16(Ad, q4_operand(w.x, mq), zf);
+      const f32x4_t D1 = mfma_bf16(Ad, q4_operand(w.y, mq), zf);
+      const f32x4_t D2 = mfma_bf16(Ad, q4_operand(w.z, mq), zf);
+      const f32x4_t D3 = mfma_bf16(Ad, q4_operand(w.w, mq), zf);
       const uint2 s2 = opaque(sdw[m]);
       const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
       const int col = gc * 64 + tcol;
@@ -1111,8 +1111,14 @@ size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
   const int per = moe_rows_per_launch(top_k);
   int r = rows < per ? rows : per;
   if (r < 1) r = 1;
-  // the largest tile count any launch of this call may use
-  return ws_layout(r * top_k, H, I, kTaskCols).total;
+  // the largest tile count any launch of this call may use; many rows may
+  // take the grouped-GEMM prefill path instead
+  const WsLayout L = ws_layout(r * top_k, H, I, kTaskCols);
+  if (rows < kPrefillMinRows) return L.total;
+  // the prefill buffers follow the status word and the decode state, which
+  // later decode calls on the same workspace still need
+  const size_t pf = L.ctr + moe_prefill_workspace_bytes(rows, top_k, H, I, E);
+  return pf > L.total ? pf : L.total;
 }
 
 int launch_fused_moe(const MoeHostArgs& h) {
@@ -1131,6 +1137,10 @@ int launch_fused_moe(const MoeHostArgs& h) {
                 "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
   if (((uintptr_t)h.workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
+  if (moe_prefill_supported(h)) {
+    const size_t base = ws_layout(1, h.H, h.I, kTaskCols).ctr;  // past the status word and decode state
+    return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base);
+  }
   if (moe_decode_supported(h)) {
     // the same layout as the size query (gi_fused_moe_workspace_bytes)
     const int per = moe_rows_per_launch(h.top_k);

@@ -203,7 +203,7 @@ __device__ __forceinline__ void route_token_any(const A& a, int t, int lane, int
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kNeg136Pair = 0xC308C308u;  // bf16 -136, twice
+constexpr uint32_t kQ4BiasPair = 0xC1C0C1C0u;  // bf16 -24, twice: the offset of the 16+q operands
 
 __device__ __forceinline__ f32x4_t mfma_bf16(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -214,8 +214,8 @@ __device__ __forceinline__ uint4 mfma_k_order(uint4 d) {
   const uint4 p = pair_permute(d);
   return make_uint4(p.x, p.z, p.y, p.w);
 }
-__device__ __forceinline__ uint4 q4_operand(uint32_t w, uint32_t m43) {
-  const Q4Pairs q = unpack_q4(w, m43);
+__device__ __forceinline__ uint4 q4_operand(uint32_t w, uint32_t mq) {
+  const Q4Pairs q = unpack_q4(w, mq);
   return make_uint4(q.p0, q.p1, q.p2, q.p3);
 }
 // position of element p (0..7) of a packed row in that order

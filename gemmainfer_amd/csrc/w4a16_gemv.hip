@@ -70,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
   const int col = tile * kCols + colq * 4;
   const bool col_ok = col < a.N;
   const int steps = (nrows + kRowsPerStep - 1) / kRowsPerStep;
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const int nbatch = (steps + kBatch - 1) / kBatch;
 
   for (int t0 = 0; t0 < a.M; t0 += NT) {
@@ -80,7 +80,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
       const int n = i / nrows, r = i - n * nrows;
       const uint4 d = *(const uint4*)(a.A + (size_t)(t0 + n) * a.K + 8 * (r_begin + r));
       xs[n * a.stage_stride + r] = pair_permute(d);
-      xb[n * a.stage_stride + r] = neg_bias_136(d);
+      xb[n * a.stage_stride + r] = q4_bias(d);
     }
     __syncthreads();
 
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
               const uint4 xp = xs[n * a.stage_stride + rl];
               const float bias = xb[n * a.stage_stride + rl];
 #pragma unroll
-              for (int q = 0; q < 4; ++q) acc[q][n] += sv[q] * dot8_q4(wv[q], xp, bias, m43);
+              for (int q = 0; q < 4; ++q) acc[q][n] += sv[q] * dot8_q4(wv[q], xp, bias, mq);
             }
           }
         }
@@ -188,8 +188,8 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
 // Matrix-core path for a few token rows and a wide N (lm_head): with 3..16
 // rows the VALU dot products of the path above cost more than the weight
 // stream, so the products run on v_mfma_f32_16x16x32_bf16 with A = the token
-// rows (zero rows past M) and B = the unpacked int4 words (128 + q), plus one
-// product with a constant -136 operand per k block for the offset.  A
+// rows (zero rows past M) and B = the unpacked int4 words (16 + q), plus one
+// product with a constant -24 operand per k block for the offset.  A
 // workgroup owns 256 columns over all of K (wave w: 64 of them; lane
 // (lq, lr) loads the 16 bytes of columns 4lr..4lr+3 at packed row 4kb + lq,
 // i.e. the B operands of four 16-column products).  The weights stream
@@ -241,9 +241,9 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
   }
   __syncthreads();
 
-  const uint32_t m43 = magic43();
+  const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 bc = make_uint4(moe::kNeg136Pair, moe::kNeg136Pair, moe::kNeg136Pair, moe::kNeg136Pair);
+  const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
   const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
   const uint2* srow = ss + wave * 16 + lr;
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
@@ -265,10 +265,10 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
       if (kb < KB) {
         const uint4 A = xrow[4 * kb];
         const uint4 wv = w[j % kMfRing];
-        D[0] = moe::mfma_bf16(A, moe::q4_operand(wv.x, m43), D[0]);
-        D[1] = moe::mfma_bf16(A, moe::q4_operand(wv.y, m43), D[1]);
-        D[2] = moe::mfma_bf16(A, moe::q4_operand(wv.z, m43), D[2]);
-        D[3] = moe::mfma_bf16(A, moe::q4_operand(wv.w, m43), D[3]);
+        D[0] = moe::mfma_bf16(A, moe::q4_operand(wv.x, mq), D[0]);
+        D[1] = moe::mfma_bf16(A, moe::q4_operand(wv.y, mq), D[1]);
+        D[2] = moe::mfma_bf16(A, moe::q4_operand(wv.z, mq), D[2]);
+        D[3] = moe::mfma_bf16(A, moe::q4_operand(wv.w, mq), D[3]);
         Db = moe::mfma_bf16(A, bc, Db);
         // a group ends after k block kb (kMfPass is a multiple of KPG, so
         // groups never straddle passes), or K ends

@@ -185,10 +185,12 @@ def fused_batched_moe(x, gate_up_packed, gate_up_scales, down_packed, down_scale
 
 def moe_layer(x, router_logits, gate_up_packed, gate_up_scales, down_packed, down_scales,
               top_k, group_size, expert_scale=None, out=None, *, spin_limit: int = 0):
-    """Router tail + fused MoE in ONE launch (gemma.py:77-98).
+    """Router tail + fused MoE (gemma.py:77-98): one launch per 8 rows up to
+    63 rows, and from 64 rows the grouped-GEMM prefill path (routing, align,
+    gate/up, down and combine launches).
 
     Returns (out [M, H] bf16 -- overwritten, idx int32 [M, top_k],
-    weights bf16 [M, top_k]).  M * top_k must be <= 256.
+    weights bf16 [M, top_k]).
     """
     dev = _on_device(x, router_logits, gate_up_packed, gate_up_scales, down_packed, down_scales)
     _require_bf16(x, "moe_layer")
@@ -198,7 +200,6 @@ def moe_layer(x, router_logits, gate_up_packed, gate_up_scales, down_packed, dow
     _require(router_logits.dtype in (torch.bfloat16, torch.float32),
              "router_logits must be bf16 or fp32", TypeError)
     _require(0 < top_k <= min(e, 64), f"top_k must be in [1, min(E, 64)], got {top_k}")
-    _require(m * top_k <= 256, f"M*top_k must be <= 256 for the one-launch layer, got {m * top_k}")
     if expert_scale is not None:
         _on_device(x, expert_scale)
         _require(expert_scale.numel() == e, "expert_scale must have E elements")

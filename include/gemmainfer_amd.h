@@ -100,7 +100,11 @@ int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
  *   d_scales   bf16 [E, d_groups, H]
  *   idx        int32|int64 [M*top_k]  w  bf16|fp16|fp32 [M*top_k]
  *   out        bf16 [M, H]            accumulated into (caller zeroes it)
- * One kernel launch per 256/top_k rows.  Requirements: H % 8 == 0,
+ * One kernel launch per 256/top_k rows (8 rows on the decode kernel); from
+ * 64 rows with top_k <= 64, a power-of-two multiple of 32 as group size,
+ * H % 64 == 0 and I % 32 == 0, the grouped-GEMM prefill path (align,
+ * gate/up, down, combine launches; each active expert read once).
+ * Requirements: H % 8 == 0,
  * I % 8 == 0, H, I multiples of 4 columns, group_size % 8 == 0, E <= 1024,
  * top_k <= 256.  Deterministic (fixed-order fp32 reductions, no float
  * atomics): the same inputs give bitwise-identical outputs.
@@ -116,10 +120,13 @@ int gi_fused_batched_moe(const void* x, int x_dtype,
                          void* workspace, size_t workspace_bytes,
                          int spin_limit, void* stream);
 
-/* Router + fused MoE in one launch: logits [M, E] (bf16/fp32) are routed as
+/* Router + fused MoE: logits [M, E] (bf16/fp32) are routed as
  * gi_moe_route_topk_softmax does (weights rounded to bf16), out[M, H] is
  * OVERWRITTEN with the MoE output, and out_idx/out_w (may be NULL) receive
- * the routing.  M*top_k <= 256.                                             */
+ * the routing.  Up to 8 rows per launch; from 64 rows (group size a power of
+ * two times 32, H % 64 == 0, I % 32 == 0) the sorted-by-expert grouped-GEMM
+ * prefill path replaces the 8-row slices of gemma.py:99-112 (routing, align,
+ * gate/up, down, combine launches).                                         */
 int gi_moe_layer_from_logits(const void* x, int x_dtype,
                              const void* logits, int logits_dtype,
                              const float* expert_scale,

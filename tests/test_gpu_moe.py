@@ -172,6 +172,67 @@ def test_fused_gemma_shapes_gs128(gemma128, m, noise):
     print(f"m={m} U={al.num_unique} {stats}")
 
 
+@pytest.mark.parametrize("m", [64, 512])
+def test_prefill_grouped_gemm_gemma(gemma128, m):
+    """From 64 rows the sorted-by-expert grouped GEMM replaces the 8-row slices
+    (gemma.py:99-112): BASELINE config 3 at m=512, i.i.d. router logits."""
+    W, Wd = gemma128
+    x = synth.activations(m, 2816, seed=500 + m)
+    logits = synth.router_logits(m, 128, seed=500 + m)
+    idx, _, w = O.route_topk_softmax(np64(logits), 8)
+    idx_t = torch.from_numpy(idx)
+    w_t = torch.from_numpy(w).to(torch.bfloat16)
+    out_in = (torch.randn(m, 2816) * 0.1).to(torch.bfloat16)   # accumulated into
+    out = out_in.to(DEV).clone()
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx_t.to(DEV), w_t.to(DEV), out, 128)
+    ref, al = _oracle_moe(x, W, idx_t, w_t, out_in, 128)
+    stats = assert_bf16_close(out, ref, f"prefill m={m}")
+    print(f"m={m} U={al.num_unique} {stats}")
+
+
+def test_prefill_duplicates_invalid_skewed(small):
+    """Prefill path with duplicate ids inside a token, ids outside [0, E), int64
+    ids, fp32 weights and a skewed routing that puts > 32 pairs on one expert
+    (several 32-row passes of one expert's weights)."""
+    W, Wd = small
+    m = 96
+    g = torch.Generator().manual_seed(9)
+    idx = torch.randint(0, 8, (m, 4), generator=g, dtype=torch.int64)
+    idx[::3, 0] = 5                       # expert 5 gets > 64 pairs
+    idx[1::7, 1] = idx[1::7, 2]           # duplicates within a token
+    idx[2::11, 3] = -1                    # skipped slots
+    idx[4::13, 2] = 8                     # id == E: skipped
+    w = torch.rand(m, 4, generator=g)
+    x = synth.activations(m, 256, seed=12)
+    out = torch.zeros(m, 256, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(DEV), w.to(DEV), out, 64)
+    ref, _ = _oracle_moe(x, W, idx, w, torch.zeros(m, 256), 64)
+    assert_bf16_close(out, ref, "prefill duplicates/invalid")
+
+
+def test_prefill_layer_matches_oracle_and_is_deterministic(gemma128):
+    """Layer mode through the prefill path: routing bit-exact, output within
+    tolerance, and bitwise-identical across calls."""
+    W, Wd = gemma128
+    m = 100
+    x = synth.activations(m, 2816, seed=77)
+    logits = synth.router_logits(m, 128, seed=77)
+    outs = []
+    for _ in range(2):
+        out, idx, w = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"],
+                                    Wd["gate_up_scales"], Wd["down_packed"], Wd["down_scales"], 8, 128)
+        outs.append(out.clone())
+    ref_out, ref_idx, ref_w, _ = O.moe_layer_from_logits(
+        np64(x), np64(logits), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
+        W["down_packed"].numpy(), np64(W["down_scales"]), 8, 128)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+    np.testing.assert_allclose(np64(w), ref_w, rtol=2.0 ** -7)
+    assert_bf16_close(outs[0], ref_out, "prefill layer")
+    assert torch.equal(outs[0], outs[1])
+
+
 def test_layer_from_logits_gemma(gemma128):
     """Layer mode; 12 and 16 rows take several launches of up to 8 rows each."""
     W, Wd = gemma128
