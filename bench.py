@@ -217,6 +217,85 @@ def bench_config(m, noise, seed, copies, steps, warmup, device):
     }
 
 
+def prefill_flops(m, top_k=TOP_K, h=H, i=I):
+    """Multiply-adds x 2 of the expert products over every (token, slot) pair."""
+    return 2.0 * m * top_k * (h * 2 * i + i * h)
+
+
+class ChunkedRunner:
+    """The reference's chunked prefill (gemma.py:99-112): the layer on 8-row
+    slices, one decode-path launch per slice, on the same logits."""
+
+    def __init__(self, m, steps, copies, device):
+        self.full = LayerRunner(m, steps, copies, device)
+        self.lib = self.full.lib
+        nbytes = self.lib.gi_fused_moe_workspace_bytes(8, TOP_K, H, I, E)
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        self.dev = device
+        torch.cuda.synchronize()
+
+    def launch(self, s):
+        f = self.full
+        W = f.copies[f.copy_of[s]]
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        for r0 in range(0, f.m, 8):
+            st = self.lib.gi_moe_layer_from_logits(
+                p(f.x[r0:r0 + 8]), L.DTYPE_BF16, p(f.logits[s][r0:r0 + 8]), L.DTYPE_FP32, None,
+                p(W["gate_up_packed"]), p(W["gate_up_scales"]), W["gate_up_scales"].shape[1],
+                p(W["down_packed"]), p(W["down_scales"]), W["down_scales"].shape[1],
+                p(f.out[r0:r0 + 8]), p(f.idx[r0:r0 + 8]), p(f.w[r0:r0 + 8]), 8, H, I, E, TOP_K, GS,
+                p(self.ws), self.ws.numel(), 0, stream)
+            L.check(st, "gi_moe_layer_from_logits (8-row slice)")
+
+
+def bench_prefill(steps, warmup, device):
+    """the MoE layer at M=512 from i.i.d. N(0,1) router
+    logits, on the grouped-GEMM prefill path, beside the same layer as 64
+    decode-path launches of 8 rows (the reference's chunking)."""
+    m = 512
+    copies = [synth.device_moe_weights(E, H, I, GS, device, seed=100 + c) for c in range(COPIES)]
+    torch.cuda.synchronize()
+    desc = make_steps(m, 0.0, 3, warmup + steps)
+    runner = LayerRunner(m, desc, copies, device)
+    for i in range(warmup):
+        runner.launch(i)
+    torch.cuda.synchronize()
+    order = [warmup + i for i in range(steps)]
+    us = time_graph(runner, order, device)
+    chunked = ChunkedRunner(m, desc, copies, device)
+    ch_order = order[: max(4, steps // 10)]
+    for i in range(2):
+        chunked.launch(order[i])
+    torch.cuda.synchronize()
+    ch_us = time_graph(chunked, ch_order, device)
+    mean_u = statistics.fmean(desc[i]["U"] for i in order)
+    nbytes = mean_u * expert_bytes()
+    gbps = nbytes / (us * 1e-6) / 1e9
+    tflops = prefill_flops(m) / (us * 1e-6) / 1e12
+    return {
+        "metric": "chunked-prefill MoE layer us (M=512, configs[3]) + achieved HBM GB/s + MFMA utilisation (1 GPU)",
+        "value": us, "unit": "us", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": us / 1000.0, "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (N(0,1) bf16 activations, i.i.d. N(0,1) fp32 router logits, uniform int4 codes, "
+                "|N(0,1)|*0.02 bf16 scales)",
+        "config": {"workload": "MoE layer from logits at M=512: route, align, grouped gate_up, grouped down, "
+                               "combine (5 launches)", "M": m, "hidden": H, "experts": E, "top_k": TOP_K,
+                   "moe_intermediate": I, "group_size": GS, "weight_copies_rotated": COPIES,
+                   "timing": "HIP graph of K steps, HIP events"},
+        "unique_experts_mean": mean_u,
+        "algorithmic_bytes_per_layer": nbytes,
+        "gbps": gbps,
+        "tflops": tflops,
+        "mfma_util": tflops * 1e12 / 2.5e15,
+        "chunked_8row_us_per_layer": ch_us,
+        "speedup_vs_chunked": ch_us / us,
+        "roofline": {"bound": "hbm", "achieved": gbps, "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": gbps / PEAK_GBPS, "traffic": None},
+    }
+
+
 CALIB_BYTES = 256 << 20
 
 # Dense W4A16 workloads (BASELINE configs 0 and 4): (M, K, N, group, softcap, copies)
@@ -430,9 +509,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["moe", *LINEAR_WORKLOADS], default="moe",
-                    help="moe (default: the BASELINE metric, M=1 value with M=7 beside it) or a dense "
-                         "W4A16 shape (linear = configs[0], lm_head = configs[4])")
+    ap.add_argument("--workload", choices=["moe", "prefill", *LINEAR_WORKLOADS], default="moe",
+                    help="moe (default: the BASELINE metric, M=1 value with M=7 beside it), prefill "
+                         "(configs[3], M=512) or a dense W4A16 shape (linear = configs[0], "
+                         "lm_head = configs[4])")
     ap.add_argument("--pmc-reduce", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
                     help="reduce two --pmc-pass counter CSVs to per-launch HBM bytes (no GPU needed)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -451,6 +531,9 @@ def main():
         sys.exit(2)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.workload == "prefill":
+        print(json.dumps(bench_prefill(min(args.steps, 50), min(args.warmup, 5), device)))
+        return
     if args.workload != "moe":
         print(json.dumps(bench_linear(args.workload, args.steps, args.warmup, device,
                                       None if args.no_cpu_baseline else args.cpu_budget_s)))

@@ -37,11 +37,8 @@ namespace gi {
 namespace {
 
 using moe::f32x4_t;
-constexpr int kPThreads = 512;
-constexpr int kPWaves = kPThreads / kWave;
-constexpr int kPRT = 2;          // 16-token row tiles per pass
-constexpr int kPMaxKbw = 12;     // gate/up k blocks per wave: H <= 3072
-constexpr int kPMaxKbwD = 3;     // down k blocks per wave: I <= 768
+constexpr int kPThreads = 256;  // 4 waves x 64 columns
+constexpr int kPRT = 3;         // 16-token row tiles per pass
 constexpr int kAlignThreads = 1024;
 constexpr uint32_t kOob = 0xFFFFFFF0u;
 
@@ -112,238 +109,209 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// gate/up
+// grouped products (gate/up and down share the structure)
 // ---------------------------------------------------------------------------
-// x operand of one lane for row tile rt at k block kb: 16 bytes of its
-// token's row (zeros past the expert's pairs: offset past the resource).
-__device__ __forceinline__ uint4 x_operand(__amdgpu_buffer_rsrc_t rx, uint32_t row_off, int kb, int lq) {
+// A workgroup of 4 waves owns 256 output columns of one expert over all of K;
+// wave w owns 64 of them: lane (lq, lr) loads the 16 bytes of columns
+// 4lr..4lr+3 at packed row 4kb + lq, the B operands of four 16-column
+// products.  Each 16-token row tile of the expert's pairs is one A operand
+// (16 bytes of the lane's token row at k 32kb + 8lq .. +7, reordered to the
+// operand's k order).  Words and operands stream through a ring of kPRing
+// k blocks per wave, as straight-line code (PASS k blocks per pass; the loads
+// past K read an offset past the resource: zeros, no memory access), so every
+// wait has an exact count.  No cross-wave reduction: every wave covers all of
+// K.
+constexpr int kPRing = 3;    // k blocks in flight per wave
+constexpr int kPPass = 96;   // k blocks per straight-line pass, gate/up (H <= 3072 in one pass)
+constexpr int kPPassD = 24;  // the same, down (I <= 768 in one pass)
+
+// x operand of one lane for a row tile at k block kb: 16 bytes of its token's
+// row (zeros past the expert's pairs: offset past the resource).
+__device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int kb, int lq) {
   const uint32_t off = row_off == kOob ? kOob : row_off + (uint32_t)(32 * kb + 8 * lq) * 2u;
-  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-  return moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
-template <int KBW>
-__global__ __launch_bounds__(kPThreads) void prefill_gu_kernel(PfArgs a) {
-  __shared__ float red[kPWaves][16][64];
-  extern __shared__ uint2 gsc[];  // [Ggu][16]: scales of the lane's 4 columns (8 gate | 8 up lanes)
+// The products of one wave over k blocks [0, KB): y[rt][q] (rows 4lq + jj of
+// row tile rt, column 4lr + q of the wave's 64) = sum over groups of
+// scale * (D + Db).  Weights: rw/wbase (+ kb * wstep), activations: ra with
+// the lanes' row offsets, scales: sc_lds[g * 64 + 16 w + lr] (4 bf16).
+template <int PASS>
+__device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint32_t wbase, uint32_t wstep,
+                                                 uint32_t wsoff, __amdgpu_buffer_rsrc_t ra,
+                                                 const uint32_t (&roff)[kPRT], int KB, int G, int gsh,
+                                                 const uint2* sc_lds, f32x4_t (&y)[kPRT][4]) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
+  const int lq = lane >> 4, lr = lane & 15;
+  const uint32_t mq = q4_magic();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
+  const int kbpg_m1 = (1 << gsh) - 1;
+#pragma unroll
+  for (int rt = 0; rt < kPRT; ++rt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[rt][q] = zf;
+  for (int kp = 0; kp < KB; kp += PASS) {
+    uint4 wr[kPRing], ar[kPRing][kPRT];
+#pragma unroll
+    for (int s = 0; s < kPRing; ++s) {
+      const bool in = kp + s < KB;
+      const u32x4_t v =
+          __builtin_amdgcn_raw_buffer_load_b128(rw, in ? wbase + (uint32_t)(kp + s) * wstep : kOob, wsoff, 2);
+      wr[s] = make_uint4(v.x, v.y, v.z, v.w);
+#pragma unroll
+      for (int rt = 0; rt < kPRT; ++rt) ar[s][rt] = row_operand(ra, in ? roff[rt] : kOob, kp + s, lq);
+    }
+    f32x4_t D[kPRT][4], Db[kPRT];
+#pragma unroll
+    for (int rt = 0; rt < kPRT; ++rt) {
+      Db[rt] = zf;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) D[rt][q] = zf;
+    }
+#pragma unroll
+    for (int j = 0; j < PASS; ++j) {
+      const int kb = kp + j;
+      const int s = j % kPRing;
+      if (kb < KB) {
+        const uint4 w = wr[s];
+        const uint4 q0 = moe::q4_operand(w.x, mq), q1 = moe::q4_operand(w.y, mq);
+        const uint4 q2 = moe::q4_operand(w.z, mq), q3 = moe::q4_operand(w.w, mq);
+#pragma unroll
+        for (int rt = 0; rt < kPRT; ++rt) {
+          const uint4 A = moe::mfma_k_order(ar[s][rt]);
+          D[rt][0] = moe::mfma_bf16(A, q0, D[rt][0]);
+          D[rt][1] = moe::mfma_bf16(A, q1, D[rt][1]);
+          D[rt][2] = moe::mfma_bf16(A, q2, D[rt][2]);
+          D[rt][3] = moe::mfma_bf16(A, q3, D[rt][3]);
+          Db[rt] = moe::mfma_bf16(A, bc, Db[rt]);
+        }
+        // a group ends after kb (PASS is a multiple of every group's k
+        // blocks), or K ends
+        if ((kb & kbpg_m1) == kbpg_m1 || kb == KB - 1) {
+          const int g = kb >> gsh;
+          if (g < G) {
+            const uint2 sv = sc_lds[g * 64 + 16 * wave + lr];
+            const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
+#pragma unroll
+            for (int rt = 0; rt < kPRT; ++rt)
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
+          }
+#pragma unroll
+          for (int rt = 0; rt < kPRT; ++rt) {
+            Db[rt] = zf;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) D[rt][q] = zf;
+          }
+        }
+      }
+      if (j + kPRing < PASS) {
+        const bool in = kb + kPRing < KB;
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+            rw, in ? wbase + (uint32_t)(kb + kPRing) * wstep : kOob, wsoff, 2);
+        wr[s] = make_uint4(v.x, v.y, v.z, v.w);
+#pragma unroll
+        for (int rt = 0; rt < kPRT; ++rt) ar[s][rt] = row_operand(ra, in ? roff[rt] : kOob, kb + kPRing, lq);
+      }
+    }
+  }
+}
+
+// gate/up: workgroup (tile t, expert e) owns gate columns [128t, 128t+128)
+// (waves 0, 1) and the same up columns (waves 2, 3); act = bf16(gelu(g)*u).
+__global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
+  __shared__ float yb[16][256];   // one row tile's gate | up sums
+  extern __shared__ uint2 gsc[];  // [Ggu][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const int tile = blockIdx.x, e = blockIdx.y;
   const int off_e = a.offsets[e], n_e = a.offsets[e + 1] - off_e;
   if (n_e <= 0) return;
   const int twoI = 2 * a.I;
-  const int KB = a.H >> 5;
-  const int kb0 = wave * KB / kPWaves, nkb = (wave + 1) * KB / kPWaves - kb0;
-  const int col = (lr < 8 ? 0 : a.I) + 32 * tile + 4 * (lr & 7);
-  for (int i = tid; i < a.Ggu * 16; i += kPThreads) {
-    const int g = i >> 4, l = i & 15;
-    const int c2 = (l < 8 ? 0 : a.I) + 32 * tile + 4 * (l & 7);
-    gsc[i] = *(const uint2*)(a.gus + ((size_t)e * a.Ggu + g) * twoI + c2);
+  // column of quad c (0..63) of this workgroup: waves 0-1 gate, 2-3 up
+  auto quad_col = [&](int c) { return (c < 32 ? 0 : a.I) + 128 * tile + 4 * (c & 31); };
+  for (int i = tid; i < a.Ggu * 64; i += kPThreads) {
+    const int g = i >> 6, c = i & 63;
+    const int col = quad_col(c);
+    gsc[i] = col + 4 <= twoI ? *(const uint2*)(a.gus + ((size_t)e * a.Ggu + g) * twoI + col) : make_uint2(0u, 0u);
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.gu, a.gu_total);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_bytes);
-  const uint32_t mq = q4_magic();
-  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
-  const int kbpg = 1 << a.gsh;
+  const int col = quad_col(16 * wave + lr);
+  const uint32_t wbase = ((uint32_t)lq * twoI + col) * 4u;
+  const uint32_t wstep = (uint32_t)twoI * 16u;  // 4 packed rows
   for (int base = 0; base < n_e; base += 16 * kPRT) {
-    // this wave's weight words (a fixed count: past its k blocks, zeros)
-    uint4 w[KBW];
-#pragma unroll
-    for (int j = 0; j < KBW; ++j) {
-      const uint32_t row = 4 * (kb0 + j) + lq;
-      const uint32_t off = j < nkb ? (row * twoI + col) * 4u : kOob;
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, off, e * a.gu_bytes, 2);
-      w[j] = make_uint4(v.x, v.y, v.z, v.w);
-    }
-    // the lanes' token rows of each row tile
-    uint32_t xoff[kPRT];
+    uint32_t roff[kPRT];
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       const int j = base + 16 * rt + lr;
-      xoff[rt] = j < n_e ? (uint32_t)(a.order[off_e + j] / a.top_k) * (uint32_t)a.H * 2u : kOob;
+      roff[rt] = j < n_e ? (uint32_t)(a.order[off_e + j] / a.top_k) * (uint32_t)a.H * 2u : kOob;
     }
-    f32x4_t y[kPRT][4], D[kPRT][4], Db[kPRT];
-#pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      Db[rt] = zf;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) y[rt][q] = D[rt][q] = zf;
-    }
-    uint4 A[kPRT];
-#pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) A[rt] = x_operand(rx, xoff[rt], kb0, lq);
-#pragma unroll
-    for (int j = 0; j < KBW; ++j) {
-      // the next k block's x goes out unconditionally (zeros past the
-      // wave's k blocks), so that every wait keeps an exact count
-      uint4 An[kPRT];
-#pragma unroll
-      for (int rt = 0; rt < kPRT; ++rt) An[rt] = x_operand(rx, j + 1 < nkb ? xoff[rt] : kOob, kb0 + j + 1, lq);
-      if (j < nkb) {
-        const int kb = kb0 + j;
-        const uint4 q0 = moe::q4_operand(w[j].x, mq), q1 = moe::q4_operand(w[j].y, mq);
-        const uint4 q2 = moe::q4_operand(w[j].z, mq), q3 = moe::q4_operand(w[j].w, mq);
-#pragma unroll
-        for (int rt = 0; rt < kPRT; ++rt) {
-          D[rt][0] = moe::mfma_bf16(A[rt], q0, D[rt][0]);
-          D[rt][1] = moe::mfma_bf16(A[rt], q1, D[rt][1]);
-          D[rt][2] = moe::mfma_bf16(A[rt], q2, D[rt][2]);
-          D[rt][3] = moe::mfma_bf16(A[rt], q3, D[rt][3]);
-          Db[rt] = moe::mfma_bf16(A[rt], bc, Db[rt]);
-        }
-        if (((kb + 1) & (kbpg - 1)) == 0 || j == nkb - 1) {
-          const int g = kb >> a.gsh;
-          if (g < a.Ggu) {
-            const uint2 sv = gsc[g * 16 + lr];
-            const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
-#pragma unroll
-            for (int rt = 0; rt < kPRT; ++rt)
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
-          }
-#pragma unroll
-          for (int rt = 0; rt < kPRT; ++rt) {
-            Db[rt] = zf;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) D[rt][q] = zf;
-          }
-        }
-      }
-#pragma unroll
-      for (int rt = 0; rt < kPRT; ++rt) A[rt] = An[rt];
-    }
-    // sums over the waves in wave order, then the activation, per row tile
+    f32x4_t y[kPRT][4];
+    grouped_products<kPPass>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, a.H >> 5, a.Ggu, a.gsh, gsc, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       __syncthreads();
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          red[wave][4 * lq + jj][(lr < 8 ? 0 : 32) + 4 * (lr & 7) + q] = y[rt][q][jj];
+        for (int jj = 0; jj < 4; ++jj) yb[4 * lq + jj][64 * wave + 4 * lr + q] = y[rt][q][jj];
       __syncthreads();
-      const int t = tid >> 5, ci = tid & 31;  // 16 tokens x 32 columns
-      const int j = base + 16 * rt + t;
-      if (j < n_e) {
-        float g = 0.f, u = 0.f;
-#pragma unroll
-        for (int w2 = 0; w2 < kPWaves; ++w2) {
-          g += red[w2][t][ci];
-          u += red[w2][t][32 + ci];
-        }
-        a.act[(size_t)(off_e + j) * a.I + 32 * tile + ci] = f32_to_bf16(gelu_tanh(g) * u);
+      for (int i = tid; i < 16 * 128; i += kPThreads) {
+        const int t = i >> 7, c = i & 127;
+        const int j = base + 16 * rt + t;
+        const int ic = 128 * tile + c;
+        if (j < n_e && ic < a.I)
+          a.act[(size_t)(off_e + j) * a.I + ic] = f32_to_bf16(gelu_tanh(yb[t][c]) * yb[t][128 + c]);
       }
     }
   }
 }
 
-// ---------------------------------------------------------------------------
-// down
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kPThreads) void prefill_down_kernel(PfArgs a) {
-  __shared__ float red[kPWaves][16][64];
-  extern __shared__ uint2 dsc[];  // [Gd][16]: scales of the lane's 4 columns
+// down: workgroup (unit d, expert e) owns output columns [256d, 256d+256);
+// y[pos] fp32 rows of the expert's pairs.
+__global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
+  extern __shared__ uint2 dsc[];  // [Gd][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const int unit = blockIdx.x, e = blockIdx.y;
   const int off_e = a.offsets[e], n_e = a.offsets[e + 1] - off_e;
   if (n_e <= 0) return;
-  const int KB = a.I >> 5;
-  const int kb0 = wave * KB / kPWaves, nkb = (wave + 1) * KB / kPWaves - kb0;
-  const int col = 64 * unit + 4 * lr;
-  for (int i = tid; i < a.Gd * 16; i += kPThreads) {
-    const int g = i >> 4, l = i & 15;
-    dsc[i] = *(const uint2*)(a.dns + ((size_t)e * a.Gd + g) * a.H + 64 * unit + 4 * l);
+  for (int i = tid; i < a.Gd * 64; i += kPThreads) {
+    const int g = i >> 6, c = i & 63;
+    const int col = 256 * unit + 4 * c;
+    dsc[i] = col + 4 <= a.H ? *(const uint2*)(a.dns + ((size_t)e * a.Gd + g) * a.H + col) : make_uint2(0u, 0u);
   }
   __syncthreads();
+  const int col = 256 * unit + 64 * wave + 4 * lr;
+  if (256 * unit + 64 * wave >= a.H) return;  // a partial last unit (no barrier follows)
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.dn, a.dn_total);
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.act, a.act_bytes);
-  const uint32_t mq = q4_magic();
-  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
-  const int kbpg = 1 << a.gsh;
+  const uint32_t wbase = ((uint32_t)lq * a.H + col) * 4u;
+  const uint32_t wstep = (uint32_t)a.H * 16u;
   for (int base = 0; base < n_e; base += 16 * kPRT) {
-    uint4 w[kPMaxKbwD];
-#pragma unroll
-    for (int j = 0; j < kPMaxKbwD; ++j) {
-      const uint32_t row = 4 * (kb0 + j) + lq;
-      const uint32_t off = j < nkb ? (row * (uint32_t)a.H + col) * 4u : kOob;
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, off, e * a.dn_bytes, 2);
-      w[j] = make_uint4(v.x, v.y, v.z, v.w);
-    }
-    uint4 A[kPMaxKbwD][kPRT];
+    uint32_t roff[kPRT];
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       const int j = base + 16 * rt + lr;
-      const uint32_t roff = j < n_e ? (uint32_t)(off_e + j) * (uint32_t)a.I * 2u : kOob;
-#pragma unroll
-      for (int jk = 0; jk < kPMaxKbwD; ++jk) A[jk][rt] = x_operand(ra, jk < nkb ? roff : kOob, kb0 + jk, lq);
+      roff[rt] = j < n_e ? (uint32_t)(off_e + j) * (uint32_t)a.I * 2u : kOob;
     }
-    f32x4_t y[kPRT][4], D[kPRT][4], Db[kPRT];
+    f32x4_t y[kPRT][4];
+    grouped_products<kPPassD>(rw, wbase, wstep, e * a.dn_bytes, ra, roff, a.I >> 5, a.Gd, a.gsh, dsc, y);
 #pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      Db[rt] = zf;
+    for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) y[rt][q] = D[rt][q] = zf;
-    }
-#pragma unroll
-    for (int j = 0; j < kPMaxKbwD; ++j) {
-      if (j < nkb) {
-        const int kb = kb0 + j;
-        const uint4 q0 = moe::q4_operand(w[j].x, mq), q1 = moe::q4_operand(w[j].y, mq);
-        const uint4 q2 = moe::q4_operand(w[j].z, mq), q3 = moe::q4_operand(w[j].w, mq);
-#pragma unroll
-        for (int rt = 0; rt < kPRT; ++rt) {
-          D[rt][0] = moe::mfma_bf16(A[j][rt], q0, D[rt][0]);
-          D[rt][1] = moe::mfma_bf16(A[j][rt], q1, D[rt][1]);
-          D[rt][2] = moe::mfma_bf16(A[j][rt], q2, D[rt][2]);
-          D[rt][3] = moe::mfma_bf16(A[j][rt], q3, D[rt][3]);
-          Db[rt] = moe::mfma_bf16(A[j][rt], bc, Db[rt]);
-        }
-        if (((kb + 1) & (kbpg - 1)) == 0 || j == nkb - 1) {
-          const int g = kb >> a.gsh;
-          if (g < a.Gd) {
-            const uint2 sv = dsc[g * 16 + lr];
-            const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
-#pragma unroll
-            for (int rt = 0; rt < kPRT; ++rt)
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
-          }
-#pragma unroll
-          for (int rt = 0; rt < kPRT; ++rt) {
-            Db[rt] = zf;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) D[rt][q] = zf;
-          }
-        }
+      for (int jj = 0; jj < 4; ++jj) {
+        const int j = base + 16 * rt + 4 * lq + jj;
+        if (j < n_e)
+          *(float4*)(a.y + (size_t)(off_e + j) * a.H + col) =
+              make_float4(y[rt][0][jj], y[rt][1][jj], y[rt][2][jj], y[rt][3][jj]);
       }
-    }
-#pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      __syncthreads();
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) red[wave][4 * lq + jj][4 * lr + q] = y[rt][q][jj];
-      __syncthreads();
-      for (int i = tid; i < 16 * 64; i += kPThreads) {
-        const int t = i >> 6, c = i & 63;
-        const int j = base + 16 * rt + t;
-        if (j < n_e) {
-          float s = 0.f;
-#pragma unroll
-          for (int w2 = 0; w2 < kPWaves; ++w2) s += red[w2][t][c];
-          a.y[(size_t)(off_e + j) * a.H + 64 * unit + c] = s;
-        }
-      }
-    }
   }
 }
 
@@ -410,13 +378,16 @@ int log2_exact(int v) {
 
 bool moe_prefill_supported(const MoeHostArgs& h) {
   if (h.M < kPrefillMinRows) return false;
-  if (h.H % 64 || h.I % 32 || h.H > 32 * kPWaves * kPMaxKbw || h.I > 32 * kPWaves * kPMaxKbwD) return false;
-  if (h.gs % 32 || log2_exact(h.gs / 32) < 0) return false;
+  if (h.H % 64 || h.I % 32) return false;
+  if (h.gs % 32 || log2_exact(h.gs / 32) < 0 || kPPassD % (h.gs / 32)) return false;
   if (h.top_k > 64 || h.E > 1024) return false;
   const long long P = (long long)h.M * h.top_k;
   // 32-bit buffer offsets
-  if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 >= (1LL << 32)) return false;
-  if ((long long)h.E * (h.I / 8) * h.H * 4 >= (1LL << 32)) return false;
+  // (reads past the last packed row of a pass stay below 2^32 too)
+  const long long kbp_gu = ((long long)h.H / 32 + kPPass - 1) / kPPass * kPPass;
+  const long long kbp_dn = ((long long)h.I / 32 + kPPassD - 1) / kPPassD * kPPassD;
+  if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 + kbp_gu * 4 * 2 * h.I * 4 >= (1LL << 32)) return false;
+  if ((long long)h.E * (h.I / 8) * h.H * 4 + kbp_dn * 4 * h.H * 4 >= (1LL << 32)) return false;
   if ((long long)h.M * h.H * 2 >= (1LL << 32) || P * h.I * 2 >= (1LL << 32)) return false;
   return P <= (1 << 20);
 }
@@ -480,12 +451,9 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   k.dn_bytes = (uint32_t)((size_t)(h.I / 8) * h.H * 4);
   k.dn_total = (uint32_t)((size_t)h.E * k.dn_bytes);
   k.act_bytes = (uint32_t)((size_t)P * h.I * 2);
-  const int kbw = (h.H / 32 + kPWaves - 1) / kPWaves;
-  const size_t gl = (size_t)h.Ggu * 16 * sizeof(uint2), dl = (size_t)h.Gd * 16 * sizeof(uint2);
-  const dim3 ggrid(h.I / 32, h.E), dgrid(h.H / 64, h.E);
-  if (kbw <= 4) hipLaunchKernelGGL(prefill_gu_kernel<4>, ggrid, dim3(kPThreads), gl, h.stream, k);
-  else if (kbw <= 8) hipLaunchKernelGGL(prefill_gu_kernel<8>, ggrid, dim3(kPThreads), gl, h.stream, k);
-  else hipLaunchKernelGGL(prefill_gu_kernel<kPMaxKbw>, ggrid, dim3(kPThreads), gl, h.stream, k);
+  const size_t gl = (size_t)h.Ggu * 64 * sizeof(uint2), dl = (size_t)h.Gd * 64 * sizeof(uint2);
+  const dim3 ggrid((h.I + 127) / 128, h.E), dgrid((h.H + 255) / 256, h.E);
+  hipLaunchKernelGGL(prefill_gu_kernel, ggrid, dim3(kPThreads), gl, h.stream, k);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill gate/up launch");
   hipLaunchKernelGGL(prefill_down_kernel, dgrid, dim3(kPThreads), dl, h.stream, k);
