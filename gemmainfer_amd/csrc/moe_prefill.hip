@@ -44,13 +44,14 @@ constexpr uint32_t kOob = 0xFFFFFFF0u;
 
 struct PfArgs {
   const uint16_t* x;
+  uint16_t* xk;        // [M][H] x with each 8-value chunk in the matrix-core k order
   const int32_t* gu;
   const uint16_t* gus;
   const int32_t* dn;
   const uint16_t* dns;
   const int* offsets;  // [E + 1]
   const int* order;    // [P] pair at each position
-  uint16_t* act;       // [P][I] bf16, positions in expert order
+  uint16_t* act;       // [P][I] bf16, positions in expert order, chunks in k order
   float* y;            // [P][H] fp32
   int M, H, I, E, top_k, Ggu, Gd, gsh;  // group size = 32 << gsh
   uint32_t x_bytes, gu_bytes, gu_total, dn_bytes, dn_total, act_bytes;
@@ -108,6 +109,13 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
   }
 }
 
+// x rows with every 8-value chunk in the matrix-core k order (one pass over x
+// instead of a reorder per product operand).
+__global__ __launch_bounds__(256) void prefill_xperm_kernel(const uint4* x, uint4* xk, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) xk[i] = moe::mfma_k_order(x[i]);
+}
+
 // ---------------------------------------------------------------------------
 // grouped products (gate/up and down share the structure)
 // ---------------------------------------------------------------------------
@@ -115,18 +123,22 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
 // wave w owns 64 of them: lane (lq, lr) loads the 16 bytes of columns
 // 4lr..4lr+3 at packed row 4kb + lq, the B operands of four 16-column
 // products.  Each 16-token row tile of the expert's pairs is one A operand
-// (16 bytes of the lane's token row at k 32kb + 8lq .. +7, reordered to the
-// operand's k order).  Words and operands stream through a ring of kPRing
-// k blocks per wave, as straight-line code (PASS k blocks per pass; the loads
-// past K read an offset past the resource: zeros, no memory access), so every
-// wait has an exact count.  No cross-wave reduction: every wave covers all of
-// K.
-constexpr int kPRing = 3;    // k blocks in flight per wave
+// (16 bytes of the lane's token row at k 32kb + 8lq .. +7; the rows are
+// stored in the operand's k order).  Every wave needs the same A operands, so
+// wave rt (< kPRT) loads row tile rt and stages it through a 3-slot LDS ring
+// (one barrier per k block) instead of each wave loading all of them.
+// Words and A tiles stream through register rings (straight-line code, PASS
+// k blocks per pass; loads past K read an offset past the resource: zeros,
+// no memory access), so every wait has an exact count.  No cross-wave
+// reduction: every wave covers all of K.
+constexpr int kPRing = 4;    // weight k blocks in flight per wave
+constexpr int kPRingA = 3;   // A tiles in flight per loading wave
+constexpr int kPSlots = 3;   // LDS slots of staged A tiles
 constexpr int kPPass = 96;   // k blocks per straight-line pass, gate/up (H <= 3072 in one pass)
 constexpr int kPPassD = 24;  // the same, down (I <= 768 in one pass)
 
-// x operand of one lane for a row tile at k block kb: 16 bytes of its token's
-// row (zeros past the expert's pairs: offset past the resource).
+// 16 bytes of a lane's row at k block kb (zeros past the expert's pairs or
+// past K: offset past the resource).
 __device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int kb, int lq) {
   const uint32_t off = row_off == kOob ? kOob : row_off + (uint32_t)(32 * kb + 8 * lq) * 2u;
   const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
@@ -136,33 +148,39 @@ __device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t 
 // The products of one wave over k blocks [0, KB): y[rt][q] (rows 4lq + jj of
 // row tile rt, column 4lr + q of the wave's 64) = sum over groups of
 // scale * (D + Db).  Weights: rw/wbase (+ kb * wstep), activations: ra with
-// the lanes' row offsets, scales: sc_lds[g * 64 + 16 w + lr] (4 bf16).
+// this wave's own row tile offset (waves < kPRT), scales:
+// sc_lds[g * 64 + 16 w + lr] (4 bf16), aring: [kPSlots][kPRT][64] uint4.
 template <int PASS>
 __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint32_t wbase, uint32_t wstep,
-                                                 uint32_t wsoff, __amdgpu_buffer_rsrc_t ra,
-                                                 const uint32_t (&roff)[kPRT], int KB, int G, int gsh,
-                                                 const uint2* sc_lds, f32x4_t (&y)[kPRT][4]) {
+                                                 uint32_t wsoff, __amdgpu_buffer_rsrc_t ra, uint32_t roff_own,
+                                                 int n_rt, int KB, int G, int gsh, const uint2* sc_lds,
+                                                 uint4* aring, f32x4_t (&y)[kPRT][4]) {
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int lq = lane >> 4, lr = lane & 15;
+  const bool loader = wave < kPRT;
   const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
   const int kbpg_m1 = (1 << gsh) - 1;
+  auto own = [&](int kb) { return kb < KB ? roff_own : kOob; };
+  auto wload = [&](int kb) {
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, kb < KB ? wbase + (uint32_t)kb * wstep : kOob,
+                                                            wsoff, 2);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  };
 #pragma unroll
   for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
     for (int q = 0; q < 4; ++q) y[rt][q] = zf;
   for (int kp = 0; kp < KB; kp += PASS) {
-    uint4 wr[kPRing], ar[kPRing][kPRT];
+    uint4 wr[kPRing], ar[kPRingA];
+    const uint4 a0 = row_operand(ra, own(kp), kp, lq);
 #pragma unroll
-    for (int s = 0; s < kPRing; ++s) {
-      const bool in = kp + s < KB;
-      const u32x4_t v =
-          __builtin_amdgcn_raw_buffer_load_b128(rw, in ? wbase + (uint32_t)(kp + s) * wstep : kOob, wsoff, 2);
-      wr[s] = make_uint4(v.x, v.y, v.z, v.w);
+    for (int s = 0; s < kPRingA; ++s) ar[s] = row_operand(ra, own(kp + 1 + s), kp + 1 + s, lq);
 #pragma unroll
-      for (int rt = 0; rt < kPRT; ++rt) ar[s][rt] = row_operand(ra, in ? roff[rt] : kOob, kp + s, lq);
-    }
+    for (int s = 0; s < kPRing; ++s) wr[s] = wload(kp + s);
+    __syncthreads();  // the previous pass's readers of the ring are done
+    if (loader) aring[wave * 64 + lane] = a0;
     f32x4_t D[kPRT][4], Db[kPRT];
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
@@ -173,50 +191,48 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
 #pragma unroll
     for (int j = 0; j < PASS; ++j) {
       const int kb = kp + j;
-      const int s = j % kPRing;
-      if (kb < KB) {
-        const uint4 w = wr[s];
-        const uint4 q0 = moe::q4_operand(w.x, mq), q1 = moe::q4_operand(w.y, mq);
-        const uint4 q2 = moe::q4_operand(w.z, mq), q3 = moe::q4_operand(w.w, mq);
+      if (kb >= KB) break;
+      // k block kb + 1 into the next LDS slot; its register slot reloads
+      if (loader) aring[(((j + 1) % kPSlots) * kPRT + wave) * 64 + lane] = ar[j % kPRingA];
+      ar[j % kPRingA] = row_operand(ra, own(kb + 1 + kPRingA), kb + 1 + kPRingA, lq);
+      lds_barrier();  // slot j % kPSlots is complete; nobody reads slot (j + 1) % kPSlots yet
+      const uint4 w = wr[j % kPRing];
+      const uint4 q0 = moe::q4_operand(w.x, mq), q1 = moe::q4_operand(w.y, mq);
+      const uint4 q2 = moe::q4_operand(w.z, mq), q3 = moe::q4_operand(w.w, mq);
 #pragma unroll
-        for (int rt = 0; rt < kPRT; ++rt) {
-          const uint4 A = moe::mfma_k_order(ar[s][rt]);
-          D[rt][0] = moe::mfma_bf16(A, q0, D[rt][0]);
-          D[rt][1] = moe::mfma_bf16(A, q1, D[rt][1]);
-          D[rt][2] = moe::mfma_bf16(A, q2, D[rt][2]);
-          D[rt][3] = moe::mfma_bf16(A, q3, D[rt][3]);
-          Db[rt] = moe::mfma_bf16(A, bc, Db[rt]);
-        }
-        // a group ends after kb (PASS is a multiple of every group's k
-        // blocks), or K ends
-        if ((kb & kbpg_m1) == kbpg_m1 || kb == KB - 1) {
-          const int g = kb >> gsh;
-          if (g < G) {
-            const uint2 sv = sc_lds[g * 64 + 16 * wave + lr];
-            const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
-#pragma unroll
-            for (int rt = 0; rt < kPRT; ++rt)
-#pragma unroll
-              for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
-          }
+      for (int rt = 0; rt < kPRT; ++rt) {
+        if (rt >= n_rt) break;  // row tiles past the expert's pairs
+        const uint4 A = aring[((j % kPSlots) * kPRT + rt) * 64 + lane];
+        D[rt][0] = moe::mfma_bf16(A, q0, D[rt][0]);
+        D[rt][1] = moe::mfma_bf16(A, q1, D[rt][1]);
+        D[rt][2] = moe::mfma_bf16(A, q2, D[rt][2]);
+        D[rt][3] = moe::mfma_bf16(A, q3, D[rt][3]);
+        Db[rt] = moe::mfma_bf16(A, bc, Db[rt]);
+      }
+      // a group ends after kb (PASS is a multiple of every group's k blocks),
+      // or K ends
+      if ((kb & kbpg_m1) == kbpg_m1 || kb == KB - 1) {
+        const int g = kb >> gsh;
+        if (g < G) {
+          const uint2 sv = sc_lds[g * 64 + 16 * wave + lr];
+          const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
 #pragma unroll
           for (int rt = 0; rt < kPRT; ++rt) {
-            Db[rt] = zf;
+            if (rt >= n_rt) break;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) D[rt][q] = zf;
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+              for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
           }
         }
-      }
-      if (j + kPRing < PASS) {
-        const bool in = kb + kPRing < KB;
-        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-            rw, in ? wbase + (uint32_t)(kb + kPRing) * wstep : kOob, wsoff, 2);
-        wr[s] = make_uint4(v.x, v.y, v.z, v.w);
 #pragma unroll
-        for (int rt = 0; rt < kPRT; ++rt) ar[s][rt] = row_operand(ra, in ? roff[rt] : kOob, kb + kPRing, lq);
+        for (int rt = 0; rt < kPRT; ++rt) {
+          Db[rt] = zf;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) D[rt][q] = zf;
+        }
       }
+      wr[j % kPRing] = wload(kb + kPRing);
     }
   }
 }
@@ -225,6 +241,7 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
 // (waves 0, 1) and the same up columns (waves 2, 3); act = bf16(gelu(g)*u).
 __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
   __shared__ float yb[16][256];   // one row tile's gate | up sums
+  __shared__ uint4 aring[kPSlots * kPRT * 64];
   extern __shared__ uint2 gsc[];  // [Ggu][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
@@ -241,19 +258,19 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
   }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.gu, a.gu_total);
-  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.xk, a.x_bytes);
   const int col = quad_col(16 * wave + lr);
   const uint32_t wbase = ((uint32_t)lq * twoI + col) * 4u;
   const uint32_t wstep = (uint32_t)twoI * 16u;  // 4 packed rows
   for (int base = 0; base < n_e; base += 16 * kPRT) {
-    uint32_t roff[kPRT];
-#pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      const int j = base + 16 * rt + lr;
-      roff[rt] = j < n_e ? (uint32_t)(a.order[off_e + j] / a.top_k) * (uint32_t)a.H * 2u : kOob;
-    }
+    // this wave's row tile (waves < kPRT load the A operands for all)
+    const int jo = base + 16 * wave + lr;
+    const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(a.order[off_e + jo] / a.top_k) * (uint32_t)a.H * 2u
+                                                 : kOob;
     f32x4_t y[kPRT][4];
-    grouped_products<kPPass>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, a.H >> 5, a.Ggu, a.gsh, gsc, y);
+    const int n_rt = min(kPRT, (n_e - base + 15) >> 4);
+    grouped_products<kPPass>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, n_rt, a.H >> 5, a.Ggu, a.gsh, gsc, aring,
+                             y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       __syncthreads();
@@ -267,7 +284,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
         const int j = base + 16 * rt + t;
         const int ic = 128 * tile + c;
         if (j < n_e && ic < a.I)
-          a.act[(size_t)(off_e + j) * a.I + ic] = f32_to_bf16(gelu_tanh(yb[t][c]) * yb[t][128 + c]);
+          a.act[(size_t)(off_e + j) * a.I + (ic & ~7) + moe::mfma_k_pos(ic & 7)] =
+              f32_to_bf16(gelu_tanh(yb[t][c]) * yb[t][128 + c]);
       }
     }
   }
@@ -276,6 +294,7 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
 // down: workgroup (unit d, expert e) owns output columns [256d, 256d+256);
 // y[pos] fp32 rows of the expert's pairs.
 __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
+  __shared__ uint4 aring[kPSlots * kPRT * 64];
   extern __shared__ uint2 dsc[];  // [Gd][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
@@ -289,26 +308,24 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
   }
   __syncthreads();
   const int col = 256 * unit + 64 * wave + 4 * lr;
-  if (256 * unit + 64 * wave >= a.H) return;  // a partial last unit (no barrier follows)
+  const bool live = 256 * unit + 64 * wave < a.H;  // a partial last unit: the wave still joins the barriers
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.dn, a.dn_total);
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.act, a.act_bytes);
   const uint32_t wbase = ((uint32_t)lq * a.H + col) * 4u;
   const uint32_t wstep = (uint32_t)a.H * 16u;
   for (int base = 0; base < n_e; base += 16 * kPRT) {
-    uint32_t roff[kPRT];
-#pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      const int j = base + 16 * rt + lr;
-      roff[rt] = j < n_e ? (uint32_t)(off_e + j) * (uint32_t)a.I * 2u : kOob;
-    }
+    const int jo = base + 16 * wave + lr;
+    const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(off_e + jo) * (uint32_t)a.I * 2u : kOob;
     f32x4_t y[kPRT][4];
-    grouped_products<kPPassD>(rw, wbase, wstep, e * a.dn_bytes, ra, roff, a.I >> 5, a.Gd, a.gsh, dsc, y);
+    const int n_rt = min(kPRT, (n_e - base + 15) >> 4);
+    grouped_products<kPPassD>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, n_rt, a.I >> 5, a.Gd, a.gsh,
+                              dsc, aring, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int j = base + 16 * rt + 4 * lq + jj;
-        if (j < n_e)
+        if (live && j < n_e)
           *(float4*)(a.y + (size_t)(off_e + j) * a.H + col) =
               make_float4(y[rt][0][jj], y[rt][1][jj], y[rt][2][jj], y[rt][3][jj]);
       }
@@ -351,7 +368,7 @@ constexpr size_t kPAlign = 256;
 inline size_t pround(size_t v) { return (v + kPAlign - 1) / kPAlign * kPAlign; }
 
 struct PfLayout {
-  size_t idx, w, offsets, order, posmap, wts, act, y, total;
+  size_t idx, w, offsets, order, posmap, wts, xk, act, y, total;
 };
 PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   const size_t P = (size_t)M * top_k;
@@ -362,7 +379,8 @@ PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   l.order = pround(l.offsets + (size_t)(E + 1) * 4);
   l.posmap = pround(l.order + P * 4);
   l.wts = pround(l.posmap + P * 4);
-  l.act = pround(l.wts + P * 4);
+  l.xk = pround(l.wts + P * 4);
+  l.act = pround(l.xk + (size_t)M * H * 2);
   l.y = pround(l.act + P * I * 2);
   l.total = pround(l.y + P * H * 4);
   return l;
@@ -429,6 +447,7 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
 
   PfArgs k{};
   k.x = (const uint16_t*)h.x;
+  k.xk = (uint16_t*)(ws + L.xk);
   k.gu = h.gu_packed;
   k.gus = (const uint16_t*)h.gu_scales;
   k.dn = h.d_packed;
@@ -451,6 +470,11 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   k.dn_bytes = (uint32_t)((size_t)(h.I / 8) * h.H * 4);
   k.dn_total = (uint32_t)((size_t)h.E * k.dn_bytes);
   k.act_bytes = (uint32_t)((size_t)P * h.I * 2);
+  const int nx = h.M * h.H / 8;
+  hipLaunchKernelGGL(prefill_xperm_kernel, dim3((nx + 255) / 256), dim3(256), 0, h.stream, (const uint4*)h.x,
+                     (uint4*)k.xk, nx);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_fail(e, "prefill x reorder launch");
   const size_t gl = (size_t)h.Ggu * 64 * sizeof(uint2), dl = (size_t)h.Gd * 64 * sizeof(uint2);
   const dim3 ggrid((h.I + 127) / 128, h.E), dgrid((h.H + 255) / 256, h.E);
   hipLaunchKernelGGL(prefill_gu_kernel, ggrid, dim3(kPThreads), gl, h.stream, k);
