@@ -84,6 +84,7 @@ constexpr int kDefaultSpin = 1 << 20;
 constexpr int kCpolNt = 2;            // non-temporal: weights are read once
 constexpr int kMaxItems = 9;          // gate/up items per workgroup and launch
 constexpr int kDownKpw = 3;           // down k blocks per wave: Tk <= 24 (I <= 768)
+constexpr int kDownPreMfma = 4;       // matrix-core path: blocks unpacked before the activations arrive
 constexpr int kMaxI = kCols * kDownKpw * kWaves;  // 768
 constexpr size_t kActParity = (size_t)kSlots * kMaxI * 2;  // bytes of one exchange buffer
 constexpr int kScaleLoads = 4;        // 16-byte down-scale chunks per thread (2048 per workgroup)
@@ -654,6 +655,27 @@ __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2
   q[0] = w.q[0];
   q[1] = w.q[1];
 }
+// The words of the first NPRE blocks already unpacked, the others packed.
+template <int BPW, int NPRE>
+struct DnMix {
+  const uint2 (&raw)[BPW][kDownKpw];
+  const DnQ (&pre)[NPRE][kDownKpw];
+};
+// word (block e, k block j) of either source; e is a constant once the block
+// loops are unrolled, so the choice costs nothing
+template <int B>
+__device__ __forceinline__ void dn_word(const uint2 (&dw)[B][kDownKpw], int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
+  dn_unpack(dw[e][j], mq, q);
+}
+template <int B>
+__device__ __forceinline__ void dn_word(const DnQ (&dw)[B][kDownKpw], int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
+  dn_unpack(dw[e][j], mq, q);
+}
+template <int B, int NPRE>
+__device__ __forceinline__ void dn_word(const DnMix<B, NPRE>& dw, int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
+  if (e < NPRE) dn_unpack(dw.pre[e < NPRE ? e : 0][j], mq, q);
+  else dn_unpack(dw.raw[e][j], mq, q);
+}
 
 // One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
 // workgroup (all of one unit).  Lane (lq, lr) takes columns 2lr, 2lr+1 at
@@ -665,7 +687,7 @@ __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2
 template <int BPW, int NT, int SPLIT, bool FULL, class W>
 __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                         int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                        const W (&dw)[BPW][kDownKpw], float (&acc)[NT][2]) {
+                                        const W& dw, float (&acc)[NT][2]) {
   constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
   const uint32_t mq = q4_magic();
@@ -682,7 +704,7 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
         Q4Pairs q[2];
-        dn_unpack(dw[e][j], mq, q);
+        dn_word(dw, e, j, mq, q);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
@@ -722,7 +744,7 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
 template <int BPW, int SPLIT, bool FULL, class W>
 __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                         int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                        const W (&dw)[BPW][kDownKpw], f32x4_t (&acc)[2]) {
+                                        const W& dw, f32x4_t (&acc)[2]) {
   constexpr int KPW = kDownKpw;
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
   const int cps = a.I >> 3;
@@ -752,7 +774,7 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
         const int sgi = j < SPLIT ? 0 : 1;
         const uint4 A = L.sact[dn_chunk<FULL>(x.ci[0], j, dp.nkb, zc)];
         Q4Pairs q[2];
-        dn_unpack(dw[e][j], mq, q);
+        dn_word(dw, e, j, mq, q);
         D[sgi][0] = mfma_bf16(A, make_uint4(q[0].p0, q[0].p1, q[0].p2, q[0].p3), D[sgi][0]);
         D[sgi][1] = mfma_bf16(A, make_uint4(q[1].p0, q[1].p1, q[1].p2, q[1].p3), D[sgi][1]);
         Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
@@ -778,7 +800,7 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
 template <int BPW, int MODE, int SPLIT, class W>
 __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                              int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                             const W (&dw)[BPW][kDownKpw], float (&accv)[MODE > 0 ? MODE : 1][2],
+                                             const W& dw, float (&accv)[MODE > 0 ? MODE : 1][2],
                                              f32x4_t (&accm)[2]) {
   constexpr int NT = MODE > 0 ? MODE : 1;
   if (dp.nkb == kDownKpw) {
@@ -791,7 +813,7 @@ __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue
 }
 template <int BPW, int MODE, class W>
 __device__ __forceinline__ void dn_run(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v, int tm_v,
-                                       int U, const DnPlan& dp, int e_lo, int e_hi, const W (&dw)[BPW][kDownKpw],
+                                       int U, const DnPlan& dp, int e_lo, int e_hi, const W& dw,
                                        float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   const int split = min(kDownKpw, (1 << a.gsh) - (dp.kbw0 & ((1 << a.gsh) - 1)));
   if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
@@ -967,13 +989,15 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   c1 = uniform(c1);
   x0 = uniform(x0);
   x1 = uniform(x1);
-  // the first batch's words unpacked while the activations are on their way
-  // (where the registers allow: one token, few blocks)
-  DnQ dq[PRE ? BPW : 1][kDownKpw];
-  if constexpr (PRE) {
+  // the first batch's words unpacked while the activations are on their way,
+  // where the registers allow: every block with one token and few blocks,
+  // the first kDownPreMfma blocks on the matrix-core path
+  constexpr int NPRE = PRE ? BPW : (MODE == 0 ? (BPW < kDownPreMfma ? BPW : kDownPreMfma) : 0);
+  DnQ dq[NPRE > 0 ? NPRE : 1][kDownKpw];
+  if constexpr (NPRE > 0) {
     const uint32_t mq = q4_magic();
 #pragma unroll
-    for (int e = 0; e < BPW; ++e)
+    for (int e = 0; e < NPRE; ++e)
 #pragma unroll
       for (int j = 0; j < kDownKpw; ++j) {
         dn_unpack(dw0[e][j], mq, dq[e][j].q);
@@ -1005,9 +1029,13 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   dp.nb = min(nb_all, BPW);
   dp.d_a = d_first;
   dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
-  if constexpr (PRE) {
+  if constexpr (NPRE == BPW) {
     dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, accv[0], accm[0]);
     if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, accv[1], accm[1]);
+  } else if constexpr (NPRE > 0) {
+    const DnMix<BPW, NPRE> mix{dw0, dq};
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, mix, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, mix, accv[1], accm[1]);
   } else {
     dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, accv[0], accm[0]);
     if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, accv[1], accm[1]);
