@@ -633,6 +633,36 @@ __device__ __forceinline__ DnBlock<NT> dn_block(const DecArgs& a, const DecProlo
   return x;
 }
 
+// The VALU path's per-block inputs in the form the products use (scales as
+// floats), built for a whole batch before the activations arrive.
+template <int NT>
+struct DnBlockF {
+  uint32_t ci[NT];
+  float wt[NT];
+  float s[4];  // first group (columns 2lr, 2lr+1), second group
+};
+template <int BPW, int NT>
+__device__ __forceinline__ void dn_blocks_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
+                                               int tm_v, int U, const DnPlan& dp, DnBlockF<NT> (&xb)[BPW]) {
+  const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + kDownKpw - 1) >> a.gsh, a.Gd - 1);
+  const int u_base = dp.blo - dp.d_a * U;
+#pragma unroll
+  for (int e = 0; e < BPW; ++e) {
+    int u = u_base + e;
+    if (u >= U) u -= U;
+    const DnBlock<NT> x = dn_block<NT, false>(a, P, L, epos_v, tm_v, u, dp.e_off + e, e < dp.nb, dp.kbw0, g1, g2);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      xb[e].ci[t] = x.ci[t];
+      xb[e].wt[t] = x.wt[t];
+    }
+    xb[e].s[0] = bf16lo(x.s1);
+    xb[e].s[1] = bf16hi(x.s1);
+    xb[e].s[2] = bf16lo(x.s2);
+    xb[e].s[3] = bf16hi(x.s2);
+  }
+}
+
 // Chunk j of a wave's k blocks (the zero row past the wave's count unless
 // every wave has KPW blocks).
 template <bool FULL>
@@ -685,21 +715,16 @@ __device__ __forceinline__ void dn_word(const DnMix<B, NPRE>& dw, int e, int j, 
 // belong to one scale group, the rest to the next.  The four lq lanes are
 // added at the end.
 template <int BPW, int NT, int SPLIT, bool FULL, class W>
-__device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
-                                        int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                        const W& dw, float (&acc)[NT][2]) {
+__device__ __forceinline__ void dn_valu(const DecArgs& a, const DnLds& L, const DnPlan& dp, int e_lo, int e_hi,
+                                        const W& dw, const DnBlockF<NT> (&xb)[BPW], float (&acc)[NT][2]) {
   constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
   const uint32_t mq = q4_magic();
-  const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
   const uint32_t zc = (uint32_t)(a.S * cps);  // the zero row
-  const int u_base = dp.blo - dp.d_a * U;     // expert of block 0
 #pragma unroll
   for (int e = 0; e < BPW; ++e) {
     if (e >= e_lo && e < e_hi) {
-      int u = u_base + e;
-      if (u >= U) u -= U;
-      const DnBlock<NT> x = dn_block<NT, false>(a, P, L, epos_v, tm_v, u, dp.e_off + e, true, dp.kbw0, g1, g2);
+      const DnBlockF<NT>& x = xb[e];
       float d[KPW][NT][2];
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
@@ -718,16 +743,14 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DecPrologue& P, 
       for (int t = 0; t < NT; ++t) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
-          const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
           // segment sums: k block 0 is always in the first group, block
           // KPW-1 in the second unless SPLIT == KPW
           float v1 = d[0][t][h], v2 = d[KPW - 1][t][h];
 #pragma unroll
           for (int j = 1; j < KPW - 1; ++j) (j < SPLIT ? v1 : v2) += d[j][t][h];
           if constexpr (SPLIT == KPW) v1 += v2;
-          float v = sa * v1;
-          if constexpr (SPLIT < KPW) v += sb * v2;
+          float v = x.s[h] * v1;
+          if constexpr (SPLIT < KPW) v += x.s[2 + h] * v2;
           acc[t][h] += x.wt[t] * v;
         }
       }
@@ -799,26 +822,27 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
 // wave has all KPW k blocks.
 template <int BPW, int MODE, int SPLIT, class W>
 __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
-                                             int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
-                                             const W& dw, float (&accv)[MODE > 0 ? MODE : 1][2],
-                                             f32x4_t (&accm)[2]) {
+                                             int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi, const W& dw,
+                                             const DnBlockF<(MODE > 0 ? MODE : 1)> (&xb)[BPW],
+                                             float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   constexpr int NT = MODE > 0 ? MODE : 1;
   if (dp.nkb == kDownKpw) {
-    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, true>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv);
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, true>(a, L, dp, e_lo, e_hi, dw, xb, accv);
     else dn_mfma<BPW, SPLIT, true>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
   } else {
-    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv);
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, false>(a, L, dp, e_lo, e_hi, dw, xb, accv);
     else dn_mfma<BPW, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
   }
 }
 template <int BPW, int MODE, class W>
 __device__ __forceinline__ void dn_run(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v, int tm_v,
                                        int U, const DnPlan& dp, int e_lo, int e_hi, const W& dw,
+                                       const DnBlockF<(MODE > 0 ? MODE : 1)> (&xb)[BPW],
                                        float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   const int split = min(kDownKpw, (1 << a.gsh) - (dp.kbw0 & ((1 << a.gsh) - 1)));
-  if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
-  else if (split == 2) dn_run_split<BPW, MODE, 2>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
-  else dn_run_split<BPW, MODE, kDownKpw>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accv, accm);
+  if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
+  else if (split == 2) dn_run_split<BPW, MODE, 2>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
+  else dn_run_split<BPW, MODE, kDownKpw>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -1008,6 +1032,15 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
                        "+v"(dq[e][j].q[h].p3));
       }
   }
+  // batch 0: the words loaded with the gate/up items; on the VALU path its
+  // per-block inputs are built before the wait as well
+  dp.blo = blo;
+  dp.e_off = 0;
+  dp.nb = min(nb_all, BPW);
+  dp.d_a = d_first;
+  dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
+  DnBlockF<NT> xb[BPW];
+  if constexpr (MODE > 0) dn_blocks_valu<BPW, NT>(a, P, L, epos_v, tm_v, U, dp, xb);
   stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
   lds_barrier();
 
@@ -1022,24 +1055,18 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
 #pragma unroll
       for (int t = 0; t < NT; ++t) accv[p][t][h] = 0.f;
     }
-  // batch 0 from the words loaded with the gate/up items, then any further
-  // batches (more blocks than the registers hold)
-  dp.blo = blo;
-  dp.e_off = 0;
-  dp.nb = min(nb_all, BPW);
-  dp.d_a = d_first;
-  dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
   if constexpr (NPRE == BPW) {
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, accv[1], accm[1]);
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, xb, accv[1], accm[1]);
   } else if constexpr (NPRE > 0) {
     const DnMix<BPW, NPRE> mix{dw0, dq};
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, mix, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, mix, accv[1], accm[1]);
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, mix, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, mix, xb, accv[1], accm[1]);
   } else {
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, accv[1], accm[1]);
+    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, xb, accv[1], accm[1]);
   }
+  // further batches (more blocks than the registers hold)
   for (int b0 = blo + BPW; b0 < bhi; b0 += BPW) {
     dp.blo = b0;
     dp.e_off = b0 - blo;
@@ -1048,8 +1075,9 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     dp.n0 = max(0, min(dp.nb, (d_first + 1) * U - b0));
     uint2 dw[BPW][kDownKpw];
     dn_load<BPW>(a, uexp_v, U, dp, dw);
-    if (dp.n0 > 0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw, accv[1], accm[1]);
+    if constexpr (MODE > 0) dn_blocks_valu<BPW, NT>(a, P, L, epos_v, tm_v, U, dp, xb);
+    if (dp.n0 > 0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw, xb, accv[1], accm[1]);
   }
   // sums over the waves, fixed order (the per-wave sums alias the staged rows)
   lds_barrier();
