@@ -217,6 +217,77 @@ def bench_config(m, noise, seed, copies, steps, warmup, device):
     }
 
 
+class FrontEndRunner:
+    """Router front-end of one MoE block (gemma.py:75-76) three ways, each step
+    on one of COPIES gate copies in rotation: ``fused`` = gi_moe_router_logits
+    (one launch); ``torch`` = the module's statements as the reference runs
+    them on this build (the drop-in rmsnorm kernel, two bf16 elementwise
+    products, the bf16 nn.Linear); ``layer`` = gi_moe_layer_from_hidden, the
+    whole block (router launch + layer launch) on the expert weight copies."""
+
+    def __init__(self, m, copies, device, mode):
+        import gemmainfer_csrc  # noqa: PLC0415  (the drop-in module)
+        self.csrc = gemmainfer_csrc
+        self.lib = L.load()
+        self.m, self.dev, self.mode, self.copies = m, device, mode, copies
+        self.x = synth.activations(m, H, seed=9).to(device)
+        self.R = []
+        for c in range(COPIES):
+            r = synth.router_weights(E, H, seed=200 + c)
+            self.R.append({k: v.to(device) for k, v in r.items()})
+        self.logits = torch.empty(m, E, dtype=torch.bfloat16, device=device)
+        self.norm = torch.empty(m, H, dtype=torch.bfloat16, device=device)
+        self.out = torch.empty(m, H, dtype=torch.bfloat16, device=device)
+        self.idx = torch.empty(m, TOP_K, dtype=torch.int32, device=device)
+        self.w = torch.empty(m, TOP_K, dtype=torch.bfloat16, device=device)
+        self.es = [r["expert_scale"].float().contiguous() for r in self.R]
+        nbytes = self.lib.gi_fused_moe_workspace_bytes(m, TOP_K, H, I, E)
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        torch.cuda.synchronize()
+
+    def launch(self, s):
+        r = self.R[s % COPIES]
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        if self.mode == "fused":
+            L.check(self.lib.gi_moe_router_logits(p(self.x), L.DTYPE_BF16, p(r["router_scale"]),
+                                                  p(r["gate"]), 1e-6, p(self.logits), self.m, H, E,
+                                                  stream), "gi_moe_router_logits")
+        elif self.mode == "torch":
+            self.csrc.rmsnorm(self.x, torch.empty(0), self.norm, 1e-6, False)
+            xn = self.norm * (r["router_scale"] * (H ** -0.5))
+            self.logits = torch.nn.functional.linear(xn, r["gate"])
+        else:
+            W = self.copies[s % COPIES]
+            L.check(self.lib.gi_moe_layer_from_hidden(
+                p(self.x), L.DTYPE_BF16, p(r["router_scale"]), p(r["gate"]), 1e-6, p(self.logits),
+                p(self.es[s % COPIES]), p(W["gate_up_packed"]), p(W["gate_up_scales"]),
+                W["gate_up_scales"].shape[1], p(W["down_packed"]), p(W["down_scales"]),
+                W["down_scales"].shape[1], p(self.out), p(self.idx), p(self.w), self.m, H, I, E,
+                TOP_K, GS, p(self.ws), self.ws.numel(), 0, stream), "gi_moe_layer_from_hidden")
+
+
+def bench_front_end(copies, steps, device):
+    """us per router front-end (fused launch vs the torch statements) at M=1
+    and M=7, and the whole block from the hidden state at M=1."""
+    res = {}
+    n = min(steps, 200)
+    for m in (1, 7):
+        row = {}
+        for mode in ("fused", "torch"):
+            runner = FrontEndRunner(m, copies, device, mode)
+            for i in range(4):
+                runner.launch(i)
+            row[f"{mode}_us"] = time_graph(runner, list(range(n)), device)
+        res[f"M{m}"] = row
+    runner = FrontEndRunner(1, copies, device, "layer")
+    for i in range(4):
+        runner.launch(i)
+    res["layer_from_hidden_m1_us"] = time_graph(runner, list(range(n)), device)
+    res["gate_bytes"] = E * H * 2
+    return res
+
+
 def prefill_flops(m, top_k=TOP_K, h=H, i=I):
     """Multiply-adds x 2 of the expert products over every (token, slot) pair."""
     return 2.0 * m * top_k * (h * 2 * i + i * h)
@@ -548,6 +619,9 @@ def main():
     print(f"[bench] M=1 {m1['us_per_layer']:.2f} us {m1['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
     m7 = bench_config(7, 0.5, 2, copies, args.steps, args.warmup, device)
     print(f"[bench] M=7 {m7['us_per_layer']:.2f} us {m7['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    fe = bench_front_end(copies, args.steps, device)
+    print(f"[bench] router front-end M=1 fused {fe['M1']['fused_us']:.2f} us, torch {fe['M1']['torch_us']:.2f} us; "
+          f"block from hidden M=1 {fe['layer_from_hidden_m1_us']:.2f} us", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_budget_s, 100000)
@@ -586,6 +660,7 @@ def main():
         "cpu_baseline": cpu,
         "m1": m1,
         "m7": m7,
+        "router_front_end": fe,
     }
     print(json.dumps(res))
 

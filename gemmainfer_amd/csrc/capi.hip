@@ -165,6 +165,35 @@ int gi_moe_layer_from_logits(const void* x, int x_dtype, const void* logits, int
   return gi::launch_fused_moe(a);
 }
 
+int gi_moe_router_logits(const void* x, int x_dtype, const void* router_scale,
+                         const void* gate_w, float eps, void* logits, int M, int H, int E,
+                         void* stream) {
+  int st = check_bf16_x(x_dtype, "moe_router_logits");
+  if (st != GI_OK) return st;
+  return gi::launch_moe_router(x, router_scale, gate_w, logits, M, H, E, eps, as_stream(stream));
+}
+
+int gi_moe_layer_from_hidden(const void* x, int x_dtype, const void* router_scale,
+                             const void* gate_w, float eps, void* logits,
+                             const float* expert_scale, const int32_t* gu_packed,
+                             const void* gu_scales, int gu_groups, const int32_t* d_packed,
+                             const void* d_scales, int d_groups, void* out, int32_t* out_idx,
+                             void* out_w, int M, int H, int I, int E, int top_k,
+                             int group_size, void* workspace, size_t workspace_bytes,
+                             int spin_limit, void* stream) {
+  int st = check_bf16_x(x_dtype, "moe_layer_from_hidden");
+  if (st != GI_OK) return st;
+  if (!logits && M > 0) return fail(GI_ERR_INVALID_ARG, "moe_layer_from_hidden: null logits");
+  if (top_k <= 0 || top_k > E)
+    return fail(GI_ERR_INVALID_ARG, "moe_layer_from_hidden: top_k must be in [1, E]");
+  st = gi::launch_moe_router(x, router_scale, gate_w, logits, M, H, E, eps, as_stream(stream));
+  if (st != GI_OK) return st;
+  return gi_moe_layer_from_logits(x, x_dtype, logits, GI_DTYPE_BF16, expert_scale, gu_packed,
+                                  gu_scales, gu_groups, d_packed, d_scales, d_groups, out,
+                                  out_idx, out_w, M, H, I, E, top_k, group_size, workspace,
+                                  workspace_bytes, spin_limit, stream);
+}
+
 int gi_workspace_status(void* workspace, size_t workspace_bytes, int32_t* host_status,
                         void* stream) {
   if (workspace_bytes < sizeof(int32_t))

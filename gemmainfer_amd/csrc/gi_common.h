@@ -42,6 +42,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
 
 __device__ __forceinline__ float round_to_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// The same rounding for two values in one v_cvt_pk_bf16_f32 (gfx950): round to
+// nearest even, NaN stays NaN; lo in bits 0-15, hi in bits 16-31.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
 __device__ __forceinline__ float fp16_to_f32(uint16_t bits) {
   _Float16 h = __builtin_bit_cast(_Float16, bits);
   return (float)h;
@@ -165,6 +173,26 @@ __device__ __forceinline__ float reduce_across_groups(float v) {
 #pragma unroll
   for (int off = kGroup; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
   return v;
+}
+
+// Sum over the 64 lanes, returned to every lane (wave-uniform).  Each row of
+// 16 lanes is summed with DPP (quad butterflies, then the half-row and row
+// mirrors), the four row sums are read with v_readlane and added in the fixed
+// order (r0 + r1) + (r2 + r3).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_f32(float v) {
+  v += dpp_f32<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);  // row_half_mirror
+  v += dpp_f32<0x140>(v);  // row_mirror
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
 }
 
 // ---- inter-workgroup data and signals ---------------------------------------

@@ -63,6 +63,8 @@ int launch_route(const void* logits, int logits_dtype, const float* expert_scale
                  int E, int top_k, int32_t* out_idx, void* out_w, int w_dtype,
                  hipStream_t stream);
 int read_workspace_status(void* workspace, int32_t* host_status, hipStream_t stream);
+int launch_moe_router(const void* x, const void* router_scale, const void* gate, void* logits, int M,
+                      int H, int E, float eps, hipStream_t stream);
 
 // ---- W4A16 linear -------------------------------------------------------------
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs);

@@ -225,6 +225,78 @@ def moe_layer(x, router_logits, gate_up_packed, gate_up_scales, down_packed, dow
     return out, idx, w
 
 
+def _router_inputs(x, router_scale, gate_weight, who):
+    dev = _on_device(x, gate_weight)
+    _require_bf16(x, who)
+    _require(x.dim() == 2, f"{who}: x must be [M, H]")
+    m, h = x.shape
+    _require(gate_weight.dim() == 2 and gate_weight.shape[1] == h,
+             f"{who}: gate weight must be [E, H={h}], got {tuple(gate_weight.shape)}")
+    _require(gate_weight.dtype == torch.bfloat16, f"{who}: gate weight must be bf16", TypeError)
+    if router_scale is not None:
+        _on_device(x, router_scale)
+        _require(router_scale.numel() == h and router_scale.dtype == torch.bfloat16,
+                 f"{who}: router_scale must be a bf16 tensor of H={h} elements")
+        router_scale = router_scale.contiguous()
+    return dev, m, h, gate_weight.shape[0], router_scale
+
+
+def moe_router_logits(x, router_scale, gate_weight, eps: float = 1e-6):
+    """Router front-end of GemmaBatchedMoE.forward (gemma.py:75-76) in one launch:
+    bf16 logits [M, E] of the gate linear applied to
+    router_norm(x) * (router_scale * H**-0.5), with the bf16 roundings of the
+    bf16 model (norm output, scaled router_scale, their product, the logits).
+    ``router_scale`` may be None (ones); ``gate_weight`` is the nn.Linear weight
+    [E, H]."""
+    dev, m, h, e, rs = _router_inputs(x, router_scale, gate_weight, "moe_router_logits")
+    logits = torch.empty((m, e), dtype=torch.bfloat16, device=dev)
+    if m == 0:
+        return logits
+    L.check(L.load().gi_moe_router_logits(
+        _ptr(x.contiguous()), L.DTYPE_BF16, _ptr(rs), _ptr(gate_weight.contiguous()), float(eps),
+        _ptr(logits), m, h, e, _stream(dev)), "moe_router_logits")
+    return logits
+
+
+def moe_layer_from_hidden(x, router_scale, gate_weight, gate_up_packed, gate_up_scales,
+                          down_packed, down_scales, top_k, group_size, expert_scale=None,
+                          eps: float = 1e-6, out=None, *, spin_limit: int = 0):
+    """GemmaBatchedMoE.forward (gemma.py:75-98) from the hidden state: the router
+    front-end (one launch) feeding ``moe_layer`` on the logits it writes.
+
+    Returns (out [M, H] bf16 -- overwritten, idx int32 [M, top_k],
+    weights bf16 [M, top_k], logits bf16 [M, E]).
+    """
+    dev, m, h, e, rs = _router_inputs(x, router_scale, gate_weight, "moe_layer_from_hidden")
+    _on_device(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
+    m2, h2, i, e2 = _moe_weight_shapes(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
+    _require(e2 == e, f"gate weight has {e} experts, the expert weights {e2}")
+    _require(0 < top_k <= min(e, 64), f"top_k must be in [1, min(E, 64)], got {top_k}")
+    if expert_scale is not None:
+        _on_device(x, expert_scale)
+        _require(expert_scale.numel() == e, "expert_scale must have E elements")
+        expert_scale = expert_scale.to(torch.float32).contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    _require(tuple(out.shape) == (m, h) and out.dtype == x.dtype and out.is_contiguous(),
+             "out must be a contiguous bf16 [M, H] tensor")
+    idx = torch.empty((m, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((m, top_k), dtype=torch.bfloat16, device=dev)
+    logits = torch.empty((m, e), dtype=torch.bfloat16, device=dev)
+    if m == 0:
+        return out, idx, w, logits
+    lib = L.load()
+    nbytes = lib.gi_fused_moe_workspace_bytes(m, top_k, h, i, e)
+    ws = _WS.get("moe", dev, nbytes)
+    L.check(lib.gi_moe_layer_from_hidden(
+        _ptr(x.contiguous()), L.DTYPE_BF16, _ptr(rs), _ptr(gate_weight.contiguous()), float(eps),
+        _ptr(logits), _ptr(expert_scale), _ptr(gate_up_packed), _ptr(gate_up_scales),
+        gate_up_scales.shape[1], _ptr(down_packed), _ptr(down_scales), down_scales.shape[1],
+        _ptr(out), _ptr(idx), _ptr(w), m, h, i, e, int(top_k), int(group_size), _ptr(ws),
+        ws.numel(), int(spin_limit), _stream(dev)), "moe_layer_from_hidden")
+    return out, idx, w, logits
+
+
 def route_topk_softmax(router_logits, top_k, expert_scale=None, out_dtype=torch.bfloat16):
     """idx int32 [M, k], w [M, k] = softmax_fp32(topk(logits)) * expert_scale, cast
     to out_dtype (gemma.py:77-80; ties -> lower expert index)."""

@@ -75,6 +75,18 @@ def activations(M: int, H: int, seed: int = 0) -> torch.Tensor:
     return torch.randn((M, H), generator=_gen(seed + 1000)).to(torch.bfloat16)
 
 
+def router_weights(E: int, H: int, seed: int = 0, gate_std: float = 2.0) -> dict:
+    """Router parameters of one MoE block (gemma.py:31-34) in bf16: router_scale
+    [H] around 1, the gate nn.Linear weight [E, H] and expert_scale [E] around 1.
+    gate_std 2 gives logits of roughly unit spread for N(0, 1) hidden states."""
+    g = _gen(seed + 3000)
+    return {
+        "router_scale": (1.0 + 0.25 * torch.randn(H, generator=g)).to(torch.bfloat16),
+        "gate": (gate_std * torch.randn((E, H), generator=g)).to(torch.bfloat16),
+        "expert_scale": (1.0 + 0.1 * torch.randn(E, generator=g)).to(torch.bfloat16),
+    }
+
+
 def router_logits(M: int, E: int, seed: int = 0, verify_noise: float = 0.0) -> torch.Tensor:
     """i.i.d. N(0,1) logits, or (verify_noise > 0) a shared base N(0,1) row plus
     per-token N(0, verify_noise) noise, so that draft tokens overlap."""

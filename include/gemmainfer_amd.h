@@ -20,6 +20,9 @@
  *   gi_moe_align                <- the per-block dedup scan of the Token-Union kernels
  *                                  csrc/marlin.cu:285-335 and :453-505 (implicit there)
  *   gi_moe_layer_from_logits    <- gemma.py:77-98 (router tail + zeroed out + fused call)
+ *   gi_moe_router_logits        <- gemma.py:75-76 (router norm, router_scale, gate linear;
+ *                                  torch ops there, rmsnorm.cu:16-73 for the norm)
+ *   gi_moe_layer_from_hidden    <- gemma.py:75-98 (the MoE block's forward)
  *   gi_softcap_inplace          <- gemmainfer_csrc.softcapping
  *                                  csrc/pybind.cpp:169-180 -> csrc/softcapping.cu:21-47
  *   gi_rmsnorm                  <- gemmainfer_csrc.rmsnorm
@@ -129,6 +132,34 @@ int gi_fused_batched_moe(const void* x, int x_dtype,
  * gate/up, down, combine launches).                                         */
 int gi_moe_layer_from_logits(const void* x, int x_dtype,
                              const void* logits, int logits_dtype,
+                             const float* expert_scale,
+                             const int32_t* gu_packed, const void* gu_scales, int gu_groups,
+                             const int32_t* d_packed, const void* d_scales, int d_groups,
+                             void* out, int32_t* out_idx, void* out_w,
+                             int M, int H, int I, int E, int top_k, int group_size,
+                             void* workspace, size_t workspace_bytes,
+                             int spin_limit, void* stream);
+
+/* ---- f3: router front-end --------------------------------------------------
+ * Replaces the torch statements of gemma.py:75-76 (GemmaRMSNorm without scale,
+ * norm.py:28-40 -> rmsnorm.cu:16-73; router_scale * hidden_size**-0.5; the
+ * bf16 nn.Linear gate) with one launch:
+ *   logits[M, E] = bf16( bf16( bf16(x * rsqrt(mean(x^2) + eps))
+ *                              * bf16(router_scale * H^-0.5) ) @ gate_w^T )
+ * x bf16 [M, H], router_scale bf16 [H] (NULL = ones), gate_w bf16 [E, H] (the
+ * nn.Linear weight), logits bf16 [M, E] (overwritten).  fp32 sums in a fixed
+ * order: deterministic, and a logit may differ from a BLAS-computed one by one
+ * bf16 ulp.  Requirements: H % 8 == 0, H <= 4096, E <= 65536.              */
+int gi_moe_router_logits(const void* x, int x_dtype, const void* router_scale,
+                         const void* gate_w, float eps, void* logits, int M, int H, int E,
+                         void* stream);
+
+/* The whole MoE block from the hidden state (gemma.py:75-98): the router
+ * front-end above writes logits (bf16 [M, E], required), then
+ * gi_moe_layer_from_logits runs on them.  Same workspace as
+ * gi_moe_layer_from_logits; two launches at M <= 8.                        */
+int gi_moe_layer_from_hidden(const void* x, int x_dtype, const void* router_scale,
+                             const void* gate_w, float eps, void* logits,
                              const float* expert_scale,
                              const int32_t* gu_packed, const void* gu_scales, int gu_groups,
                              const int32_t* d_packed, const void* d_scales, int d_groups,

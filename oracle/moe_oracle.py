@@ -25,6 +25,12 @@ Pinning (what checks this restatement, see tests/test_oracle.py):
   token_union_align     hand-written known-answer cases (duplicates across and
                         within tokens, invalid ids, U=1, U=S, M=1/7/8/9) and a
                         brute-force restatement of the reference's O(S^2) scan.
+  router_logits         norm step against the reference C++ fallback
+                        ``cpu_gemma_rmsnorm`` (no weight) from oracle/_ref; the
+                        scale and product steps against torch's own bf16
+                        elementwise ops (the statements of gemma.py:75); the
+                        gate against torch.nn.functional.linear in bf16;
+                        closed forms (constant rows, identity gate).
   fused_batched_moe     reference C++ fallback ``cpu_fused_batched_moe`` from
                         oracle/_ref (gs=64, all groups full); brute force on tiny
                         shapes; all-zero scales -> zero output; linearity in the
@@ -184,6 +190,49 @@ def softcap(y, cap) -> np.ndarray:
     """cap * tanh(y / cap)  (softcapping.cu:16-17, pybind.cpp:134)."""
     y = np.asarray(y, dtype=np.float64)
     return cap * np.tanh(y / cap)
+
+
+# --------------------------------------------------------------------------
+# router front-end (gemma.py:75-76)
+# --------------------------------------------------------------------------
+def rmsnorm_noscale_bf16(x, eps):
+    """GemmaRMSNorm(with_scale=False) on bf16 rows (norm.py:28-40 ->
+    rmsnorm.cu:16-73 on the GPU, pybind.cpp:87-103 on the CPU): fp32 products
+    x * rsqrt(mean(x^2) + eps), rounded to bf16.  The mean is taken in float64
+    and rsqrt rounded to fp32 once; the product is formed in fp32 as the
+    reference does, then rounded to bf16."""
+    xf = np.asarray(x, dtype=np.float64)
+    ms = np.mean(xf * xf, axis=-1, keepdims=True)
+    r = (1.0 / np.sqrt(ms + np.float64(np.float32(eps)))).astype(np.float32)
+    return bf16_round((xf.astype(np.float32) * r).astype(np.float64))
+
+
+def router_scale_bf16(router_scale, hidden):
+    """``router_scale * (hidden_size ** -0.5)`` (gemma.py:75): a bf16 parameter
+    times a Python float, computed in fp32 with the scalar cast to fp32, bf16
+    result.  router_scale None = the parameter's initial ones (gemma.py:32)."""
+    c = np.float32(hidden ** -0.5)
+    rs = (np.ones(hidden, dtype=np.float32) if router_scale is None
+          else np.asarray(router_scale, dtype=np.float64).astype(np.float32))
+    return bf16_round((rs * c).astype(np.float64))
+
+
+def router_logits(x, router_scale, gate_w, eps=1e-6):
+    """Router front-end of GemmaBatchedMoE.forward (gemma.py:75-76):
+
+        x_normed = bf16(norm(x) * bf16(router_scale * H^-0.5))   (bf16 * bf16)
+        logits   = bf16(x_normed @ gate_w.T)                      (nn.Linear, no bias)
+
+    The dot products are exact (float64) and rounded once; the reference's
+    fp32 accumulation differs from them by far less than one bf16 ulp except
+    next to a rounding boundary.  Returns (logits float64 [M, E],
+    x_normed float64 [M, H])."""
+    xf = np.asarray(x, dtype=np.float64)
+    n = rmsnorm_noscale_bf16(xf, eps)
+    s = router_scale_bf16(router_scale, xf.shape[-1])
+    xr = bf16_round(n * s)
+    g = np.asarray(gate_w, dtype=np.float64)
+    return bf16_round(xr @ g.T), xr
 
 
 # --------------------------------------------------------------------------

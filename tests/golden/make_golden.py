@@ -79,6 +79,24 @@ def elementwise_case():
                         capped_bf16=bits(capped))
 
 
+def router_case(name, m, h, e, seed):
+    """Router front-end (gemma.py:75-76): the norm through the reference's CPU
+    fallback rmsnorm with no weight (pybind.cpp:87-103), the rest as the
+    module's own torch statements on bf16 CPU tensors."""
+    x = synth.activations(m, h, seed=seed)
+    x[0] *= 20.0   # rows of very different RMS
+    if m > 1:
+        x[1] *= 0.05
+    W = synth.router_weights(e, h, seed=seed)
+    y = torch.empty_like(x)
+    R.rmsnorm(x, torch.empty(0), y, 1e-6, False)
+    xr = y * (W["router_scale"] * (h ** -0.5))
+    logits = torch.nn.functional.linear(xr, W["gate"])
+    np.savez_compressed(OUT / f"{name}.npz", x_bf16=bits(x), router_scale_bf16=bits(W["router_scale"]),
+                        gate_bf16=bits(W["gate"]), norm_bf16=bits(y), x_normed_bf16=bits(xr),
+                        logits_bf16=bits(logits), eps=np.float32(1e-6))
+
+
 def main():
     linear_case("linear_m1_k256_n96_gs64", 1, 256, 96, 64, seed=1)
     linear_case("linear_m5_k512_n128_gs128", 5, 512, 128, 128, seed=2)
@@ -89,6 +107,7 @@ def main():
     moe_case("moe_m3_dups_gs64", 3, 256, 128, 8, 4, 64, seed=7,
              idx=[[1, 1, 2, 3], [2, 5, 5, 5], [0, 7, 1, 2]])
     elementwise_case()
+    router_case("router_m3_h512_e16", 3, 512, 16, seed=8)
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)
 

@@ -32,3 +32,23 @@ def assert_bf16_close(got: torch.Tensor, ref64: np.ndarray, what: str = "") -> d
         f"{what}: {int(bad.sum())} elements outside {ATOL} + 2^-7|ref|; worst "
         f"{float(np.max(np.abs(g - ref64) - bound)):.3e} over bound ({stats})")
     return stats
+
+
+def bf16_ulp(v) -> np.ndarray:
+    """Spacing of bf16 values at |v| (normal range; 2^-133 floor)."""
+    _, e = np.frexp(np.maximum(np.abs(np.asarray(v, dtype=np.float64)), 2.0 ** -126))
+    return np.ldexp(1.0, e - 8)
+
+
+def assert_logits_close(got: torch.Tensor, ref64: np.ndarray, what: str = "",
+                        min_exact: float = 0.97) -> None:
+    """Router logits: every element within one bf16 ulp of the oracle (the fp32
+    sum order may move a value across a rounding boundary), and nearly all of
+    them bit-identical."""
+    g = np64(got)
+    assert g.shape == ref64.shape, (what, g.shape, ref64.shape)
+    diff = np.abs(g - ref64)
+    bad = diff > bf16_ulp(ref64)
+    assert not bad.any(), f"{what}: {int(bad.sum())} logits more than one bf16 ulp off; max diff {diff.max():.3e}"
+    exact = float(np.mean(g == ref64))
+    assert exact >= min_exact, f"{what}: only {exact:.4f} of logits bit-identical"

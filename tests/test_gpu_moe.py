@@ -10,7 +10,7 @@ import torch
 from gemmainfer_amd import ops, synth
 from gemmainfer_amd import _lib as L
 from oracle import moe_oracle as O
-from tests.helpers import assert_bf16_close, np64
+from tests.helpers import assert_bf16_close, assert_logits_close, np64
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -248,6 +248,60 @@ def test_layer_from_logits_gemma(gemma128):
         np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
         np.testing.assert_allclose(np64(w), ref_w, rtol=2.0 ** -7)
         assert_bf16_close(out, ref_out, f"layer m={m}")
+
+
+# ---------------------------------------------------------------- router front-end
+ROUTER_SHAPES = [(1, 2816, 128), (7, 2816, 128), (8, 2816, 128), (13, 2816, 128),
+                 (100, 2816, 128), (3, 256, 8), (5, 1024, 1000), (2, 4096, 64), (9, 520, 36)]
+
+
+@pytest.mark.parametrize("m,h,e", ROUTER_SHAPES)
+def test_router_logits_match_oracle(m, h, e):
+    """gemma.py:75-76 in one launch against the oracle: every logit within one
+    bf16 ulp, nearly all bit-identical; with and without router_scale."""
+    x = synth.activations(m, h, seed=m + h) * torch.linspace(0.05, 8, m).unsqueeze(1).to(torch.bfloat16)
+    W = synth.router_weights(e, h, seed=e)
+    for rs in (W["router_scale"], None):
+        print(f"router m={m} h={h} e={e} scale={rs is not None}", flush=True)
+        got = ops.moe_router_logits(x.to(DEV), None if rs is None else rs.to(DEV), W["gate"].to(DEV))
+        ref, _ = O.router_logits(np64(x), None if rs is None else np64(rs), np64(W["gate"]), 1e-6)
+        assert_logits_close(got, ref, f"router m={m} h={h} e={e}")
+
+
+def test_router_matches_reference_golden():
+    g = np.load(GOLDEN / "router_m3_h512_e16.npz")
+    x = _bits_to_bf16(g["x_bf16"]).to(DEV)
+    rs = _bits_to_bf16(g["router_scale_bf16"]).to(DEV)
+    gate = _bits_to_bf16(g["gate_bf16"]).to(DEV)
+    got = ops.moe_router_logits(x, rs, gate, float(g["eps"]))
+    ref = O.bf16_bits_to_f64(g["logits_bf16"])
+    assert_logits_close(got, ref, "router golden", min_exact=0.9)
+
+
+@pytest.mark.parametrize("m", [1, 7, 100])
+def test_layer_from_hidden_gemma(gemma128, m):
+    """The MoE block from the hidden state: logits as the oracle's router
+    front-end; routing bit-exact and output within tolerance against the
+    oracle run on those logits; bitwise equal to moe_layer on the same logits."""
+    W, Wd = gemma128
+    R = synth.router_weights(128, 2816, seed=m)
+    x = synth.activations(m, 2816, seed=40 + m).to(DEV)
+    es = R["expert_scale"].to(DEV)
+    print(f"layer_from_hidden m={m}", flush=True)
+    out, idx, w, logits = ops.moe_layer_from_hidden(
+        x, R["router_scale"].to(DEV), R["gate"].to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+        Wd["down_packed"], Wd["down_scales"], 8, 128, expert_scale=es)
+    ref_logits, _ = O.router_logits(np64(x), np64(R["router_scale"]), np64(R["gate"]), 1e-6)
+    assert_logits_close(logits, ref_logits, f"layer_from_hidden logits m={m}")
+    ref_out, ref_idx, ref_w, _ = O.moe_layer_from_logits(
+        np64(x), np64(logits), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
+        W["down_packed"].numpy(), np64(W["down_scales"]), 8, 128, expert_scale=np64(R["expert_scale"]))
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx)
+    np.testing.assert_allclose(np64(w), ref_w, rtol=2.0 ** -7)
+    assert_bf16_close(out, ref_out, f"layer_from_hidden m={m}")
+    out2, idx2, w2 = ops.moe_layer(x, logits, Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                   Wd["down_packed"], Wd["down_scales"], 8, 128, expert_scale=es)
+    assert torch.equal(out, out2) and torch.equal(idx, idx2) and torch.equal(w, w2)
 
 
 def test_deterministic_bitwise(gemma128):

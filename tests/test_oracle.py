@@ -158,6 +158,93 @@ def test_elementwise_golden_roundtrip():
                                rtol=2.0 ** -6, atol=1e-6)
 
 
+# --------------------------------------------------------------------------- router front-end
+def _ulp_bf16(v):
+    """Spacing of bf16 values at |v| (normal range)."""
+    _, e = np.frexp(np.maximum(np.abs(v), 2.0 ** -126))
+    return np.ldexp(1.0, e - 8)
+
+
+def test_router_golden_steps():
+    """Each step of the oracle's router front-end against the fixture made by the
+    reference's CPU rmsnorm (no weight) and the module's torch statements."""
+    g = load("router_m3_h512_e16")
+    x, rs, gate = f64(g["x_bf16"]), f64(g["router_scale_bf16"]), f64(g["gate_bf16"])
+    eps = float(g["eps"])
+    n = O.rmsnorm_noscale_bf16(x, eps)
+    ref_n = f64(g["norm_bf16"])
+    assert np.mean(n == ref_n) > 0.995
+    assert np.all(np.abs(n - ref_n) <= _ulp_bf16(ref_n))
+    # scale and product: exact given the reference's norm
+    xr = O.bf16_round(ref_n * O.router_scale_bf16(rs, x.shape[1]))
+    np.testing.assert_array_equal(xr, f64(g["x_normed_bf16"]))
+    logits, xr_full = O.router_logits(x, rs, gate, eps)
+    ref_l = f64(g["logits_bf16"])
+    assert np.all(np.abs(logits - ref_l) <= _ulp_bf16(ref_l)), np.abs(logits - ref_l).max()
+    assert np.mean(logits == ref_l) > 0.9
+
+
+def test_router_steps_match_torch_statements():
+    """gemma.py:75-76 as torch evaluates it on bf16 CPU tensors, at Gemma's shape."""
+    R = ref_module()
+    x = synth.activations(9, 2816, seed=31) * torch.linspace(0.01, 30, 9).unsqueeze(1).to(torch.bfloat16)
+    W = synth.router_weights(128, 2816, seed=31)
+    y = torch.empty_like(x)
+    R.rmsnorm(x, torch.empty(0), y, 1e-6, False)
+    n = O.rmsnorm_noscale_bf16(t64(x), 1e-6)
+    assert np.all(np.abs(n - t64(y)) <= _ulp_bf16(t64(y)))
+    assert np.mean(n == t64(y)) > 0.995
+    s_torch = W["router_scale"] * (2816 ** -0.5)
+    np.testing.assert_array_equal(O.router_scale_bf16(t64(W["router_scale"]), 2816), t64(s_torch))
+    xr_torch = y * s_torch
+    np.testing.assert_array_equal(O.bf16_round(t64(y) * t64(s_torch)), t64(xr_torch))
+    lin = F.linear(xr_torch, W["gate"])
+    ours = O.bf16_round(t64(xr_torch) @ t64(W["gate"]).T)
+    assert np.all(np.abs(ours - t64(lin)) <= _ulp_bf16(t64(lin)))
+
+
+def test_router_closed_forms():
+    h, e = 256, 64
+    # constant rows: norm = a / sqrt(a^2 + eps) -> bf16 1.0 for |a| >> sqrt(eps);
+    # identity gate rows pick x_normed[e] = bf16(H^-0.5)
+    x = np.full((2, h), 2.0)
+    x[1] = -0.5
+    gate = np.zeros((e, h))
+    gate[np.arange(e), np.arange(e)] = 1.0
+    logits, xr = O.router_logits(x, None, gate)
+    c = float(torch.tensor(h ** -0.5, dtype=torch.float32).to(torch.bfloat16))
+    np.testing.assert_array_equal(logits[0], np.full(e, c))
+    np.testing.assert_array_equal(logits[1], np.full(e, -c))
+    # all-zero row stays zero (eps keeps rsqrt finite)
+    z, _ = O.router_logits(np.zeros((1, h)), None, gate)
+    assert np.all(z == 0.0)
+    # exact symmetries: negating router_scale negates the logits; a power-of-two
+    # gate scale scales them exactly
+    rng = np.random.default_rng(3)
+    xs = O.bf16_round(rng.standard_normal((4, h)))
+    rs = O.bf16_round(1 + 0.2 * rng.standard_normal(h))
+    g = O.bf16_round(rng.standard_normal((e, h)))
+    a, _ = O.router_logits(xs, rs, g)
+    b, _ = O.router_logits(xs, -rs, g)
+    d, _ = O.router_logits(xs, rs, 4.0 * g)
+    np.testing.assert_array_equal(a, -b)
+    np.testing.assert_array_equal(4.0 * a, d)
+    # brute force on a tiny case: scalar loops with the same roundings
+    xt, rt, gt = xs[:2, :16], rs[:16], g[:3, :16]
+    ref = np.zeros((2, 3))
+    for m in range(2):
+        ms = sum(v * v for v in xt[m]) / 16
+        r = np.float32(1.0 / np.sqrt(ms + np.float64(np.float32(1e-6))))
+        for k in range(3):
+            acc = 0.0
+            for j in range(16):
+                nv = O.bf16_round(np.float64(np.float32(xt[m, j]) * r))
+                sv = O.bf16_round(np.float64(np.float32(rt[j]) * np.float32(16 ** -0.5)))
+                acc += O.bf16_round(nv * sv) * gt[k, j]
+            ref[m, k] = O.bf16_round(acc)
+    np.testing.assert_array_equal(O.router_logits(xt, rt, gt)[0], ref)
+
+
 # --------------------------------------------------------------------------- routing
 @pytest.mark.parametrize("m,e,k", [(1, 128, 8), (7, 128, 8), (33, 64, 4), (5, 8, 2)])
 def test_route_matches_torch_topk_softmax(m, e, k):
