@@ -214,6 +214,13 @@ int gi_w4a16_linear(const void* A, int a_dtype, const int32_t* B_packed, const v
                           workspace, workspace_bytes, as_stream(stream));
 }
 
+int gi_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int N,
+                    int K, int n_groups, int32_t* packed_out, void* scales_out, int64_t ld_out,
+                    void* stream) {
+  return gi::launch_w4a16_ingest(weight_packed, weight_scale, scale_dtype, N, K, n_groups, packed_out,
+                                 scales_out, ld_out, as_stream(stream));
+}
+
 int gi_softcap_inplace(void* x, int dtype, int64_t n, float cap, void* stream) {
   return gi::launch_softcap(x, dtype, n, cap, as_stream(stream));
 }

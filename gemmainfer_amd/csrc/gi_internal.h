@@ -72,6 +72,10 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
                  int M, int K, int N, int gs, float softcap, void* workspace,
                  size_t workspace_bytes, hipStream_t stream);
 
+int launch_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int N,
+                        int K, int n_groups, int32_t* packed_out, void* scales_out, int64_t ld_out,
+                        hipStream_t stream);
+
 // ---- companions -------------------------------------------------------------
 int launch_softcap(void* x, int dtype, int64_t n, float cap, hipStream_t stream);
 int launch_rmsnorm(const void* in, const void* weight, void* out, int dtype, int64_t rows,

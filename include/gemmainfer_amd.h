@@ -23,6 +23,8 @@
  *   gi_moe_router_logits        <- gemma.py:75-76 (router norm, router_scale, gate linear;
  *                                  torch ops there, rmsnorm.cu:16-73 for the norm)
  *   gi_moe_layer_from_hidden    <- gemma.py:75-98 (the MoE block's forward)
+ *   gi_w4a16_ingest             <- gemmainfer/utils/weights.py:100-159 (checkpoint
+ *                                  transposition of weight_packed / weight_scale)
  *   gi_softcap_inplace          <- gemmainfer_csrc.softcapping
  *                                  csrc/pybind.cpp:169-180 -> csrc/softcapping.cu:21-47
  *   gi_rmsnorm                  <- gemmainfer_csrc.rmsnorm
@@ -183,6 +185,19 @@ int gi_w4a16_linear(const void* A, int a_dtype,
                     const int32_t* B_packed, const void* scales, int n_groups,
                     void* C, int M, int K, int N, int group_size, float softcap,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- f4: checkpoint ingest ------------------------------------------------
+ * Replaces the `t.t()` + copy of weights.py:100-159 that turns a
+ * compressed-tensors W4A16 linear into the layout the kernels read:
+ *   weight_packed int32 [N, K/8]   ->  packed_out int32 [K/8, ld_out] (columns 0..N-1)
+ *   weight_scale  [N, n_groups]    ->  scales_out bf16  [n_groups, ld_out]
+ * (bf16/fp16/fp32 scales, rounded to bf16 to nearest even).  Words are moved
+ * unchanged.  Pass pointers offset by I columns and ld_out = 2I to fill the up
+ * half of an expert's gate_up (weights.py:152-159).  One tiled transpose
+ * launch per tensor; n_groups = 0 or K = 0 skips that tensor.              */
+int gi_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype,
+                    int N, int K, int n_groups, int32_t* packed_out, void* scales_out,
+                    int64_t ld_out, void* stream);
 
 /* ---- drop-in companions (not on the MoE hot path) ----------------------- */
 /* x <- cap * tanh(x / cap), n elements, bf16/fp16/fp32.                      */

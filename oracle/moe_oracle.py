@@ -31,6 +31,9 @@ Pinning (what checks this restatement, see tests/test_oracle.py):
                         elementwise ops (the statements of gemma.py:75); the
                         gate against torch.nn.functional.linear in bf16;
                         closed forms (constant rows, identity gate).
+  from_compressed       scalar brute force over the compressed-tensors layout
+                        (nibble i of word [n][j] is k = 8j + i); round trip
+                        through the transposed writer.
   fused_batched_moe     reference C++ fallback ``cpu_fused_batched_moe`` from
                         oracle/_ref (gs=64, all groups full); brute force on tiny
                         shapes; all-zero scales -> zero output; linearity in the
@@ -140,6 +143,15 @@ def quantize_w4(weight, group_size) -> tuple[np.ndarray, np.ndarray]:
     s = bf16_round(np.maximum(np.abs(wt).max(axis=1), 1e-5) / 7.0)
     q = np.clip(np.rint(wt / s[:, None, :]) + ZERO_POINT, 0, 15).reshape(k, n)
     return pack_int4(q), s
+
+
+def from_compressed(weight_packed, weight_scale):
+    """compressed-tensors W4A16 linear (``weight_packed`` int32 [N, K/8],
+    ``weight_scale`` [N, groups]) -> (packed [K/8, N], scales [groups, N]) as
+    this oracle and the kernels take them: the ``t.t()`` of
+    weights.py:100-159."""
+    return (np.ascontiguousarray(np.asarray(weight_packed).T),
+            np.ascontiguousarray(np.asarray(weight_scale, dtype=np.float64).T))
 
 
 def dequant(packed, scales, group_size) -> np.ndarray:
