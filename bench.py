@@ -466,6 +466,100 @@ def bench_linear(name, steps, warmup, device, cpu_budget_s=None):
     }
 
 
+# Gemma-4-26B-A4B dense W4A16 linears of one decoder layer, (K, N), checkpoint
+# group size 64 (attention.py:115-122, activations.py:26-28): a sliding-window
+# layer has q, k, v, o and the shared MLP; a global layer's attention has
+# q_global, k_global (= v) and o_global instead.
+DENSE_PROJ = [
+    ("q", 2816, 4096), ("k", 2816, 2048), ("v", 2816, 2048), ("o", 4096, 2816),
+    ("mlp_gate", 2816, 2112), ("mlp_up", 2816, 2112), ("mlp_down", 2112, 2816),
+    ("q_global", 2816, 8192), ("k_global", 2816, 1024), ("o_global", 8192, 2816),
+]
+DENSE_GS = 64
+SLIDING = ("q", "k", "v", "o", "mlp_gate", "mlp_up", "mlp_down")
+
+
+def bench_ingest(device):
+    """gi_w4a16_ingest of one MoE layer's experts (128 x gate, up, down at
+    H=2816, I=704, gs 64) from checkpoint layout already in HBM: bytes read +
+    written per second, eager launches between HIP events."""
+    lib = L.load()
+    g = torch.Generator(device=device)
+    g.manual_seed(1)
+    shapes = [(I, H), (I, H), (H, I)]  # (N, K): gate, up, down
+    src = [(torch.randint(-(2 ** 31), 2 ** 31, (n, k // 8), generator=g, device=device, dtype=torch.int64)
+            .to(torch.int32), torch.randn((n, k // DENSE_GS), generator=g, device=device).to(torch.bfloat16))
+           for n, k in shapes]
+    gu = torch.empty((E, H // 8, 2 * I), dtype=torch.int32, device=device)
+    gus = torch.empty((E, H // DENSE_GS, 2 * I), dtype=torch.bfloat16, device=device)
+    dn = torch.empty((E, I // 8, H), dtype=torch.int32, device=device)
+    dns = torch.empty((E, I // DENSE_GS, H), dtype=torch.bfloat16, device=device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+
+    def one_layer():
+        for e in range(E):
+            for j, (dst_p, dst_s, lo, ld) in enumerate(((gu[e], gus[e], 0, 2 * I), (gu[e], gus[e], I, 2 * I),
+                                                        (dn[e], dns[e], 0, H))):
+                n, k = shapes[j]
+                wp, ws = src[j]
+                st = lib.gi_w4a16_ingest(p(wp), p(ws), L.DTYPE_BF16, n, k, k // DENSE_GS,
+                                         ctypes.c_void_p(dst_p.data_ptr() + 4 * lo),
+                                         ctypes.c_void_p(dst_s.data_ptr() + 2 * lo), ld, stream)
+                L.check(st, "gi_w4a16_ingest")
+
+    one_layer()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    one_layer()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0
+    nbytes = 2 * E * sum(n * (k // 8) * 4 + n * (k // DENSE_GS) * 2 for n, k in shapes)
+    return {"us_per_moe_layer": us, "bytes_read_plus_written": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
+            "launches": 2 * 3 * E}
+
+
+def bench_dense(steps, warmup, device):
+    res = {}
+    for m in (1, 7):
+        row = {}
+        for name, k, n in DENSE_PROJ:
+            nbytes = linear_bytes(k, n, DENSE_GS)
+            copies = max(2, math.ceil(600e6 / nbytes))  # > the 256 MB MALL between reuses
+            runner = LinearRunner(m, k, n, DENSE_GS, 0.0, copies, device)
+            for i in range(min(warmup, 5)):
+                runner.launch(i)
+            us = time_graph(runner, list(range(min(steps, 200))), device)
+            row[name] = {"K": k, "N": n, "us": us, "bytes": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9}
+            del runner
+            torch.cuda.empty_cache()
+        tot_us = sum(row[x]["us"] for x in SLIDING)
+        tot_b = sum(row[x]["bytes"] for x in SLIDING)
+        res[f"M{m}"] = {"sliding_layer_us": tot_us, "sliding_layer_gbps": tot_b / (tot_us * 1e-6) / 1e9,
+                        "sliding_layer_bytes": tot_b, "per_projection": row}
+        print(f"[bench] dense M={m}: sliding layer {tot_us:.1f} us, "
+              f"{res[f'M{m}']['sliding_layer_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    ing = bench_ingest(device)
+    m1 = res["M1"]
+    return {
+        "metric": "dense W4A16 projections of one Gemma-4-26B-A4B sliding-window layer (q, k, v, o, "
+                  "shared MLP), us + achieved HBM GB/s at M=1 and M=7 (gs 64, 1 GPU)",
+        "value": m1["sliding_layer_gbps"], "unit": "GB/s", "n_gpus": 1, "steps": min(steps, 200),
+        "warmup": min(warmup, 5), "ms_per_step": m1["sliding_layer_us"] / 1000.0, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform int4 words, N(0,1)*0.02 bf16 scales, N(0,1) bf16 activations)",
+        "config": {"workload": "dense: gi_w4a16_linear per projection, one launch each, weight copies "
+                               "rotated past the MALL", "group_size": DENSE_GS,
+                   "timing": "HIP graph per projection, HIP events"},
+        "roofline": {"bound": "hbm", "achieved": m1["sliding_layer_gbps"], "peak": PEAK_GBPS, "unit": "GB/s",
+                     "frac": m1["sliding_layer_gbps"] / PEAK_GBPS, "traffic": None},
+        "cpu_baseline": None,
+        "M1": m1, "M7": res["M7"], "ingest": ing,
+    }
+
+
 def pmc_pass(copies, steps, warmup, device):
     """Eager launches for one rocprofv3 --pmc pass (FETCH_SIZE or WRITE_SIZE).
 
@@ -580,7 +674,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["moe", "prefill", *LINEAR_WORKLOADS], default="moe",
+    ap.add_argument("--workload", choices=["moe", "prefill", "dense", *LINEAR_WORKLOADS], default="moe",
                     help="moe (default: the BASELINE metric, M=1 value with M=7 beside it), prefill "
                          "(configs[3], M=512) or a dense W4A16 shape (linear = configs[0], "
                          "lm_head = configs[4])")
@@ -604,6 +698,9 @@ def main():
     torch.cuda.set_device(device)
     if args.workload == "prefill":
         print(json.dumps(bench_prefill(min(args.steps, 50), min(args.warmup, 5), device)))
+        return
+    if args.workload == "dense":
+        print(json.dumps(bench_dense(args.steps, args.warmup, device)))
         return
     if args.workload != "moe":
         print(json.dumps(bench_linear(args.workload, args.steps, args.warmup, device,

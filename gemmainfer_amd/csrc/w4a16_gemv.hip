@@ -185,6 +185,141 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Decode-shape path (M <= 8): the same tiling (64 columns x one K slice per
+// workgroup, 4 packed rows x 256 B per wave instruction) with every global
+// load of the workgroup issued before any is used -- S steps of weight words
+// and their scales, then the slice's token rows -- so a launch is one memory
+// round trip, the products and the split-K reduction.  Masked loads (rows
+// past the slice or past the last scale group, columns past N, tokens past
+// M) read zeros through the buffer range check; a zero scale then zeroes the
+// word's contribution, so no lane branches.  The plan picks S so that the
+// grid is about 256 workgroups: all of the matrix is requested at once.
+constexpr int kGemvTargetWgs = 320;
+constexpr int kGemvNt = 2;  // cache policy: non-temporal (weights are read once)
+
+template <int NT, int S>
+__global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
+  constexpr int kRows = S * kRowsPerStep;  // packed rows per slice
+  __shared__ uint4 xs[NT][kRows];
+  __shared__ float xb[NT][kRows];
+  __shared__ float red[kWaves * NT * kCols];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int rsub = lane >> 4, colq = lane & 15;
+  const int tile = blockIdx.x, split = blockIdx.y;
+  const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  const int r_begin = split * kRows;
+  const int nrows = min(kRows, Kp - r_begin);
+  const int col = tile * kCols + colq * 4;
+  const bool col_ok = col < a.N;
+
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, (uint32_t)((size_t)Kp * a.N * 4));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  uint4 w[S];
+  uint2 sc[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const int rl = j * kRowsPerStep + wave * 4 + rsub;
+    const int r = r_begin + rl;
+    const bool ok = col_ok && rl < nrows;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * a.N + col) * 4) : kOob,
+                                                            0, kGemvNt);
+    w[j] = make_uint4(d.x, d.y, d.z, d.w);
+    const int g = r / rpg;
+    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob,
+                                                           0, 0);
+    sc[j] = make_uint2(e.x, e.y);
+  }
+  constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;  // 16-byte x vectors per thread
+  uint4 xv[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int idx = tid + kThreads * i;
+    const int n = idx / kRows, rr = idx - n * kRows;
+    const bool ok = n < NT && n < a.M && rr < nrows;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(
+        ra, ok ? (uint32_t)(((size_t)n * a.K + 8 * (r_begin + rr)) * 2) : kOob, 0, 0);
+    xv[i] = make_uint4(d.x, d.y, d.z, d.w);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int idx = tid + kThreads * i;
+    const int n = idx / kRows, rr = idx - n * kRows;
+    if (n < NT) {
+      xs[n][rr] = pair_permute(xv[i]);
+      xb[n][rr] = q4_bias(xv[i]);
+    }
+  }
+  __syncthreads();
+
+  const uint32_t mq = q4_magic();
+  float acc[4][NT];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const int rl = j * kRowsPerStep + wave * 4 + rsub;
+    const float sv[4] = {bf16lo(sc[j].x), bf16hi(sc[j].x), bf16lo(sc[j].y), bf16hi(sc[j].y)};
+    const Q4Pairs u[4] = {unpack_q4(w[j].x, mq), unpack_q4(w[j].y, mq), unpack_q4(w[j].z, mq),
+                          unpack_q4(w[j].w, mq)};
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const uint4 xp = xs[n][rl];
+      const float bias = xb[n][rl];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q][n] = fmaf(sv[q], dot_unpacked(u[q], xp, bias), acc[q][n]);
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[q][n] = reduce_across_groups<16>(acc[q][n]);
+  if (rsub == 0) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[(wave * NT + n) * kCols + colq * 4 + q] = acc[q][n];
+  }
+  __syncthreads();
+  const int mt = min(NT, a.M);
+  for (int i = tid; i < mt * kCols; i += kThreads) {
+    const int n = i / kCols, cc = i - n * kCols;
+    const int oc = tile * kCols + cc;
+    if (oc < a.N) {
+      const float y = (red[(0 * NT + n) * kCols + cc] + red[(1 * NT + n) * kCols + cc]) +
+                      (red[(2 * NT + n) * kCols + cc] + red[(3 * NT + n) * kCols + cc]);
+      const size_t o = (size_t)n * a.N + oc;
+      if (a.ks == 1) a.C[o] = f32_to_bf16(epilogue(y, a.cap));
+      else st_coherent_f32(a.part + (size_t)split * a.M * a.N + o, y);
+    }
+  }
+  if (a.ks == 1) return;
+
+  // Last K slice to arrive for this column tile sums the partials in slice order.
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0) last = atomic_add_relaxed(&a.ctr[tile], 1) == a.ks - 1;
+  __syncthreads();
+  if (!last) return;
+  for (int i = tid; i < mt * kCols; i += kThreads) {
+    const int t = i / kCols, cc = i - t * kCols;
+    const int oc = tile * kCols + cc;
+    if (oc < a.N) {
+      const size_t o = (size_t)t * a.N + oc;
+      float y = 0.f;
+      for (int s2 = 0; s2 < a.ks; ++s2) y += ld_coherent_f32(a.part + (size_t)s2 * a.M * a.N + o);
+      a.C[o] = f32_to_bf16(epilogue(y, a.cap));
+    }
+  }
+  if (tid == 0) store_relaxed(&a.ctr[tile], 0);
+}
+
+// ---------------------------------------------------------------------------
 // Matrix-core path for a few token rows and a wide N (lm_head): with 3..16
 // rows the VALU dot products of the path above cost more than the weight
 // stream, so the products run on v_mfma_f32_16x16x32_bf16 with A = the token
@@ -326,10 +461,35 @@ struct Plan {
   size_t ctr_off, part_off, total;
 };
 
+constexpr int kGemvSteps[] = {1, 2, 3, 4, 6, 8, 12};
+// Split-K workspace: arrival counters at the front, partials from a fixed
+// offset.  Calls of different shapes share one workspace, so the counter
+// region must never be reused for partials (a counter left non-zero by
+// another call's partials breaks the last-arriver test): it is sized for
+// N <= 64 * 16384.
+constexpr size_t kCtrBytes = 16384 * sizeof(int);
+
 Plan make_plan(int M, int K, int N) {
   Plan p;
   const int Kp = K >> 3;
   p.tiles = (N + kCols - 1) / kCols;
+  if (M <= 8) {  // decode-shape path: S steps of 16 packed rows per K slice
+    p.nt = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;
+    int steps = kGemvSteps[6];
+    for (int st : kGemvSteps) {
+      const int ks = (Kp + st * kRowsPerStep - 1) / (st * kRowsPerStep);
+      if ((long)p.tiles * ks <= kGemvTargetWgs) {
+        steps = st;
+        break;
+      }
+    }
+    p.rows_per_split = steps * kRowsPerStep;
+    p.ks = (Kp + p.rows_per_split - 1) / p.rows_per_split;
+    p.ctr_off = 0;
+    p.part_off = kCtrBytes;
+    p.total = p.ks > 1 ? round_up(p.part_off + (size_t)p.ks * M * N * sizeof(float)) : 0;
+    return p;
+  }
   p.nt = M <= 1 ? 1 : (M <= 4 ? 4 : 8);
   int ks = (kTargetWgs + p.tiles - 1) / p.tiles;
   const int max_ks = (Kp + kRowsPerStep - 1) / kRowsPerStep;
@@ -349,7 +509,7 @@ Plan make_plan(int M, int K, int N) {
   p.ks = ks;
   p.rows_per_split = rps;
   p.ctr_off = 0;
-  p.part_off = round_up((size_t)p.tiles * sizeof(int));
+  p.part_off = kCtrBytes;
   p.total = ks > 1 ? round_up(p.part_off + (size_t)ks * M * N * sizeof(float)) : 0;
   return p;
 }
@@ -357,8 +517,9 @@ Plan make_plan(int M, int K, int N) {
 }  // namespace
 
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
-  (void)gs;
   if (M <= 0 || K <= 0 || N <= 0) return 0;
+  // the matrix-core path needs none (scales with the full ceil(K / gs) groups)
+  if (gs > 0 && mfma_path(M, K, N, gs, (K + gs - 1) / gs)) return 0;
   return make_plan(M, K, N).total;
 }
 
@@ -397,6 +558,8 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     return GI_OK;
   }
   const Plan p = make_plan(M, K, N);
+  if (p.ks > 1 && (size_t)p.tiles * sizeof(int) > kCtrBytes)
+    return fail(GI_ERR_UNSUPPORTED, "w4a16: N too large for the split-K path (N <= 1048576)");
   if (p.ks > 1) {
     if (!workspace || workspace_bytes < p.total)
       return fail(GI_ERR_WORKSPACE, "w4a16: workspace missing or smaller than gi_w4a16_workspace_bytes()");
@@ -419,8 +582,30 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
   k.rows_per_split = p.rows_per_split;
   k.stage_stride = p.rows_per_split;
   k.cap = softcap;
-  const size_t dyn = (size_t)p.nt * p.rows_per_split * (sizeof(uint4) + sizeof(float));
   const dim3 grid(p.tiles, p.ks);
+  if (M <= 8) {
+    const int steps = p.rows_per_split / kRowsPerStep;
+    switch (p.nt * 100 + steps) {
+#define GI_GEMV_CASE(NT, S)                                                                    \
+  case NT * 100 + S:                                                                           \
+    hipLaunchKernelGGL((w4a16_gemv_kernel<NT, S>), grid, dim3(kThreads), 0, stream, k); \
+    break;
+#define GI_GEMV_NT(NT) GI_GEMV_CASE(NT, 1) GI_GEMV_CASE(NT, 2) GI_GEMV_CASE(NT, 3) GI_GEMV_CASE(NT, 4) \
+  GI_GEMV_CASE(NT, 6) GI_GEMV_CASE(NT, 8) GI_GEMV_CASE(NT, 12)
+      GI_GEMV_NT(1)
+      GI_GEMV_NT(2)
+      GI_GEMV_NT(4)
+      GI_GEMV_NT(8)
+#undef GI_GEMV_NT
+#undef GI_GEMV_CASE
+      default:
+        return fail(GI_ERR_UNSUPPORTED, "w4a16: no decode-shape variant for this plan");
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
+    return GI_OK;
+  }
+  const size_t dyn = (size_t)p.nt * p.rows_per_split * (sizeof(uint4) + sizeof(float));
   if (p.nt == 1) hipLaunchKernelGGL(w4a16_kernel<1>, grid, dim3(kThreads), dyn, stream, k);
   else if (p.nt == 4) hipLaunchKernelGGL(w4a16_kernel<4>, grid, dim3(kThreads), dyn, stream, k);
   else hipLaunchKernelGGL(w4a16_kernel<8>, grid, dim3(kThreads), dyn, stream, k);
