@@ -320,6 +320,129 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// One or two token rows and K <= 8192: 16 columns per workgroup over ALL of
+// K, so N / 16 workgroups fill the chip without a K split and a launch has no
+// inter-workgroup exchange at all.  Lane (rrow = lane >> 2, colq = lane & 3)
+// loads the 16 bytes of columns 4colq..4colq+3 at packed row
+// 64j + 16wave + rrow: one wave instruction reads 16 rows x 64 B.  As in the
+// path above every load goes out first (weights, scales, then the token rows
+// into LDS), masked loads read zeros and zero scales cancel them.  The sums
+// over the 16 lanes of a column group: two DPP rotations inside each row of
+// 16 lanes, then the 16 (row, wave) partials of a column in LDS, added in a
+// fixed order.
+constexpr int kNarrowCols = 16;
+
+template <int NT, int S>
+__global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(GemvArgs a) {
+  constexpr int kRows = S * 64;  // packed rows covered (>= K / 8)
+  __shared__ uint4 xs[NT][kRows];
+  __shared__ float xb[NT][kRows];
+  __shared__ float red[kWaves * 4][NT][kNarrowCols];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int rrow = lane >> 2, colq = lane & 3;
+  const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  const int col = blockIdx.x * kNarrowCols + colq * 4;
+  const bool col_ok = col < a.N;
+
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, (uint32_t)((size_t)Kp * a.N * 4));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  uint4 w[S];
+  uint2 sc[S];
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const int r = 64 * j + 16 * wave + rrow;
+    const bool ok = col_ok && r < Kp;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * a.N + col) * 4) : kOob,
+                                                            0, kGemvNt);
+    w[j] = make_uint4(d.x, d.y, d.z, d.w);
+    const int g = r / rpg;
+    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob,
+                                                           0, 0);
+    sc[j] = make_uint2(e.x, e.y);
+  }
+  constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;
+  uint4 xv[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int idx = tid + kThreads * i;
+    const int n = idx / kRows, rr = idx - n * kRows;
+    const bool ok = n < NT && n < a.M && rr < Kp;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(ra, ok ? (uint32_t)(((size_t)n * a.K + 8 * rr) * 2) : kOob,
+                                                            0, 0);
+    xv[i] = make_uint4(d.x, d.y, d.z, d.w);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int idx = tid + kThreads * i;
+    const int n = idx / kRows, rr = idx - n * kRows;
+    if (n < NT) {
+      xs[n][rr] = pair_permute(xv[i]);
+      xb[n][rr] = q4_bias(xv[i]);
+    }
+  }
+  __syncthreads();
+
+  const uint32_t mq = q4_magic();
+  float acc[4][NT];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const int r = 64 * j + 16 * wave + rrow;
+    const float sv[4] = {bf16lo(sc[j].x), bf16hi(sc[j].x), bf16lo(sc[j].y), bf16hi(sc[j].y)};
+    const Q4Pairs u[4] = {unpack_q4(w[j].x, mq), unpack_q4(w[j].y, mq), unpack_q4(w[j].z, mq),
+                          unpack_q4(w[j].w, mq)};
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const uint4 xp = xs[n][r];
+      const float bias = xb[n][r];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q][n] = fmaf(sv[q], dot_unpacked(u[q], xp, bias), acc[q][n]);
+    }
+  }
+  // lanes c, c+4, c+8, c+12 of each 16-lane row share a column group
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      float v = acc[q][n];
+      v += dpp_f32<0x124>(v);  // row_ror:4
+      v += dpp_f32<0x128>(v);  // row_ror:8
+      acc[q][n] = v;
+    }
+  if ((lane & 15) < 4) {
+    const int slot = wave * 4 + (lane >> 4);
+#pragma unroll
+    for (int n = 0; n < NT; ++n)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) red[slot][n][colq * 4 + q] = acc[q][n];
+  }
+  __syncthreads();
+  if (tid < NT * kNarrowCols) {
+    const int n = tid / kNarrowCols, cc = tid - n * kNarrowCols;
+    const int oc = blockIdx.x * kNarrowCols + cc;
+    if (n < a.M && oc < a.N) {
+      float y = 0.f;
+#pragma unroll
+      for (int i = 0; i < kWaves * 4; ++i) y += red[i][n][cc];
+      a.C[(size_t)n * a.N + oc] = f32_to_bf16(epilogue(y, a.cap));
+    }
+  }
+}
+
+constexpr int kNarrowSteps[] = {2, 4, 6, 8, 12, 16};
+
+bool narrow_path(int M, int K, int N) {
+  const int Kp = K / 8;
+  return M <= 2 && Kp <= 64 * 16 && N >= 1024 && (size_t)Kp * N * 4 < (1ull << 32);
+}
+
+// ---------------------------------------------------------------------------
 // Matrix-core path for a few token rows and a wide N (lm_head): with 3..16
 // rows the VALU dot products of the path above cost more than the weight
 // stream, so the products run on v_mfma_f32_16x16x32_bf16 with A = the token
@@ -518,6 +641,7 @@ Plan make_plan(int M, int K, int N) {
 
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
+  if (narrow_path(M, K, N)) return 0;
   // the matrix-core path needs none (scales with the full ceil(K / gs) groups)
   if (gs > 0 && mfma_path(M, K, N, gs, (K + gs - 1) / gs)) return 0;
   return make_plan(M, K, N).total;
@@ -555,6 +679,45 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
       hipLaunchKernelGGL(w4a16_mfma_kernel<4>, dim3(N / kMfCols), dim3(kMfThreads), lds, stream, k);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "w4a16 matrix-core launch");
+    return GI_OK;
+  }
+  if (narrow_path(M, K, N)) {
+    GemvArgs k{};
+    k.A = (const uint16_t*)A;
+    k.B = B;
+    k.S = (const uint16_t*)scales;
+    k.C = (uint16_t*)C;
+    k.M = M;
+    k.K = K;
+    k.N = N;
+    k.gs = gs;
+    k.G = n_groups;
+    k.ks = 1;
+    k.cap = softcap;
+    const int need = (K / 8 + 63) / 64;
+    int steps = 16;
+    for (int st : kNarrowSteps)
+      if (st >= need) {
+        steps = st;
+        break;
+      }
+    const dim3 grid((unsigned)((N + kNarrowCols - 1) / kNarrowCols));
+    switch ((M <= 1 ? 100 : 200) + steps) {
+#define GI_NARROW_CASE(NT, S)                                                                    \
+  case NT * 100 + S:                                                                             \
+    hipLaunchKernelGGL((w4a16_narrow_kernel<NT, S>), grid, dim3(kThreads), 0, stream, k); \
+    break;
+#define GI_NARROW_NT(NT) GI_NARROW_CASE(NT, 2) GI_NARROW_CASE(NT, 4) GI_NARROW_CASE(NT, 6) \
+  GI_NARROW_CASE(NT, 8) GI_NARROW_CASE(NT, 12) GI_NARROW_CASE(NT, 16)
+      GI_NARROW_NT(1)
+      GI_NARROW_NT(2)
+#undef GI_NARROW_NT
+#undef GI_NARROW_CASE
+      default:
+        return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "w4a16 narrow launch");
     return GI_OK;
   }
   const Plan p = make_plan(M, K, N);
