@@ -674,7 +674,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
-    ap.add_argument("--workload", choices=["moe", "prefill", "dense", *LINEAR_WORKLOADS], default="moe",
+    ap.add_argument("--workload", choices=["moe", "prefill", "dense", "router", *LINEAR_WORKLOADS],
+                    default="moe",
                     help="moe (default: the BASELINE metric, M=1 value with M=7 beside it), prefill "
                          "(configs[3], M=512) or a dense W4A16 shape (linear = configs[0], "
                          "lm_head = configs[4])")
@@ -702,7 +703,7 @@ def main():
     if args.workload == "dense":
         print(json.dumps(bench_dense(args.steps, args.warmup, device)))
         return
-    if args.workload != "moe":
+    if args.workload not in ("moe", "router"):
         print(json.dumps(bench_linear(args.workload, args.steps, args.warmup, device,
                                       None if args.no_cpu_baseline else args.cpu_budget_s)))
         return
@@ -711,6 +712,23 @@ def main():
     print(f"[bench] weights ready: {COPIES} x {E} experts", file=sys.stderr, flush=True)
     if args.pmc_pass:
         pmc_pass(copies, args.steps, args.warmup, device)
+        return
+    if args.workload == "router":
+        fe = bench_front_end(copies, args.steps, device)
+        print(json.dumps({
+            "metric": "MoE router front-end us (gemma.py:75-76: router norm, router_scale, gate linear) "
+                      "at M=1 and M=7, one launch vs the module's torch statements (1 GPU)",
+            "value": fe["M1"]["fused_us"], "unit": "us", "n_gpus": 1, "steps": min(args.steps, 200),
+            "warmup": 4, "ms_per_step": fe["M1"]["fused_us"] / 1000.0, "higher_is_better": False,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic (N(0,1) bf16 hidden states, router weights of gemmainfer_amd.synth)",
+            "config": {"workload": "router: gi_moe_router_logits, one launch per step, 4 gate copies rotated",
+                       "hidden": H, "experts": E, "timing": "HIP graph of K steps, HIP events"},
+            "roofline": {"bound": "hbm", "achieved": fe["gate_bytes"] / (fe["M1"]["fused_us"] * 1e-6) / 1e9,
+                         "peak": PEAK_GBPS, "unit": "GB/s",
+                         "frac": fe["gate_bytes"] / (fe["M1"]["fused_us"] * 1e-6) / 1e9 / PEAK_GBPS,
+                         "traffic": None},
+            "cpu_baseline": None, "router_front_end": fe}))
         return
     m1 = bench_config(1, 0.0, 1, copies, args.steps, args.warmup, device)
     print(f"[bench] M=1 {m1['us_per_layer']:.2f} us {m1['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
