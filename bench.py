@@ -521,6 +521,63 @@ def bench_ingest(device):
             "launches": 2 * 3 * E}
 
 
+class FusedDenseRunner:
+    """A sliding-window layer's dense W4A16 work as this library's fused calls:
+    q, k, v in one gi_w4a16_linear_multi, o, the shared MLP's gate/up with the
+    gelu*up epilogue (gi_w4a16_gated_mlp) and down: 4 calls where the
+    reference makes 7 linears plus a gelu and a product.  Weight copies are
+    rotated past the MALL."""
+
+    def __init__(self, m, device):
+        self.lib = L.load()
+        self.m, self.dev = m, device
+        shp = {x[0]: (x[1], x[2]) for x in DENSE_PROJ}
+        per_copy = sum(linear_bytes(*shp[x], DENSE_GS) for x in SLIDING)
+        self.copies = max(2, math.ceil(600e6 / per_copy))
+        g = torch.Generator(device=device)
+        g.manual_seed(3)
+
+        def mk(k, n):
+            B = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), generator=g, device=device,
+                              dtype=torch.int64).to(torch.int32)
+            S = (torch.randn((math.ceil(k / DENSE_GS), n), generator=g, device=device).abs() * 0.02).to(torch.bfloat16)
+            return B, S
+        self.W = [{x: mk(*shp[x]) for x in SLIDING} for _ in range(self.copies)]
+        self.x = synth.activations(m, H, seed=1).to(device)
+        self.q = torch.empty(m, 4096, dtype=torch.bfloat16, device=device)
+        self.k = torch.empty(m, 2048, dtype=torch.bfloat16, device=device)
+        self.v = torch.empty(m, 2048, dtype=torch.bfloat16, device=device)
+        self.attn = synth.activations(m, 4096, seed=2).to(device)
+        self.o = torch.empty(m, H, dtype=torch.bfloat16, device=device)
+        self.act = torch.empty(m, 2112, dtype=torch.bfloat16, device=device)
+        self.y = torch.empty(m, H, dtype=torch.bfloat16, device=device)
+        nb = max([self.lib.gi_w4a16_workspace_bytes(m, shp[x][0], shp[x][1], DENSE_GS) for x in SLIDING] +
+                 [self.lib.gi_w4a16_gated_mlp_workspace_bytes(m, H, 2112, DENSE_GS)])
+        self.ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=device)
+        torch.cuda.synchronize()
+
+    def launch(self, i):
+        W = self.W[i % self.copies]
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        ws, wsn = p(self.ws), self.ws.numel()
+        vp3 = lambda ts: (ctypes.c_void_p * 3)(*[t.data_ptr() for t in ts])  # noqa: E731
+        L.check(self.lib.gi_w4a16_linear_multi(
+            p(self.x), L.DTYPE_BF16, 3, vp3([W["q"][0], W["k"][0], W["v"][0]]),
+            vp3([W["q"][1], W["k"][1], W["v"][1]]), (ctypes.c_int * 3)(*[W[x][1].shape[0] for x in "qkv"]),
+            vp3([self.q, self.k, self.v]), (ctypes.c_int * 3)(4096, 2048, 2048), self.m, H, DENSE_GS, ws, wsn,
+            stream), "qkv")
+        L.check(self.lib.gi_w4a16_linear(p(self.attn), L.DTYPE_BF16, p(W["o"][0]), p(W["o"][1]), W["o"][1].shape[0],
+                                         p(self.o), self.m, 4096, H, DENSE_GS, 0.0, ws, wsn, stream), "o")
+        L.check(self.lib.gi_w4a16_gated_mlp(
+            p(self.o), L.DTYPE_BF16, p(W["mlp_gate"][0]), p(W["mlp_gate"][1]), W["mlp_gate"][1].shape[0],
+            p(W["mlp_up"][0]), p(W["mlp_up"][1]), W["mlp_up"][1].shape[0], p(self.act), self.m, H, 2112, DENSE_GS,
+            ws, wsn, stream), "gated mlp")
+        L.check(self.lib.gi_w4a16_linear(p(self.act), L.DTYPE_BF16, p(W["mlp_down"][0]), p(W["mlp_down"][1]),
+                                         W["mlp_down"][1].shape[0], p(self.y), self.m, 2112, H, DENSE_GS, 0.0,
+                                         ws, wsn, stream), "down")
+
+
 def bench_dense(steps, warmup, device):
     res = {}
     for m in (1, 7):
@@ -537,8 +594,18 @@ def bench_dense(steps, warmup, device):
             torch.cuda.empty_cache()
         tot_us = sum(row[x]["us"] for x in SLIDING)
         tot_b = sum(row[x]["bytes"] for x in SLIDING)
+        fr = FusedDenseRunner(m, device)
+        for i in range(min(warmup, 5)):
+            fr.launch(i)
+        fused_us = time_graph(fr, list(range(min(steps, 200))), device)
+        del fr
+        torch.cuda.empty_cache()
         res[f"M{m}"] = {"sliding_layer_us": tot_us, "sliding_layer_gbps": tot_b / (tot_us * 1e-6) / 1e9,
-                        "sliding_layer_bytes": tot_b, "per_projection": row}
+                        "sliding_layer_bytes": tot_b, "per_projection": row,
+                        "sliding_layer_fused_us": fused_us,
+                        "sliding_layer_fused_gbps": tot_b / (fused_us * 1e-6) / 1e9}
+        print(f"[bench] dense M={m}: fused calls (qkv, o, gated mlp, down) {fused_us:.1f} us", file=sys.stderr,
+              flush=True)
         print(f"[bench] dense M={m}: sliding layer {tot_us:.1f} us, "
               f"{res[f'M{m}']['sliding_layer_gbps']:.0f} GB/s", file=sys.stderr, flush=True)
     ing = bench_ingest(device)

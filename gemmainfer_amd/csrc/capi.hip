@@ -214,6 +214,29 @@ int gi_w4a16_linear(const void* A, int a_dtype, const int32_t* B_packed, const v
                           workspace, workspace_bytes, as_stream(stream));
 }
 
+int gi_w4a16_linear_multi(const void* A, int a_dtype, int n_proj, const int32_t* const* B_packed,
+                          const void* const* scales, const int* n_groups, void* const* C, const int* N, int M,
+                          int K, int group_size, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_bf16_x(a_dtype, "w4a16_linear_multi");
+  if (st != GI_OK) return st;
+  return gi::launch_w4a16_multi(A, n_proj, B_packed, scales, n_groups, C, N, M, K, group_size, workspace,
+                                workspace_bytes, as_stream(stream));
+}
+
+size_t gi_w4a16_gated_mlp_workspace_bytes(int M, int K, int N, int group_size) {
+  return gi::w4a16_gated_workspace_bytes(M, K, N, group_size);
+}
+
+int gi_w4a16_gated_mlp(const void* A, int a_dtype, const int32_t* gate_packed, const void* gate_scales,
+                       int gate_groups, const int32_t* up_packed, const void* up_scales, int up_groups, void* out,
+                       int M, int K, int N, int group_size, void* workspace, size_t workspace_bytes,
+                       void* stream) {
+  int st = check_bf16_x(a_dtype, "w4a16_gated_mlp");
+  if (st != GI_OK) return st;
+  return gi::launch_w4a16_gated(A, gate_packed, gate_scales, gate_groups, up_packed, up_scales, up_groups, out, M,
+                                K, N, group_size, workspace, workspace_bytes, as_stream(stream));
+}
+
 int gi_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int N,
                     int K, int n_groups, int32_t* packed_out, void* scales_out, int64_t ld_out,
                     void* stream) {

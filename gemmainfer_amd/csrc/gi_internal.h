@@ -72,6 +72,13 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
                  int M, int K, int N, int gs, float softcap, void* workspace,
                  size_t workspace_bytes, hipStream_t stream);
 
+int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void* const* scales, const int* n_groups,
+                       void* const* C, const int* N, int M, int K, int gs, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+size_t w4a16_gated_workspace_bytes(int M, int K, int N, int gs);
+int launch_w4a16_gated(const void* A, const int32_t* gB, const void* gS, int gG, const int32_t* uB, const void* uS,
+                       int uG, void* out, int M, int K, int N, int gs, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
 int launch_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int N,
                         int K, int n_groups, int32_t* packed_out, void* scales_out, int64_t ld_out,
                         hipStream_t stream);

@@ -331,37 +331,111 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
 // 16 lanes, then the 16 (row, wave) partials of a column in LDS, added in a
 // fixed order.
 constexpr int kNarrowCols = 16;
+constexpr int kMaxSegs = 4;
 
-template <int NT, int S>
-__global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(GemvArgs a) {
-  constexpr int kRows = S * 64;  // packed rows covered (>= K / 8)
-  __shared__ uint4 xs[NT][kRows];
-  __shared__ float xb[NT][kRows];
-  __shared__ float red[kWaves * 4][NT][kNarrowCols];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int rrow = lane >> 2, colq = lane & 3;
-  const int Kp = a.K >> 3, rpg = a.gs >> 3;
-  const int col = blockIdx.x * kNarrowCols + colq * 4;
-  const bool col_ok = col < a.N;
+// Several projections of the same token rows in one launch: segment s owns
+// column tiles [tile0, tile0 + ceil(N / 16)).  GATED: segments 0 and 1 are
+// the gate and up projections of a gated MLP with the same N; every
+// workgroup computes both for its 16 columns and writes
+// bf16(bf16(gelu_tanh(bf16(gate))) * bf16(up)) to segment 0's output.
+struct NarrowSeg {
+  const int32_t* B;  // [K/8, N]
+  const uint16_t* S; // [G, N]
+  uint16_t* C;       // [M, N]
+  int N, G, tile0;
+};
+struct NarrowArgs {
+  const uint16_t* A;  // [M, K]
+  int M, K, gs, nseg;
+  float cap;
+  NarrowSeg seg[kMaxSegs];
+};
 
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, (uint32_t)((size_t)Kp * a.N * 4));
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
-  constexpr uint32_t kOob = 0xFFFFFFF0u;
+template <int S>
+struct NarrowW {
   uint4 w[S];
   uint2 sc[S];
+};
+
+template <int S>
+__device__ __forceinline__ void narrow_issue(const NarrowSeg& sg, int Kp, int rpg, int col, int wave, int rrow,
+                                             NarrowW<S>& o) {
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(sg.B, (uint32_t)((size_t)Kp * sg.N * 4));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sg.S, (uint32_t)((size_t)sg.G * sg.N * 2));
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  const bool col_ok = col < sg.N;
 #pragma unroll
   for (int j = 0; j < S; ++j) {
     const int r = 64 * j + 16 * wave + rrow;
     const bool ok = col_ok && r < Kp;
-    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * a.N + col) * 4) : kOob,
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * sg.N + col) * 4) : kOob,
                                                             0, kGemvNt);
-    w[j] = make_uint4(d.x, d.y, d.z, d.w);
+    o.w[j] = make_uint4(d.x, d.y, d.z, d.w);
     const int g = r / rpg;
-    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob,
+    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < sg.G) ? (uint32_t)((g * sg.N + col) * 2) : kOob,
                                                            0, 0);
-    sc[j] = make_uint2(e.x, e.y);
+    o.sc[j] = make_uint2(e.x, e.y);
   }
+}
+
+template <int NT, int S, int kRows>
+__device__ __forceinline__ void narrow_products(const NarrowW<S>& in, const uint4 (&xs)[NT][kRows],
+                                                const float (&xb)[NT][kRows], int wave, int rrow, uint32_t mq,
+                                                float (&acc)[4][NT]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const int r = 64 * j + 16 * wave + rrow;
+    const float sv[4] = {bf16lo(in.sc[j].x), bf16hi(in.sc[j].x), bf16lo(in.sc[j].y), bf16hi(in.sc[j].y)};
+    const Q4Pairs u[4] = {unpack_q4(in.w[j].x, mq), unpack_q4(in.w[j].y, mq), unpack_q4(in.w[j].z, mq),
+                          unpack_q4(in.w[j].w, mq)};
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const uint4 xp = xs[n][r];
+      const float bias = xb[n][r];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) acc[q][n] = fmaf(sv[q], dot_unpacked(u[q], xp, bias), acc[q][n]);
+    }
+  }
+  // lanes c, c+4, c+8, c+12 of each 16-lane row share a column group
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      float v = acc[q][n];
+      v += dpp_f32<0x124>(v);  // row_ror:4
+      v += dpp_f32<0x128>(v);  // row_ror:8
+      acc[q][n] = v;
+    }
+}
+
+template <int NT, int S, bool GATED>
+__global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
+  constexpr int kRows = S * 64;  // packed rows covered (>= K / 8)
+  constexpr int kOut = GATED ? 2 : 1;
+  __shared__ uint4 xs[NT][kRows];
+  __shared__ float xb[NT][kRows];
+  __shared__ float red[kOut][kWaves * 4][NT][kNarrowCols];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int rrow = lane >> 2, colq = lane & 3;
+  const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  // the workgroup's segment, by uniform selects (no dynamic kernarg index)
+  NarrowSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i)
+    if (!GATED && (int)blockIdx.x >= a.seg[i].tile0) sg = a.seg[i];
+  const int c0 = ((int)blockIdx.x - sg.tile0) * kNarrowCols;
+  const int col = c0 + colq * 4;
+
+  NarrowW<S> w0;
+  narrow_issue<S>(sg, Kp, rpg, col, wave, rrow, w0);
+  NarrowW<S> w1;
+  if constexpr (GATED) narrow_issue<S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
   constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;
   uint4 xv[kXPer];
 #pragma unroll
@@ -386,51 +460,46 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(GemvArgs a) {
   __syncthreads();
 
   const uint32_t mq = q4_magic();
-  float acc[4][NT];
+  const int slot = wave * 4 + (lane >> 4);
+  {
+    float acc[4][NT];
+    narrow_products<NT, S, kRows>(w0, xs, xb, wave, rrow, mq, acc);
+    if ((lane & 15) < 4) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+      for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
-#pragma unroll
-  for (int j = 0; j < S; ++j) {
-    const int r = 64 * j + 16 * wave + rrow;
-    const float sv[4] = {bf16lo(sc[j].x), bf16hi(sc[j].x), bf16lo(sc[j].y), bf16hi(sc[j].y)};
-    const Q4Pairs u[4] = {unpack_q4(w[j].x, mq), unpack_q4(w[j].y, mq), unpack_q4(w[j].z, mq),
-                          unpack_q4(w[j].w, mq)};
-#pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      const uint4 xp = xs[n][r];
-      const float bias = xb[n][r];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) acc[q][n] = fmaf(sv[q], dot_unpacked(u[q], xp, bias), acc[q][n]);
+        for (int q = 0; q < 4; ++q) red[0][slot][n][colq * 4 + q] = acc[q][n];
     }
   }
-  // lanes c, c+4, c+8, c+12 of each 16-lane row share a column group
+  if constexpr (GATED) {
+    float acc[4][NT];
+    narrow_products<NT, S, kRows>(w1, xs, xb, wave, rrow, mq, acc);
+    if ((lane & 15) < 4) {
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+      for (int n = 0; n < NT; ++n)
 #pragma unroll
-    for (int n = 0; n < NT; ++n) {
-      float v = acc[q][n];
-      v += dpp_f32<0x124>(v);  // row_ror:4
-      v += dpp_f32<0x128>(v);  // row_ror:8
-      acc[q][n] = v;
+        for (int q = 0; q < 4; ++q) red[kOut - 1][slot][n][colq * 4 + q] = acc[q][n];
     }
-  if ((lane & 15) < 4) {
-    const int slot = wave * 4 + (lane >> 4);
-#pragma unroll
-    for (int n = 0; n < NT; ++n)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) red[slot][n][colq * 4 + q] = acc[q][n];
   }
   __syncthreads();
   if (tid < NT * kNarrowCols) {
     const int n = tid / kNarrowCols, cc = tid - n * kNarrowCols;
-    const int oc = blockIdx.x * kNarrowCols + cc;
-    if (n < a.M && oc < a.N) {
+    const int oc = c0 + cc;
+    if (n < a.M && oc < sg.N) {
       float y = 0.f;
 #pragma unroll
-      for (int i = 0; i < kWaves * 4; ++i) y += red[i][n][cc];
-      a.C[(size_t)n * a.N + oc] = f32_to_bf16(epilogue(y, a.cap));
+      for (int i = 0; i < kWaves * 4; ++i) y += red[0][i][n][cc];
+      if constexpr (GATED) {
+        float u = 0.f;
+#pragma unroll
+        for (int i = 0; i < kWaves * 4; ++i) u += red[kOut - 1][i][n][cc];
+        // activations.py:26-28 on bf16 tensors: each linear's output, the
+        // gelu and the product are rounded to bf16
+        const float g = round_to_bf16(gelu_tanh(round_to_bf16(y)));
+        sg.C[(size_t)n * sg.N + oc] = f32_to_bf16(g * round_to_bf16(u));
+      } else {
+        sg.C[(size_t)n * sg.N + oc] = f32_to_bf16(epilogue(y, a.cap));
+      }
     }
   }
 }
@@ -440,6 +509,51 @@ constexpr int kNarrowSteps[] = {2, 4, 6, 8, 12, 16};
 bool narrow_path(int M, int K, int N) {
   const int Kp = K / 8;
   return M <= 2 && Kp <= 64 * 16 && N >= 1024 && (size_t)Kp * N * 4 < (1ull << 32);
+}
+
+int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSeg* segs, int nseg, bool gated,
+                  hipStream_t stream) {
+  NarrowArgs k{};
+  k.A = (const uint16_t*)A;
+  k.M = M;
+  k.K = K;
+  k.gs = gs;
+  k.cap = cap;
+  k.nseg = nseg;
+  int tiles = 0;
+  for (int i = 0; i < nseg; ++i) {
+    k.seg[i] = segs[i];
+    k.seg[i].tile0 = gated ? 0 : tiles;
+    if (!gated) tiles += (segs[i].N + kNarrowCols - 1) / kNarrowCols;
+  }
+  if (gated) tiles = (segs[0].N + kNarrowCols - 1) / kNarrowCols;
+  for (int i = nseg; i < kMaxSegs; ++i) k.seg[i].tile0 = 0x7fffffff;
+  const int need = (K / 8 + 63) / 64;
+  int steps = 16;
+  for (int st : kNarrowSteps)
+    if (st >= need) {
+      steps = st;
+      break;
+    }
+  const dim3 grid((unsigned)tiles);
+  switch ((gated ? 1000 : 0) + (M <= 1 ? 100 : 200) + steps) {
+#define GI_NARROW_CASE(G, NT, S)                                                                          \
+  case (G ? 1000 : 0) + NT * 100 + S:                                                                     \
+    hipLaunchKernelGGL((w4a16_narrow_kernel<NT, S, G>), grid, dim3(kThreads), 0, stream, k); \
+    break;
+#define GI_NARROW_NT(G, NT) GI_NARROW_CASE(G, NT, 2) GI_NARROW_CASE(G, NT, 4) GI_NARROW_CASE(G, NT, 6) \
+  GI_NARROW_CASE(G, NT, 8) GI_NARROW_CASE(G, NT, 12) GI_NARROW_CASE(G, NT, 16)
+    GI_NARROW_NT(false, 1)
+    GI_NARROW_NT(false, 2)
+    GI_NARROW_NT(true, 1)
+    GI_NARROW_NT(true, 2)
+#undef GI_NARROW_NT
+#undef GI_NARROW_CASE
+    default:
+      return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 narrow launch");
 }
 
 // ---------------------------------------------------------------------------
@@ -682,43 +796,8 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     return GI_OK;
   }
   if (narrow_path(M, K, N)) {
-    GemvArgs k{};
-    k.A = (const uint16_t*)A;
-    k.B = B;
-    k.S = (const uint16_t*)scales;
-    k.C = (uint16_t*)C;
-    k.M = M;
-    k.K = K;
-    k.N = N;
-    k.gs = gs;
-    k.G = n_groups;
-    k.ks = 1;
-    k.cap = softcap;
-    const int need = (K / 8 + 63) / 64;
-    int steps = 16;
-    for (int st : kNarrowSteps)
-      if (st >= need) {
-        steps = st;
-        break;
-      }
-    const dim3 grid((unsigned)((N + kNarrowCols - 1) / kNarrowCols));
-    switch ((M <= 1 ? 100 : 200) + steps) {
-#define GI_NARROW_CASE(NT, S)                                                                    \
-  case NT * 100 + S:                                                                             \
-    hipLaunchKernelGGL((w4a16_narrow_kernel<NT, S>), grid, dim3(kThreads), 0, stream, k); \
-    break;
-#define GI_NARROW_NT(NT) GI_NARROW_CASE(NT, 2) GI_NARROW_CASE(NT, 4) GI_NARROW_CASE(NT, 6) \
-  GI_NARROW_CASE(NT, 8) GI_NARROW_CASE(NT, 12) GI_NARROW_CASE(NT, 16)
-      GI_NARROW_NT(1)
-      GI_NARROW_NT(2)
-#undef GI_NARROW_NT
-#undef GI_NARROW_CASE
-      default:
-        return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
-    }
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return hip_fail(e, "w4a16 narrow launch");
-    return GI_OK;
+    NarrowSeg sg{B, (const uint16_t*)scales, (uint16_t*)C, N, n_groups, 0};
+    return launch_narrow(A, M, K, gs, softcap, &sg, 1, false, stream);
   }
   const Plan p = make_plan(M, K, N);
   if (p.ks > 1 && (size_t)p.tiles * sizeof(int) > kCtrBytes)
@@ -775,6 +854,103 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "w4a16 launch");
   return GI_OK;
+}
+
+// ---- several projections of one input, and the gated MLP --------------------
+namespace {
+
+int check_linear(const void* A, const int32_t* B, const void* scales, int n_groups, const void* C, int M, int K,
+                 int N, int gs, const char* who) {
+  if (M < 0 || K <= 0 || N <= 0) return fail(GI_ERR_INVALID_ARG, std::string(who) + ": K, N > 0 and M >= 0 required");
+  if (K % 8 || N % 4) return fail(GI_ERR_INVALID_ARG, std::string(who) + ": K % 8 == 0 and N % 4 == 0 required");
+  if (gs <= 0 || gs % 8 || n_groups <= 0)
+    return fail(GI_ERR_INVALID_ARG, std::string(who) + ": bad group size or group count");
+  if (!A || !B || !scales || !C) return fail(GI_ERR_INVALID_ARG, std::string(who) + ": null tensor pointer");
+  if ((((uintptr_t)A) | ((uintptr_t)B)) % 16 || ((uintptr_t)scales) % 8)
+    return fail(GI_ERR_INVALID_ARG, std::string(who) + ": A/B_packed 16-byte and scales 8-byte alignment required");
+  return GI_OK;
+}
+
+bool narrow_multi(int M, int K, const int* N, int n) {
+  if (M > 2 || K / 8 > 64 * 16) return false;
+  long total = 0;
+  for (int i = 0; i < n; ++i) {
+    if ((size_t)(K / 8) * N[i] * 4 >= (1ull << 32)) return false;
+    total += N[i];
+  }
+  return total >= 1024;
+}
+
+__global__ __launch_bounds__(256) void gelu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float gl = round_to_bf16(gelu_tanh(bf16_to_f32(g[i])));
+    out[i] = f32_to_bf16(gl * bf16_to_f32(u[i]));
+  }
+}
+
+size_t gated_tmp_off(int M, int K, int N) { return round_up(make_plan(M, K, N).total); }
+
+}  // namespace
+
+int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void* const* scales, const int* n_groups,
+                       void* const* C, const int* N, int M, int K, int gs, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  if (n <= 0 || n > kMaxSegs) return fail(GI_ERR_INVALID_ARG, "w4a16_multi: 1 to 4 projections");
+  if (!B || !scales || !n_groups || !C || !N) return fail(GI_ERR_INVALID_ARG, "w4a16_multi: null array");
+  for (int i = 0; i < n; ++i) {
+    const int st = check_linear(A, B[i], scales[i], n_groups[i], C[i], M, K, N[i], gs, "w4a16_multi");
+    if (st != GI_OK) return st;
+  }
+  if (M == 0) return GI_OK;
+  if (narrow_multi(M, K, N, n)) {
+    NarrowSeg sg[kMaxSegs];
+    for (int i = 0; i < n; ++i) sg[i] = NarrowSeg{B[i], (const uint16_t*)scales[i], (uint16_t*)C[i], N[i], n_groups[i], 0};
+    return launch_narrow(A, M, K, gs, 0.f, sg, n, false, stream);
+  }
+  for (int i = 0; i < n; ++i) {
+    const int st = launch_w4a16(A, B[i], scales[i], n_groups[i], C[i], M, K, N[i], gs, 0.f, workspace,
+                                workspace_bytes, stream);
+    if (st != GI_OK) return st;
+  }
+  return GI_OK;
+}
+
+size_t w4a16_gated_workspace_bytes(int M, int K, int N, int gs) {
+  if (M <= 0 || K <= 0 || N <= 0) return 0;
+  if (M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32)) return 0;
+  (void)gs;
+  return gated_tmp_off(M, K, N) + 2 * round_up((size_t)M * N * 2);
+}
+
+int launch_w4a16_gated(const void* A, const int32_t* gB, const void* gS, int gG, const int32_t* uB, const void* uS,
+                       int uG, void* out, int M, int K, int N, int gs, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream) {
+  int st = check_linear(A, gB, gS, gG, out, M, K, N, gs, "w4a16_gated_mlp");
+  if (st != GI_OK) return st;
+  st = check_linear(A, uB, uS, uG, out, M, K, N, gs, "w4a16_gated_mlp");
+  if (st != GI_OK) return st;
+  if (M == 0) return GI_OK;
+  if (M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32)) {
+    const NarrowSeg sg[2] = {NarrowSeg{gB, (const uint16_t*)gS, (uint16_t*)out, N, gG, 0},
+                             NarrowSeg{uB, (const uint16_t*)uS, nullptr, N, uG, 0}};
+    return launch_narrow(A, M, K, gs, 0.f, sg, 2, true, stream);
+  }
+  const size_t need = w4a16_gated_workspace_bytes(M, K, N, gs);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace) % kAlign)
+    return fail(GI_ERR_WORKSPACE, "w4a16_gated_mlp: workspace missing, misaligned or smaller than "
+                                  "gi_w4a16_gated_mlp_workspace_bytes()");
+  uint16_t* tg = (uint16_t*)((char*)workspace + gated_tmp_off(M, K, N));
+  uint16_t* tu = (uint16_t*)((char*)tg + round_up((size_t)M * N * 2));
+  st = launch_w4a16(A, gB, gS, gG, tg, M, K, N, gs, 0.f, workspace, workspace_bytes, stream);
+  if (st != GI_OK) return st;
+  st = launch_w4a16(A, uB, uS, uG, tu, M, K, N, gs, 0.f, workspace, workspace_bytes, stream);
+  if (st != GI_OK) return st;
+  const int64_t n = (int64_t)M * N;
+  const int blocks = (int)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(gelu_mul_kernel, dim3(blocks), dim3(256), 0, stream, tg, tu, (uint16_t*)out, n);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16_gated_mlp launch");
 }
 
 }  // namespace gi

@@ -390,6 +390,66 @@ def w4a16_linear(A, B_packed, scales, group_size, softcap: Optional[float] = Non
     return C
 
 
+def _linear_operands(A, B_packed, scales, who):
+    _require(B_packed.dim() == 2 and B_packed.dtype == torch.int32 and B_packed.shape[0] * 8 == A.shape[1],
+             f"{who}: B_packed must be int32 [K/8, N] with K={A.shape[1]}, got {tuple(B_packed.shape)}")
+    _require(scales.dim() == 2 and scales.shape[1] == B_packed.shape[1] and scales.dtype == A.dtype,
+             f"{who}: scales must be [groups, N] of A's dtype")
+    _require(B_packed.is_contiguous() and scales.is_contiguous(), f"{who}: B_packed/scales must be contiguous")
+
+
+def w4a16_linear_multi(A, weights, group_size):
+    """Several W4A16 projections of the same rows (the q, k, v marlin_w4a16 calls
+    of attention.py:115-122) in one call: one launch for one or two rows.
+    ``weights`` is a list of up to 4 (B_packed, scales); returns the outputs."""
+    dev = _on_device(A, *[t for w in weights for t in w])
+    _require_bf16(A, "w4a16_linear_multi")
+    _require(A.dim() == 2, "A must be [M, K]")
+    _require(1 <= len(weights) <= 4, "1 to 4 projections")
+    m, k = A.shape
+    for B, S in weights:
+        _linear_operands(A, B, S, "w4a16_linear_multi")
+    outs = [torch.empty((m, B.shape[1]), dtype=A.dtype, device=dev) for B, _ in weights]
+    if m == 0:
+        return outs
+    lib = L.load()
+    nbytes = max(lib.gi_w4a16_workspace_bytes(m, k, B.shape[1], group_size) for B, _ in weights)
+    ws = _WS.get("w4a16", dev, nbytes) if nbytes else None
+    n = len(weights)
+    arr = lambda vals: (ctypes.c_void_p * n)(*[v.data_ptr() for v in vals])  # noqa: E731
+    L.check(lib.gi_w4a16_linear_multi(
+        _ptr(A.contiguous()), L.DTYPE_BF16, n, arr([B for B, _ in weights]), arr([S for _, S in weights]),
+        (ctypes.c_int * n)(*[S.shape[0] for _, S in weights]), arr(outs),
+        (ctypes.c_int * n)(*[B.shape[1] for B, _ in weights]), m, k, int(group_size), _ptr(ws),
+        0 if ws is None else ws.numel(), _stream(dev)), "w4a16_linear_multi")
+    return outs
+
+
+def gated_mlp_act(A, gate, up, group_size):
+    """GemmaMLP's ``gelu_tanh(gate_proj(x)) * up_proj(x)`` (activations.py:26-28)
+    with the bf16 roundings of those torch statements; one launch for one or
+    two rows.  ``gate`` and ``up`` are (B_packed, scales); returns bf16 [M, N]."""
+    dev = _on_device(A, *gate, *up)
+    _require_bf16(A, "gated_mlp_act")
+    _require(A.dim() == 2, "A must be [M, K]")
+    _linear_operands(A, *gate, "gated_mlp_act")
+    _linear_operands(A, *up, "gated_mlp_act")
+    _require(gate[0].shape == up[0].shape, "gate and up projections must have the same shape")
+    m, k = A.shape
+    n = gate[0].shape[1]
+    out = torch.empty((m, n), dtype=A.dtype, device=dev)
+    if m == 0:
+        return out
+    lib = L.load()
+    nbytes = lib.gi_w4a16_gated_mlp_workspace_bytes(m, k, n, group_size)
+    ws = _WS.get("w4a16", dev, nbytes) if nbytes else None
+    L.check(lib.gi_w4a16_gated_mlp(
+        _ptr(A.contiguous()), L.DTYPE_BF16, _ptr(gate[0]), _ptr(gate[1]), gate[1].shape[0], _ptr(up[0]),
+        _ptr(up[1]), up[1].shape[0], _ptr(out), m, k, n, int(group_size), _ptr(ws),
+        0 if ws is None else ws.numel(), _stream(dev)), "gated_mlp_act")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # companions
 # ---------------------------------------------------------------------------

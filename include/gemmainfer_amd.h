@@ -23,6 +23,8 @@
  *   gi_moe_router_logits        <- gemma.py:75-76 (router norm, router_scale, gate linear;
  *                                  torch ops there, rmsnorm.cu:16-73 for the norm)
  *   gi_moe_layer_from_hidden    <- gemma.py:75-98 (the MoE block's forward)
+ *   gi_w4a16_linear_multi       <- the q/k/v marlin_w4a16 calls of attention.py:115-122
+ *   gi_w4a16_gated_mlp          <- GemmaMLP gate/up + gelu * up (activations.py:26-28)
  *   gi_w4a16_ingest             <- gemmainfer/utils/weights.py:100-159 (checkpoint
  *                                  transposition of weight_packed / weight_scale)
  *   gi_softcap_inplace          <- gemmainfer_csrc.softcapping
@@ -185,6 +187,34 @@ int gi_w4a16_linear(const void* A, int a_dtype,
                     const int32_t* B_packed, const void* scales, int n_groups,
                     void* C, int M, int K, int N, int group_size, float softcap,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- f4: dense callers ----------------------------------------------------
+ * Several W4A16 projections of the same rows A[M, K] in one launch: the q, k
+ * and v projections of attention.py:115-122 (three marlin_w4a16 calls on one
+ * input there).  C[i][M, N[i]] = A @ dequant(B_packed[i], scales[i]) for
+ * i < n_proj <= 4.  One launch when M <= 2 and K <= 8192 (16-column tiles
+ * of every projection in one grid); otherwise one gi_w4a16_linear per
+ * projection, in order, sharing the workspace (size it with the largest
+ * gi_w4a16_workspace_bytes of the projections).  Arrays are host memory.   */
+int gi_w4a16_linear_multi(const void* A, int a_dtype, int n_proj,
+                          const int32_t* const* B_packed, const void* const* scales,
+                          const int* n_groups, void* const* C, const int* N,
+                          int M, int K, int group_size,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* The gated MLP's first half (activations.py:26-28):
+ *   out[M, N] = bf16( bf16(gelu_tanh(bf16(A @ Wg))) * bf16(A @ Wu) )
+ * with the bf16 roundings of the torch statements.  M <= 2, K <= 8192: one
+ * launch (both projections per 16-column tile, the gelu and product in the
+ * epilogue, no workspace).  Otherwise two linears into the workspace and an
+ * elementwise launch; size the workspace with
+ * gi_w4a16_gated_mlp_workspace_bytes (0 for the one-launch shapes).       */
+size_t gi_w4a16_gated_mlp_workspace_bytes(int M, int K, int N, int group_size);
+int gi_w4a16_gated_mlp(const void* A, int a_dtype,
+                       const int32_t* gate_packed, const void* gate_scales, int gate_groups,
+                       const int32_t* up_packed, const void* up_scales, int up_groups,
+                       void* out, int M, int K, int N, int group_size,
+                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- f4: checkpoint ingest ------------------------------------------------
  * Replaces the `t.t()` + copy of weights.py:100-159 that turns a

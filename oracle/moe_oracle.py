@@ -31,6 +31,8 @@ Pinning (what checks this restatement, see tests/test_oracle.py):
                         elementwise ops (the statements of gemma.py:75); the
                         gate against torch.nn.functional.linear in bf16;
                         closed forms (constant rows, identity gate).
+  gated_mlp_act         the torch statements (F.gelu approximate='tanh' and the
+                        product on bf16 tensors) on the same bf16 linear outputs.
   from_compressed       scalar brute force over the compressed-tensors layout
                         (nibble i of word [n][j] is k = 8j + i); round trip
                         through the transposed writer.
@@ -196,6 +198,14 @@ def gelu_tanh(x) -> np.ndarray:
     F.gelu(approximate='tanh') at gemma.py:137, pybind.cpp:237)."""
     x = np.asarray(x, dtype=np.float64)
     return 0.5 * x * (1.0 + np.tanh(GELU_C * (x + GELU_A * x * x * x)))
+
+
+def gated_mlp_act(a, gate, up, group_size) -> np.ndarray:
+    """GemmaMLP's first half on bf16 tensors (activations.py:26-28):
+    bf16(bf16(gelu_tanh(bf16(a @ Wg))) * bf16(a @ Wu)); gate/up = (packed, scales)."""
+    g = bf16_round(w4a16_linear(a, *gate, group_size))
+    u = bf16_round(w4a16_linear(a, *up, group_size))
+    return bf16_round(bf16_round(gelu_tanh(g)) * u)
 
 
 def softcap(y, cap) -> np.ndarray:

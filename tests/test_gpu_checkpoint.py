@@ -142,3 +142,37 @@ def test_dense_callers_gemma_gs64(name, m):
     cols = torch.randperm(n, generator=torch.Generator().manual_seed(m))[:384].sort().values
     ref = O.w4a16_linear(np64(A), B[:, cols].numpy(), np64(S[:, cols]), 64)
     assert_bf16_close(C_[:, cols.to(DEV)], ref, f"dense {name} m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 7])
+def test_linear_multi_qkv(m):
+    """q, k, v of one input in one call: equal to three separate linears, and to
+    the oracle on sampled columns."""
+    print(f"qkv m={m}", flush=True)
+    shapes = [(2816, 4096), (2816, 2048), (2816, 2048)]
+    W = [synth.linear_weights(k, n, 64, seed=50 + i) for i, (k, n) in enumerate(shapes)]
+    Wd = [(B.to(DEV), S.to(DEV)) for B, S in W]
+    A = synth.activations(m, 2816, seed=60 + m).to(DEV)
+    outs = ops.w4a16_linear_multi(A, Wd, 64)
+    for i, ((B, S), (Bd, Sd)) in enumerate(zip(W, Wd)):
+        sep = ops.w4a16_linear(A, Bd, Sd, 64)
+        assert torch.equal(outs[i], sep), f"projection {i}"
+        cols = torch.arange(0, B.shape[1], 17)
+        ref = O.w4a16_linear(np64(A), B[:, cols].numpy(), np64(S[:, cols]), 64)
+        assert_bf16_close(outs[i][:, cols.to(DEV)], ref, f"qkv[{i}] m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2, 7, 64])
+def test_gated_mlp_act(m):
+    """Shared-MLP gate/up with the gelu*up epilogue (one launch at 1-2 rows)
+    against the oracle of activations.py:26-28."""
+    print(f"gated mlp m={m}", flush=True)
+    k, n = 2816, 2112
+    G = synth.linear_weights(k, n, 64, seed=70)
+    U = synth.linear_weights(k, n, 64, seed=71)
+    A = synth.activations(m, k, seed=72 + m)
+    out = ops.gated_mlp_act(A.to(DEV), (G[0].to(DEV), G[1].to(DEV)), (U[0].to(DEV), U[1].to(DEV)), 64)
+    cols = torch.arange(0, n, 11)
+    ref = O.gated_mlp_act(np64(A), (G[0][:, cols].numpy(), np64(G[1][:, cols])),
+                          (U[0][:, cols].numpy(), np64(U[1][:, cols])), 64)
+    assert_bf16_close(out[:, cols.to(DEV)], ref, f"gated mlp m={m}")

@@ -158,6 +158,23 @@ def test_elementwise_golden_roundtrip():
                                rtol=2.0 ** -6, atol=1e-6)
 
 
+def test_gated_mlp_act_matches_torch_statements():
+    """activations.py:26-28 on bf16 tensors: F.gelu(approximate='tanh') of the
+    bf16 gate output, times the bf16 up output, each rounded to bf16."""
+    B1, S1 = synth.linear_weights(256, 96, 64, seed=41)
+    B2, S2 = synth.linear_weights(256, 96, 64, seed=42)
+    a = synth.activations(3, 256, seed=43)
+    ours = O.gated_mlp_act(t64(a), (B1.numpy(), t64(S1)), (B2.numpy(), t64(S2)), 64)
+    g = torch.from_numpy(O.bf16_round(O.w4a16_linear(t64(a), B1.numpy(), t64(S1), 64))).to(torch.bfloat16)
+    u = torch.from_numpy(O.bf16_round(O.w4a16_linear(t64(a), B2.numpy(), t64(S2), 64))).to(torch.bfloat16)
+    theirs = t64(F.gelu(g, approximate="tanh") * u)
+    ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(theirs), 2.0 ** -126))[1] - 8)
+    # torch evaluates gelu in fp32, where tanh of a large negative argument is
+    # exactly -1 and gelu(-5.6) is 0; the float64 oracle keeps ~1e-9 there
+    assert np.all(np.abs(ours - theirs) <= ulp + 1e-7)
+    assert np.mean(ours == theirs) > 0.97
+
+
 # --------------------------------------------------------------------------- router front-end
 def _ulp_bf16(v):
     """Spacing of bf16 values at |v| (normal range)."""
