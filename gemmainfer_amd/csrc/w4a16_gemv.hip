@@ -681,6 +681,165 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Matrix-core path for 3..16 rows and the narrower N of the dense projections:
+// a workgroup of 8 waves owns 64 columns over all of K, the waves splitting K
+// into 8 ranges of KBW k blocks (KBW a multiple of the group's k blocks, so
+// no group straddles two waves).  Lane (lq, lr) loads the 16 bytes of columns
+// 4lr..4lr+3 at packed row 4kb + lq: the B operands of four 16-column
+// products, as on the lm_head path.  Every weight and scale load of a wave
+// goes out first (k blocks past K and columns past N read zeros), then the
+// token rows are staged into LDS in the matrix-core k order; the partial
+// sums of the 8 waves are added in LDS in a fixed order.  No K split across
+// workgroups, so a launch has no inter-workgroup exchange.
+constexpr int kMnWaves = 8;
+constexpr int kMnThreads = kMnWaves * kWave;
+constexpr int kMnCols = 64;
+
+template <int KBW, int KPG>
+__global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a) {
+  extern __shared__ uint4 mf_lds[];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lq = lane >> 4, lr = lane & 15;
+  const int Kp = a.K >> 3, KB = a.K >> 5;
+  const int col = blockIdx.x * kMnCols + 4 * lr;
+  const bool col_ok = col < a.N;
+  constexpr int NG = KBW / KPG;  // scale groups per wave
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
+  const int kb0 = wave * KBW;
+  uint4 w[KBW];
+#pragma unroll
+  for (int s = 0; s < KBW; ++s) {
+    const int kb = kb0 + s;
+    const bool ok = col_ok && kb < KB;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+        rb, ok ? (uint32_t)(((size_t)(4 * kb + lq) * a.N + col) * 4) : kOob, 0, kGemvNt);
+    w[s] = make_uint4(v.x, v.y, v.z, v.w);
+  }
+  uint2 sc[NG];
+#pragma unroll
+  for (int t = 0; t < NG; ++t) {
+    const int g = kb0 / KPG + t;
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(
+        rs, (col_ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob, 0, 0);
+    sc[t] = make_uint2(v.x, v.y);
+  }
+  // token rows in the matrix-core k order; row M (and rows past it) zero
+  uint4* xs = mf_lds;  // [M + 1][Kp]
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  for (int i = tid; i < (a.M + 1) * Kp; i += kMnThreads) {
+    const int n = i / Kp, r = i - n * Kp;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+        ra, n < a.M ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
+    xs[i] = moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
+  }
+  __syncthreads();
+
+  const uint32_t mq = q4_magic();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
+  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
+  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+  f32x4_t y[4] = {zf, zf, zf, zf};
+#pragma unroll
+  for (int t = 0; t < NG; ++t) {
+    f32x4_t D[4] = {zf, zf, zf, zf};
+    f32x4_t Db = zf;
+#pragma unroll
+    for (int s = 0; s < KPG; ++s) {
+      const int j = t * KPG + s;
+      const int kb = kb0 + j;
+      const uint4 A = kb < KB ? xrow[4 * kb] : z4;
+      D[0] = moe::mfma_bf16(A, moe::q4_operand(w[j].x, mq), D[0]);
+      D[1] = moe::mfma_bf16(A, moe::q4_operand(w[j].y, mq), D[1]);
+      D[2] = moe::mfma_bf16(A, moe::q4_operand(w[j].z, mq), D[2]);
+      D[3] = moe::mfma_bf16(A, moe::q4_operand(w[j].w, mq), D[3]);
+      Db = moe::mfma_bf16(A, bc, Db);
+    }
+    const float scv[4] = {bf16lo(sc[t].x), bf16hi(sc[t].x), bf16lo(sc[t].y), bf16hi(sc[t].y)};
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) y[q][jj] += scv[q] * (D[q][jj] + Db[jj]);
+  }
+  // y[q][jj]: token row 4lq + jj, column 4lr + q of the tile
+  __syncthreads();  // every wave is done with xs
+  float* red = (float*)mf_lds;  // [8 waves][16 rows][64 columns]
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj)
+    *(float4*)(red + ((size_t)wave * 16 + 4 * lq + jj) * kMnCols + 4 * lr) =
+        make_float4(y[0][jj], y[1][jj], y[2][jj], y[3][jj]);
+  __syncthreads();
+  for (int i = tid; i < a.M * kMnCols; i += kMnThreads) {
+    const int t = i / kMnCols, c = i - t * kMnCols;
+    const int oc = blockIdx.x * kMnCols + c;
+    if (oc < a.N) {
+      float v = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < kMnWaves; ++ww) v += red[((size_t)ww * 16 + t) * kMnCols + c];
+      a.C[(size_t)t * a.N + oc] = f32_to_bf16(epilogue(v, a.cap));
+    }
+  }
+}
+
+constexpr size_t kMnMaxLds = 150 * 1024;
+constexpr int kMnKbw[] = {4, 8, 12, 16, 24, 32};
+
+size_t mfma_narrow_lds(int M, int K) {
+  const size_t xs = (size_t)(M + 1) * (K / 8) * 16;
+  const size_t red = (size_t)kMnWaves * 16 * kMnCols * 4;
+  return xs > red ? xs : red;
+}
+
+bool mfma_narrow_path(int M, int K, int N, int gs) {
+  // group size 64 keeps twice the scales per wave: k blocks per wave <= 16 (no spills)
+  return M >= 3 && M <= kMfMaxM && K % 32 == 0 && K <= kMnWaves * 32 * (gs == 64 ? 16 : 32) &&
+         (gs == 64 || gs == 128) &&
+         mfma_narrow_lds(M, K) <= kMnMaxLds && (size_t)(K / 8) * N * 4 < (1ull << 32);
+}
+
+template <int KBW, int KPG>
+int launch_mfma_narrow_variant(const MfArgs& k, size_t lds, hipStream_t stream) {
+  static bool attr_set[64];
+  int dev = 0;
+  hipError_t e0 = hipGetDevice(&dev);
+  if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
+  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+    e0 = hipFuncSetAttribute((const void*)w4a16_mfma_narrow_kernel<KBW, KPG>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMnMaxLds);
+    if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
+    attr_set[dev] = true;
+  }
+  hipLaunchKernelGGL((w4a16_mfma_narrow_kernel<KBW, KPG>), dim3((unsigned)((k.N + kMnCols - 1) / kMnCols)),
+                     dim3(kMnThreads), lds, stream, k);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 matrix-core narrow launch");
+}
+
+int launch_mfma_narrow(const MfArgs& k, int gs, hipStream_t stream) {
+  const int need = (k.K / 32 + kMnWaves - 1) / kMnWaves;  // k blocks per wave
+  const size_t lds = mfma_narrow_lds(k.M, k.K);
+  int kbw = 32;
+  for (int v : kMnKbw)
+    if (v >= need) {
+      kbw = v;
+      break;
+    }
+  const int kpg = gs / 32;
+  switch (kbw * 10 + kpg) {
+#define GI_MN_CASE(KBW, KPG) \
+  case KBW * 10 + KPG:       \
+    return launch_mfma_narrow_variant<KBW, KPG>(k, lds, stream);
+    GI_MN_CASE(4, 2) GI_MN_CASE(8, 2) GI_MN_CASE(12, 2) GI_MN_CASE(16, 2)
+    GI_MN_CASE(4, 4) GI_MN_CASE(8, 4) GI_MN_CASE(12, 4) GI_MN_CASE(16, 4) GI_MN_CASE(24, 4) GI_MN_CASE(32, 4)
+#undef GI_MN_CASE
+    default:
+      return fail(GI_ERR_UNSUPPORTED, "w4a16: no matrix-core narrow variant for this shape");
+  }
+}
+
 bool mfma_path(int M, int K, int N, int gs, int G) {
   if (M < 3 || M > kMfMaxM || K % 32 || (gs != 64 && gs != 128) || N % kMfCols || N / kMfCols < 256) return false;
   // 32-bit buffer offsets, including reads past the last row of a pass
@@ -756,6 +915,7 @@ Plan make_plan(int M, int K, int N) {
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
   if (narrow_path(M, K, N)) return 0;
+  if (gs > 0 && mfma_narrow_path(M, K, N, gs)) return 0;
   // the matrix-core path needs none (scales with the full ceil(K / gs) groups)
   if (gs > 0 && mfma_path(M, K, N, gs, (K + gs - 1) / gs)) return 0;
   return make_plan(M, K, N).total;
@@ -794,6 +954,20 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "w4a16 matrix-core launch");
     return GI_OK;
+  }
+  if (mfma_narrow_path(M, K, N, gs)) {
+    MfArgs k{};
+    k.A = (const uint16_t*)A;
+    k.B = B;
+    k.S = (const uint16_t*)scales;
+    k.C = (uint16_t*)C;
+    k.M = M;
+    k.K = K;
+    k.N = N;
+    k.G = n_groups;
+    k.b_bytes = (uint32_t)((size_t)(K / 8) * N * 4);
+    k.cap = softcap;
+    return launch_mfma_narrow(k, gs, stream);
   }
   if (narrow_path(M, K, N)) {
     NarrowSeg sg{B, (const uint16_t*)scales, (uint16_t*)C, N, n_groups, 0};
