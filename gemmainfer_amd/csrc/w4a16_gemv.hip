@@ -589,6 +589,9 @@ struct MfArgs {
   int M, K, N, G;
   uint32_t b_bytes;
   float cap;
+  float* part;  // [ks, M, N] fp32 (matrix-core narrow path, ks > 1)
+  int* ctr;     // [N / 64] arrival counters (ks > 1)
+  int ks;       // K slices over gridDim.y
 };
 
 template <int KPG>
@@ -692,6 +695,14 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
 // token rows are staged into LDS in the matrix-core k order; the partial
 // sums of the 8 waves are added in LDS in a fixed order.  No K split across
 // workgroups, so a launch has no inter-workgroup exchange.
+constexpr size_t kAlign = 256;
+inline size_t round_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+// Split-K workspace: arrival counters at the front, partials from a fixed
+// offset.  Calls of different shapes share one workspace, so the counter
+// region must never be reused for partials (a counter left non-zero by
+// another call's partials breaks the last-arriver test): it is sized for
+// N <= 64 * 16384.
+constexpr size_t kCtrBytes = 16384 * sizeof(int);
 constexpr int kMnWaves = 8;
 constexpr int kMnThreads = kMnWaves * kWave;
 constexpr int kMnCols = 64;
@@ -708,7 +719,8 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a)
   constexpr uint32_t kOob = 0xFFFFFFF0u;
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
-  const int kb0 = wave * KBW;
+  const int slice = blockIdx.y;
+  const int kb0 = (slice * kMnWaves + wave) * KBW;
   uint4 w[KBW];
 #pragma unroll
   for (int s = 0; s < KBW; ++s) {
@@ -779,13 +791,32 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a)
       float v = 0.f;
 #pragma unroll
       for (int ww = 0; ww < kMnWaves; ++ww) v += red[((size_t)ww * 16 + t) * kMnCols + c];
+      if (a.ks == 1) a.C[(size_t)t * a.N + oc] = f32_to_bf16(epilogue(v, a.cap));
+      else st_coherent_f32(a.part + ((size_t)slice * a.M + t) * a.N + oc, v);
+    }
+  }
+  if (a.ks == 1) return;
+  // the last K slice to arrive for this column tile sums the partials in slice order
+  __shared__ int last;
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0) last = atomic_add_relaxed(&a.ctr[blockIdx.x], 1) == a.ks - 1;
+  __syncthreads();
+  if (!last) return;
+  for (int i = tid; i < a.M * kMnCols; i += kMnThreads) {
+    const int t = i / kMnCols, c = i - t * kMnCols;
+    const int oc = blockIdx.x * kMnCols + c;
+    if (oc < a.N) {
+      float v = 0.f;
+      for (int s2 = 0; s2 < a.ks; ++s2) v += ld_coherent_f32(a.part + ((size_t)s2 * a.M + t) * a.N + oc);
       a.C[(size_t)t * a.N + oc] = f32_to_bf16(epilogue(v, a.cap));
     }
   }
+  if (tid == 0) store_relaxed(&a.ctr[blockIdx.x], 0);
 }
 
 constexpr size_t kMnMaxLds = 150 * 1024;
-constexpr int kMnKbw[] = {4, 8, 12, 16, 24, 32};
+constexpr int kMnKbw[] = {2, 4, 8, 12, 16, 24, 32};
 
 size_t mfma_narrow_lds(int M, int K) {
   const size_t xs = (size_t)(M + 1) * (K / 8) * 16;
@@ -812,27 +843,57 @@ int launch_mfma_narrow_variant(const MfArgs& k, size_t lds, hipStream_t stream) 
     if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((w4a16_mfma_narrow_kernel<KBW, KPG>), dim3((unsigned)((k.N + kMnCols - 1) / kMnCols)),
-                     dim3(kMnThreads), lds, stream, k);
+  hipLaunchKernelGGL((w4a16_mfma_narrow_kernel<KBW, KPG>),
+                     dim3((unsigned)((k.N + kMnCols - 1) / kMnCols), (unsigned)k.ks), dim3(kMnThreads), lds,
+                     stream, k);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 matrix-core narrow launch");
 }
 
-int launch_mfma_narrow(const MfArgs& k, int gs, hipStream_t stream) {
-  const int need = (k.K / 32 + kMnWaves - 1) / kMnWaves;  // k blocks per wave
-  const size_t lds = mfma_narrow_lds(k.M, k.K);
-  int kbw = 32;
+// K split of the matrix-core narrow path: enough slices that the grid has
+// about kMnTargetWgs workgroups, each wave at least one scale group of k blocks.
+constexpr int kMnTargetWgs = 256;
+struct MnPlan {
+  int kbw, ks;
+};
+MnPlan mn_plan(int K, int N, int gs) {
+  const int KB = K / 32, kpg = gs / 32;
+  const int tiles = (N + kMnCols - 1) / kMnCols;
+  const int ks_want = (kMnTargetWgs + tiles - 1) / tiles;
+  const int per_slice = (KB + ks_want - 1) / ks_want;
+  const int need = (per_slice + kMnWaves - 1) / kMnWaves;  // k blocks per wave
+  MnPlan p{32, 1};
   for (int v : kMnKbw)
-    if (v >= need) {
-      kbw = v;
+    if (v >= need && v >= kpg) {
+      p.kbw = v;
       break;
     }
+  p.ks = (KB + kMnWaves * p.kbw - 1) / (kMnWaves * p.kbw);
+  return p;
+}
+size_t mn_workspace_bytes(int M, int K, int N, int gs) {
+  const MnPlan p = mn_plan(K, N, gs);
+  return p.ks > 1 ? round_up(kCtrBytes + (size_t)p.ks * M * N * sizeof(float)) : 0;
+}
+
+int launch_mfma_narrow(MfArgs k, int gs, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const MnPlan p = mn_plan(k.K, k.N, gs);
+  const size_t lds = mfma_narrow_lds(k.M, k.K);
+  k.ks = p.ks;
+  if (p.ks > 1) {
+    if ((size_t)((k.N + kMnCols - 1) / kMnCols) * sizeof(int) > kCtrBytes)
+      return fail(GI_ERR_UNSUPPORTED, "w4a16: N too large for the split matrix-core path");
+    if (!workspace || workspace_bytes < mn_workspace_bytes(k.M, k.K, k.N, gs) || ((uintptr_t)workspace) % kAlign)
+      return fail(GI_ERR_WORKSPACE, "w4a16: workspace missing, misaligned or smaller than gi_w4a16_workspace_bytes()");
+    k.ctr = (int*)workspace;
+    k.part = (float*)((char*)workspace + kCtrBytes);
+  }
   const int kpg = gs / 32;
-  switch (kbw * 10 + kpg) {
+  switch (p.kbw * 10 + kpg) {
 #define GI_MN_CASE(KBW, KPG) \
   case KBW * 10 + KPG:       \
     return launch_mfma_narrow_variant<KBW, KPG>(k, lds, stream);
-    GI_MN_CASE(4, 2) GI_MN_CASE(8, 2) GI_MN_CASE(12, 2) GI_MN_CASE(16, 2)
+    GI_MN_CASE(2, 2) GI_MN_CASE(4, 2) GI_MN_CASE(8, 2) GI_MN_CASE(12, 2) GI_MN_CASE(16, 2)
     GI_MN_CASE(4, 4) GI_MN_CASE(8, 4) GI_MN_CASE(12, 4) GI_MN_CASE(16, 4) GI_MN_CASE(24, 4) GI_MN_CASE(32, 4)
 #undef GI_MN_CASE
     default:
@@ -849,8 +910,6 @@ bool mfma_path(int M, int K, int N, int gs, int G) {
   return lds <= 64 * 1024;
 }
 
-constexpr size_t kAlign = 256;
-inline size_t round_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 struct Plan {
   int ks, rows_per_split, tiles, nt;
@@ -858,12 +917,6 @@ struct Plan {
 };
 
 constexpr int kGemvSteps[] = {1, 2, 3, 4, 6, 8, 12};
-// Split-K workspace: arrival counters at the front, partials from a fixed
-// offset.  Calls of different shapes share one workspace, so the counter
-// region must never be reused for partials (a counter left non-zero by
-// another call's partials breaks the last-arriver test): it is sized for
-// N <= 64 * 16384.
-constexpr size_t kCtrBytes = 16384 * sizeof(int);
 
 Plan make_plan(int M, int K, int N) {
   Plan p;
@@ -915,7 +968,7 @@ Plan make_plan(int M, int K, int N) {
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
   if (narrow_path(M, K, N)) return 0;
-  if (gs > 0 && mfma_narrow_path(M, K, N, gs)) return 0;
+  if (gs > 0 && mfma_narrow_path(M, K, N, gs)) return mn_workspace_bytes(M, K, N, gs);
   // the matrix-core path needs none (scales with the full ceil(K / gs) groups)
   if (gs > 0 && mfma_path(M, K, N, gs, (K + gs - 1) / gs)) return 0;
   return make_plan(M, K, N).total;
@@ -967,7 +1020,7 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     k.G = n_groups;
     k.b_bytes = (uint32_t)((size_t)(K / 8) * N * 4);
     k.cap = softcap;
-    return launch_mfma_narrow(k, gs, stream);
+    return launch_mfma_narrow(k, gs, workspace, workspace_bytes, stream);
   }
   if (narrow_path(M, K, N)) {
     NarrowSeg sg{B, (const uint16_t*)scales, (uint16_t*)C, N, n_groups, 0};

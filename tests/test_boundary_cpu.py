@@ -57,8 +57,8 @@ def test_workspace_queries_are_host_only(lib):
     assert lib.gi_fused_moe_workspace_bytes(1, 0, 2816, 704, 128) == 0
     assert lib.gi_w4a16_workspace_bytes(6, 2816, 262144, 128) == 0      # wide N: matrix cores, no K split
     assert lib.gi_w4a16_workspace_bytes(1, 2816, 2816, 128) == 0         # 1-2 rows: 16-column tiles, no K split
-    assert lib.gi_w4a16_workspace_bytes(4, 2816, 2816, 128) == 0         # 3-16 rows: matrix cores, no K split
-    assert lib.gi_w4a16_workspace_bytes(4, 16384, 2816, 128) > 0         # long K: split-K partials
+    assert lib.gi_w4a16_workspace_bytes(4, 2816, 2816, 128) > 0          # 3-16 rows: matrix cores, K split
+    assert lib.gi_w4a16_workspace_bytes(4, 16384, 2816, 128) > 0         # long K: VALU split-K partials
 
 
 def _moe_call(lib, **over):
