@@ -373,6 +373,7 @@ CALIB_BYTES = 256 << 20
 LINEAR_WORKLOADS = {
     "linear": (1, 2816, 2816, 128, 0.0, 300),        # configs[0] shape, 4.09 MB per weight copy
     "lm_head": (6, 2816, 262144, 128, 30.0, 4),      # configs[4], 380.6 MB per copy
+    "lm_head_m1": (1, 2816, 262144, 128, 30.0, 4),   # the same lm_head for one decoded token
 }
 
 

@@ -557,9 +557,11 @@ int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSe
 }
 
 // ---------------------------------------------------------------------------
-// Matrix-core path for a few token rows and a wide N (lm_head): with 3..16
-// rows the VALU dot products of the path above cost more than the weight
-// stream, so the products run on v_mfma_f32_16x16x32_bf16 with A = the token
+// Matrix-core path for up to 16 token rows and a wide N (lm_head): the
+// products run on v_mfma_f32_16x16x32_bf16 (with 3..16 rows the VALU dot
+// products would cost more than the weight stream; with one or two rows this
+// kernel's long register ring still streams a 380 MB lm_head faster than
+// 16384 narrow workgroups do) with A = the token
 // rows (zero rows past M) and B = the unpacked int4 words (16 + q), plus one
 // product with a constant -24 operand per k block for the offset.  A
 // workgroup owns 256 columns over all of K (wave w: 64 of them; lane
@@ -902,7 +904,9 @@ int launch_mfma_narrow(MfArgs k, int gs, void* workspace, size_t workspace_bytes
 }
 
 bool mfma_path(int M, int K, int N, int gs, int G) {
-  if (M < 3 || M > kMfMaxM || K % 32 || (gs != 64 && gs != 128) || N % kMfCols || N / kMfCols < 256) return false;
+  // wide N (lm_head): the matrix cores stream best from one row up (rows past
+  // M are zero operand rows)
+  if (M < 1 || M > kMfMaxM || K % 32 || (gs != 64 && gs != 128) || N % kMfCols || N / kMfCols < 256) return false;
   // 32-bit buffer offsets, including reads past the last row of a pass
   const long long kb_pad = (long long)(K / 32 + kMfPass - 1) / kMfPass * kMfPass;
   if (kb_pad * 4 * N * 4 >= (1LL << 32)) return false;

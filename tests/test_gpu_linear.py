@@ -61,16 +61,20 @@ def test_lm_head_softcap_column_subset():
     assert float(C.float().abs().max()) <= 30.0
 
 
-@pytest.mark.parametrize("m,gs,floor_groups,cap", [
-    (3, 128, False, None),   # fewest rows on the matrix-core path
-    (6, 64, False, 30.0),    # two k blocks per group, softcap
-    (16, 128, False, None),  # a full 16-row operand
-    (7, 128, True, None),    # floor-size scales: rows past the last group dropped
+@pytest.mark.parametrize("m,gs,floor_groups,cap,n", [
+    (3, 128, False, None, 65536),   # the wide-N matrix-core path
+    (6, 64, False, 30.0, 65536),    # two k blocks per group, softcap
+    (16, 128, False, None, 65536),  # a full 16-row operand
+    (7, 128, True, None, 65536),    # floor-size scales: rows past the last group dropped
+    (1, 128, False, 30.0, 65536),   # one row (zero operand rows) on the wide-N matrix-core path
+    (1, 128, False, 30.0, 16384),   # one row: the 16-column narrow path with the softcap epilogue
+    (2, 64, True, None, 16384),     # two rows, floor-size scales on the narrow path
 ])
-def test_w4a16_matrix_core_path(m, gs, floor_groups, cap):
-    """3 <= M <= 16 with N >= 65536 runs the matrix-core kernel: checked against
-    the float64 oracle on 1024 random columns of every 256-column tile shape."""
-    k, n = 2816 if not floor_groups else 2880, 65536
+def test_w4a16_matrix_core_path(m, gs, floor_groups, cap, n):
+    """N >= 65536 runs the wide matrix-core kernel (any M <= 16); 1-2 rows at
+    narrower N the 16-column narrow kernel: checked against the float64 oracle
+    on 1024 random columns."""
+    k = 2816 if not floor_groups else 2880
     g = torch.Generator(device=DEV)
     g.manual_seed(m * 7 + gs)
     B = torch.randint(-(2 ** 31), 2 ** 31, (k // 8, n), generator=g, device=DEV,
