@@ -553,7 +553,9 @@ class FusedDenseRunner:
         self.act = torch.empty(m, 2112, dtype=torch.bfloat16, device=device)
         self.y = torch.empty(m, H, dtype=torch.bfloat16, device=device)
         nb = max([self.lib.gi_w4a16_workspace_bytes(m, shp[x][0], shp[x][1], DENSE_GS) for x in SLIDING] +
-                 [self.lib.gi_w4a16_gated_mlp_workspace_bytes(m, H, 2112, DENSE_GS)])
+                 [self.lib.gi_w4a16_gated_mlp_workspace_bytes(m, H, 2112, DENSE_GS),
+                  self.lib.gi_w4a16_linear_multi_workspace_bytes(3, (ctypes.c_int * 3)(4096, 2048, 2048), m, H,
+                                                                 DENSE_GS)])
         self.ws = torch.zeros(max(nb, 256), dtype=torch.uint8, device=device)
         torch.cuda.synchronize()
 

@@ -60,6 +60,7 @@ SIGNATURES = {
                                 c_void_p]),
     "gi_w4a16_linear_multi": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                       c_void_p, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
+    "gi_w4a16_linear_multi_workspace_bytes": (c_size_t, [c_int, c_void_p, c_int, c_int, c_int]),
     "gi_w4a16_gated_mlp_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "gi_w4a16_gated_mlp": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
                                    c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),

@@ -223,6 +223,10 @@ int gi_w4a16_linear_multi(const void* A, int a_dtype, int n_proj, const int32_t*
                                 workspace_bytes, as_stream(stream));
 }
 
+size_t gi_w4a16_linear_multi_workspace_bytes(int n_proj, const int* N, int M, int K, int group_size) {
+  return gi::w4a16_multi_workspace_bytes(n_proj, N, M, K, group_size);
+}
+
 size_t gi_w4a16_gated_mlp_workspace_bytes(int M, int K, int N, int group_size) {
   return gi::w4a16_gated_workspace_bytes(M, K, N, group_size);
 }

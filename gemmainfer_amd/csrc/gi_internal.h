@@ -76,6 +76,7 @@ int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void
                        void* const* C, const int* N, int M, int K, int gs, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
 size_t w4a16_gated_workspace_bytes(int M, int K, int N, int gs);
+size_t w4a16_multi_workspace_bytes(int n, const int* N, int M, int K, int gs);
 int launch_w4a16_gated(const void* A, const int32_t* gB, const void* gS, int gG, const int32_t* uB, const void* uS,
                        int uG, void* out, int M, int K, int N, int gs, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);

@@ -709,56 +709,55 @@ constexpr int kMnWaves = 8;
 constexpr int kMnThreads = kMnWaves * kWave;
 constexpr int kMnCols = 64;
 
+// Segments as on the VALU narrow path: several projections of the same rows
+// in one grid (segment s owns 64-column tiles [tile0, tile0 + ceil(N/64))),
+// or GATED: the gate and up projections of a gated MLP, both computed by
+// every workgroup for its 64 columns, written as
+// bf16(bf16(gelu_tanh(bf16(gate))) * bf16(up)).  With a K split the fp32
+// partials are indexed by the grid's global column (tile * 64 + c).
+struct MnArgs {
+  const uint16_t* A;  // [M, K]
+  int M, K, ks, ntot;  // ntot = tiles * 64
+  float cap;
+  float* part;  // [ks][GATED ? 2 : 1][M][ntot] (ks > 1)
+  int* ctr;     // [tiles] (ks > 1)
+  NarrowSeg seg[kMaxSegs];
+};
+
 template <int KBW, int KPG>
-__global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a) {
-  extern __shared__ uint4 mf_lds[];
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int lq = lane >> 4, lr = lane & 15;
-  const int Kp = a.K >> 3, KB = a.K >> 5;
-  const int col = blockIdx.x * kMnCols + 4 * lr;
-  const bool col_ok = col < a.N;
-  constexpr int NG = KBW / KPG;  // scale groups per wave
+__device__ __forceinline__ void mn_issue(const NarrowSeg& sg, int Kp, int KB, int col, int kb0, int lq,
+                                         uint4 (&w)[KBW], uint2 (&sc)[KBW / KPG]) {
   constexpr uint32_t kOob = 0xFFFFFFF0u;
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
-  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
-  const int slice = blockIdx.y;
-  const int kb0 = (slice * kMnWaves + wave) * KBW;
-  uint4 w[KBW];
+  const bool col_ok = col < sg.N;
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(sg.B, (uint32_t)((size_t)Kp * sg.N * 4));
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sg.S, (uint32_t)((size_t)sg.G * sg.N * 2));
 #pragma unroll
   for (int s = 0; s < KBW; ++s) {
     const int kb = kb0 + s;
     const bool ok = col_ok && kb < KB;
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-        rb, ok ? (uint32_t)(((size_t)(4 * kb + lq) * a.N + col) * 4) : kOob, 0, kGemvNt);
+        rb, ok ? (uint32_t)(((size_t)(4 * kb + lq) * sg.N + col) * 4) : kOob, 0, kGemvNt);
     w[s] = make_uint4(v.x, v.y, v.z, v.w);
   }
-  uint2 sc[NG];
 #pragma unroll
-  for (int t = 0; t < NG; ++t) {
+  for (int t = 0; t < KBW / KPG; ++t) {
     const int g = kb0 / KPG + t;
     const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(
-        rs, (col_ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob, 0, 0);
+        rs, (col_ok && g < sg.G) ? (uint32_t)((g * sg.N + col) * 2) : kOob, 0, 0);
     sc[t] = make_uint2(v.x, v.y);
   }
-  // token rows in the matrix-core k order; row M (and rows past it) zero
-  uint4* xs = mf_lds;  // [M + 1][Kp]
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
-  for (int i = tid; i < (a.M + 1) * Kp; i += kMnThreads) {
-    const int n = i / Kp, r = i - n * Kp;
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-        ra, n < a.M ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
-    xs[i] = moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
-  }
-  __syncthreads();
+}
 
-  const uint32_t mq = q4_magic();
+template <int KBW, int KPG>
+__device__ __forceinline__ void mn_products(const uint4 (&w)[KBW], const uint2 (&sc)[KBW / KPG], const uint4* xrow,
+                                            int kb0, int KB, uint32_t mq, f32x4_t (&y)[4]) {
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
-  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
   const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-  f32x4_t y[4] = {zf, zf, zf, zf};
 #pragma unroll
-  for (int t = 0; t < NG; ++t) {
+  for (int q = 0; q < 4; ++q) y[q] = zf;
+#pragma unroll
+  for (int t = 0; t < KBW / KPG; ++t) {
     f32x4_t D[4] = {zf, zf, zf, zf};
     f32x4_t Db = zf;
 #pragma unroll
@@ -778,23 +777,82 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) y[q][jj] += scv[q] * (D[q][jj] + Db[jj]);
   }
+}
+
+__device__ __forceinline__ float mn_out(float y, float u, float cap, bool gated) {
+  // activations.py:26-28 on bf16 tensors for the gated form
+  return gated ? round_to_bf16(gelu_tanh(round_to_bf16(y))) * round_to_bf16(u) : epilogue(y, cap);
+}
+
+template <int KBW, int KPG, bool GATED>
+__global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MnArgs a) {
+  extern __shared__ uint4 mf_lds[];
+  constexpr int kOut = GATED ? 2 : 1;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int lq = lane >> 4, lr = lane & 15;
+  const int Kp = a.K >> 3, KB = a.K >> 5;
+  // the workgroup's segment, by uniform selects (no dynamic kernarg index)
+  NarrowSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i)
+    if (!GATED && (int)blockIdx.x >= a.seg[i].tile0) sg = a.seg[i];
+  const int c0 = ((int)blockIdx.x - sg.tile0) * kMnCols;
+  const int col = c0 + 4 * lr;
+  const int slice = blockIdx.y;
+  const int kb0 = (slice * kMnWaves + wave) * KBW;
+  uint4 w0[KBW];
+  uint2 s0[KBW / KPG];
+  mn_issue<KBW, KPG>(sg, Kp, KB, col, kb0, lq, w0, s0);
+  uint4 w1[GATED ? KBW : 1];
+  uint2 s1[GATED ? KBW / KPG : 1];
+  if constexpr (GATED) mn_issue<KBW, KPG>(a.seg[1], Kp, KB, col, kb0, lq, w1, s1);
+  // token rows in the matrix-core k order; row M (and rows past it) zero
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  uint4* xs = mf_lds;  // [M + 1][Kp]
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  for (int i = tid; i < (a.M + 1) * Kp; i += kMnThreads) {
+    const int n = i / Kp, r = i - n * Kp;
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+        ra, n < a.M ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
+    xs[i] = moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
+  }
+  __syncthreads();
+
+  const uint32_t mq = q4_magic();
+  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
+  f32x4_t y0[4], y1[4];
+  mn_products<KBW, KPG>(w0, s0, xrow, kb0, KB, mq, y0);
+  if constexpr (GATED) mn_products<KBW, KPG>(w1, s1, xrow, kb0, KB, mq, y1);
   // y[q][jj]: token row 4lq + jj, column 4lr + q of the tile
   __syncthreads();  // every wave is done with xs
-  float* red = (float*)mf_lds;  // [8 waves][16 rows][64 columns]
+  float* red = (float*)mf_lds;  // [kOut][8 waves][16 rows][64 columns]
 #pragma unroll
-  for (int jj = 0; jj < 4; ++jj)
+  for (int jj = 0; jj < 4; ++jj) {
     *(float4*)(red + ((size_t)wave * 16 + 4 * lq + jj) * kMnCols + 4 * lr) =
-        make_float4(y[0][jj], y[1][jj], y[2][jj], y[3][jj]);
+        make_float4(y0[0][jj], y0[1][jj], y0[2][jj], y0[3][jj]);
+    if constexpr (GATED)
+      *(float4*)(red + ((size_t)(kMnWaves + wave) * 16 + 4 * lq + jj) * kMnCols + 4 * lr) =
+          make_float4(y1[0][jj], y1[1][jj], y1[2][jj], y1[3][jj]);
+  }
   __syncthreads();
+  const int gcol0 = (int)blockIdx.x * kMnCols;
   for (int i = tid; i < a.M * kMnCols; i += kMnThreads) {
     const int t = i / kMnCols, c = i - t * kMnCols;
-    const int oc = blockIdx.x * kMnCols + c;
-    if (oc < a.N) {
-      float v = 0.f;
+    const int oc = c0 + c;
+    if (oc < sg.N) {
+      float v[kOut];
 #pragma unroll
-      for (int ww = 0; ww < kMnWaves; ++ww) v += red[((size_t)ww * 16 + t) * kMnCols + c];
-      if (a.ks == 1) a.C[(size_t)t * a.N + oc] = f32_to_bf16(epilogue(v, a.cap));
-      else st_coherent_f32(a.part + ((size_t)slice * a.M + t) * a.N + oc, v);
+      for (int o = 0; o < kOut; ++o) {
+        v[o] = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kMnWaves; ++ww) v[o] += red[((size_t)(o * kMnWaves + ww) * 16 + t) * kMnCols + c];
+      }
+      if (a.ks == 1)
+        sg.C[(size_t)t * sg.N + oc] = f32_to_bf16(mn_out(v[0], v[kOut - 1], a.cap, GATED));
+      else
+#pragma unroll
+        for (int o = 0; o < kOut; ++o)
+          st_coherent_f32(a.part + (((size_t)slice * kOut + o) * a.M + t) * a.ntot + gcol0 + c, v[o]);
     }
   }
   if (a.ks == 1) return;
@@ -807,11 +865,16 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a)
   if (!last) return;
   for (int i = tid; i < a.M * kMnCols; i += kMnThreads) {
     const int t = i / kMnCols, c = i - t * kMnCols;
-    const int oc = blockIdx.x * kMnCols + c;
-    if (oc < a.N) {
-      float v = 0.f;
-      for (int s2 = 0; s2 < a.ks; ++s2) v += ld_coherent_f32(a.part + ((size_t)s2 * a.M + t) * a.N + oc);
-      a.C[(size_t)t * a.N + oc] = f32_to_bf16(epilogue(v, a.cap));
+    const int oc = c0 + c;
+    if (oc < sg.N) {
+      float v[kOut];
+#pragma unroll
+      for (int o = 0; o < kOut; ++o) {
+        v[o] = 0.f;
+        for (int s2 = 0; s2 < a.ks; ++s2)
+          v[o] += ld_coherent_f32(a.part + (((size_t)s2 * kOut + o) * a.M + t) * a.ntot + gcol0 + c);
+      }
+      sg.C[(size_t)t * sg.N + oc] = f32_to_bf16(mn_out(v[0], v[kOut - 1], a.cap, GATED));
     }
   }
   if (tid == 0) store_relaxed(&a.ctr[blockIdx.x], 0);
@@ -820,34 +883,39 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MfArgs a)
 constexpr size_t kMnMaxLds = 150 * 1024;
 constexpr int kMnKbw[] = {2, 4, 8, 12, 16, 24, 32};
 
-size_t mfma_narrow_lds(int M, int K) {
+size_t mfma_narrow_lds(int M, int K, bool gated) {
   const size_t xs = (size_t)(M + 1) * (K / 8) * 16;
-  const size_t red = (size_t)kMnWaves * 16 * kMnCols * 4;
+  const size_t red = (size_t)(gated ? 2 : 1) * kMnWaves * 16 * kMnCols * 4;
   return xs > red ? xs : red;
 }
 
-bool mfma_narrow_path(int M, int K, int N, int gs) {
-  // group size 64 keeps twice the scales per wave: k blocks per wave <= 16 (no spills)
-  return M >= 3 && M <= kMfMaxM && K % 32 == 0 && K <= kMnWaves * 32 * (gs == 64 ? 16 : 32) &&
-         (gs == 64 || gs == 128) &&
-         mfma_narrow_lds(M, K) <= kMnMaxLds && (size_t)(K / 8) * N * 4 < (1ull << 32);
+// k blocks per wave at most: twice the weights (gated) or twice the scales
+// (group size 64) per wave would otherwise spill
+int mn_max_kbw(int gs, bool gated) { return gated ? 8 : (gs == 64 ? 16 : 32); }
+
+bool mfma_narrow_ok(int M, int K, int gs, bool gated) {
+  return M >= 3 && M <= kMfMaxM && K % 32 == 0 && (gs == 64 || gs == 128) &&
+         K <= kMnWaves * 32 * mn_max_kbw(gs, gated) && mfma_narrow_lds(M, K, gated) <= kMnMaxLds;
 }
 
-template <int KBW, int KPG>
-int launch_mfma_narrow_variant(const MfArgs& k, size_t lds, hipStream_t stream) {
+bool mfma_narrow_path(int M, int K, int N, int gs) {
+  return mfma_narrow_ok(M, K, gs, false) && (size_t)(K / 8) * N * 4 < (1ull << 32);
+}
+
+template <int KBW, int KPG, bool G>
+int launch_mfma_narrow_variant(const MnArgs& k, int tiles, size_t lds, hipStream_t stream) {
   static bool attr_set[64];
   int dev = 0;
   hipError_t e0 = hipGetDevice(&dev);
   if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
   if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    e0 = hipFuncSetAttribute((const void*)w4a16_mfma_narrow_kernel<KBW, KPG>,
+    e0 = hipFuncSetAttribute((const void*)w4a16_mfma_narrow_kernel<KBW, KPG, G>,
                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMnMaxLds);
     if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL((w4a16_mfma_narrow_kernel<KBW, KPG>),
-                     dim3((unsigned)((k.N + kMnCols - 1) / kMnCols), (unsigned)k.ks), dim3(kMnThreads), lds,
-                     stream, k);
+  hipLaunchKernelGGL((w4a16_mfma_narrow_kernel<KBW, KPG, G>), dim3((unsigned)tiles, (unsigned)k.ks),
+                     dim3(kMnThreads), lds, stream, k);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 matrix-core narrow launch");
 }
@@ -858,45 +926,70 @@ constexpr int kMnTargetWgs = 256;
 struct MnPlan {
   int kbw, ks;
 };
-MnPlan mn_plan(int K, int N, int gs) {
+MnPlan mn_plan(int K, int tiles, int gs, bool gated) {
   const int KB = K / 32, kpg = gs / 32;
-  const int tiles = (N + kMnCols - 1) / kMnCols;
   const int ks_want = (kMnTargetWgs + tiles - 1) / tiles;
   const int per_slice = (KB + ks_want - 1) / ks_want;
   const int need = (per_slice + kMnWaves - 1) / kMnWaves;  // k blocks per wave
-  MnPlan p{32, 1};
+  MnPlan p{mn_max_kbw(gs, gated), 1};
   for (int v : kMnKbw)
-    if (v >= need && v >= kpg) {
+    if (v >= need && v >= kpg && v <= mn_max_kbw(gs, gated)) {
       p.kbw = v;
       break;
     }
   p.ks = (KB + kMnWaves * p.kbw - 1) / (kMnWaves * p.kbw);
   return p;
 }
-size_t mn_workspace_bytes(int M, int K, int N, int gs) {
-  const MnPlan p = mn_plan(K, N, gs);
-  return p.ks > 1 ? round_up(kCtrBytes + (size_t)p.ks * M * N * sizeof(float)) : 0;
+int mn_tiles(const int* N, int n) {
+  int t = 0;
+  for (int i = 0; i < n; ++i) t += (N[i] + kMnCols - 1) / kMnCols;
+  return t;
+}
+size_t mn_workspace_bytes(int M, int K, int tiles, int gs, bool gated) {
+  const MnPlan p = mn_plan(K, tiles, gs, gated);
+  return p.ks > 1 ? round_up(kCtrBytes + (size_t)p.ks * (gated ? 2 : 1) * M * tiles * kMnCols * sizeof(float)) : 0;
 }
 
-int launch_mfma_narrow(MfArgs k, int gs, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  const MnPlan p = mn_plan(k.K, k.N, gs);
-  const size_t lds = mfma_narrow_lds(k.M, k.K);
+// segs: the projections (for gated: gate then up, same N); caller checked
+// mfma_narrow_ok and the 32-bit offsets of every segment.
+int launch_mfma_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSeg* segs, int nseg, bool gated,
+                       void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  MnArgs k{};
+  k.A = (const uint16_t*)A;
+  k.M = M;
+  k.K = K;
+  k.cap = cap;
+  int tiles = 0;
+  for (int i = 0; i < nseg; ++i) {
+    k.seg[i] = segs[i];
+    k.seg[i].tile0 = gated ? 0 : tiles;
+    if (!gated) tiles += (segs[i].N + kMnCols - 1) / kMnCols;
+  }
+  if (gated) tiles = (segs[0].N + kMnCols - 1) / kMnCols;
+  for (int i = nseg; i < kMaxSegs; ++i) k.seg[i].tile0 = 0x7fffffff;
+  k.ntot = tiles * kMnCols;
+  const MnPlan p = mn_plan(K, tiles, gs, gated);
   k.ks = p.ks;
   if (p.ks > 1) {
-    if ((size_t)((k.N + kMnCols - 1) / kMnCols) * sizeof(int) > kCtrBytes)
+    if ((size_t)tiles * sizeof(int) > kCtrBytes)
       return fail(GI_ERR_UNSUPPORTED, "w4a16: N too large for the split matrix-core path");
-    if (!workspace || workspace_bytes < mn_workspace_bytes(k.M, k.K, k.N, gs) || ((uintptr_t)workspace) % kAlign)
-      return fail(GI_ERR_WORKSPACE, "w4a16: workspace missing, misaligned or smaller than gi_w4a16_workspace_bytes()");
+    if (!workspace || workspace_bytes < mn_workspace_bytes(M, K, tiles, gs, gated) ||
+        ((uintptr_t)workspace) % kAlign)
+      return fail(GI_ERR_WORKSPACE, "w4a16: workspace missing, misaligned or smaller than the workspace query");
     k.ctr = (int*)workspace;
     k.part = (float*)((char*)workspace + kCtrBytes);
   }
+  const size_t lds = mfma_narrow_lds(M, K, gated);
   const int kpg = gs / 32;
-  switch (p.kbw * 10 + kpg) {
-#define GI_MN_CASE(KBW, KPG) \
-  case KBW * 10 + KPG:       \
-    return launch_mfma_narrow_variant<KBW, KPG>(k, lds, stream);
-    GI_MN_CASE(2, 2) GI_MN_CASE(4, 2) GI_MN_CASE(8, 2) GI_MN_CASE(12, 2) GI_MN_CASE(16, 2)
-    GI_MN_CASE(4, 4) GI_MN_CASE(8, 4) GI_MN_CASE(12, 4) GI_MN_CASE(16, 4) GI_MN_CASE(24, 4) GI_MN_CASE(32, 4)
+  switch ((gated ? 10000 : 0) + p.kbw * 10 + kpg) {
+#define GI_MN_CASE(G, KBW, KPG)                      \
+  case (G ? 10000 : 0) + KBW * 10 + KPG:            \
+    return launch_mfma_narrow_variant<KBW, KPG, G>(k, tiles, lds, stream);
+    GI_MN_CASE(false, 2, 2) GI_MN_CASE(false, 4, 2) GI_MN_CASE(false, 8, 2) GI_MN_CASE(false, 12, 2)
+    GI_MN_CASE(false, 16, 2) GI_MN_CASE(false, 4, 4) GI_MN_CASE(false, 8, 4) GI_MN_CASE(false, 12, 4)
+    GI_MN_CASE(false, 16, 4) GI_MN_CASE(false, 24, 4) GI_MN_CASE(false, 32, 4)
+    GI_MN_CASE(true, 2, 2) GI_MN_CASE(true, 4, 2) GI_MN_CASE(true, 8, 2) GI_MN_CASE(true, 4, 4)
+    GI_MN_CASE(true, 8, 4)
 #undef GI_MN_CASE
     default:
       return fail(GI_ERR_UNSUPPORTED, "w4a16: no matrix-core narrow variant for this shape");
@@ -972,7 +1065,8 @@ Plan make_plan(int M, int K, int N) {
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
   if (narrow_path(M, K, N)) return 0;
-  if (gs > 0 && mfma_narrow_path(M, K, N, gs)) return mn_workspace_bytes(M, K, N, gs);
+  if (gs > 0 && mfma_narrow_path(M, K, N, gs))
+    return mn_workspace_bytes(M, K, (N + kMnCols - 1) / kMnCols, gs, false);
   // the matrix-core path needs none (scales with the full ceil(K / gs) groups)
   if (gs > 0 && mfma_path(M, K, N, gs, (K + gs - 1) / gs)) return 0;
   return make_plan(M, K, N).total;
@@ -1013,18 +1107,8 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     return GI_OK;
   }
   if (mfma_narrow_path(M, K, N, gs)) {
-    MfArgs k{};
-    k.A = (const uint16_t*)A;
-    k.B = B;
-    k.S = (const uint16_t*)scales;
-    k.C = (uint16_t*)C;
-    k.M = M;
-    k.K = K;
-    k.N = N;
-    k.G = n_groups;
-    k.b_bytes = (uint32_t)((size_t)(K / 8) * N * 4);
-    k.cap = softcap;
-    return launch_mfma_narrow(k, gs, workspace, workspace_bytes, stream);
+    const NarrowSeg sg{B, (const uint16_t*)scales, (uint16_t*)C, N, n_groups, 0};
+    return launch_mfma_narrow(A, M, K, gs, softcap, &sg, 1, false, workspace, workspace_bytes, stream);
   }
   if (narrow_path(M, K, N)) {
     NarrowSeg sg{B, (const uint16_t*)scales, (uint16_t*)C, N, n_groups, 0};
@@ -1122,6 +1206,20 @@ __global__ __launch_bounds__(256) void gelu_mul_kernel(const uint16_t* g, const 
 
 size_t gated_tmp_off(int M, int K, int N) { return round_up(make_plan(M, K, N).total); }
 
+bool mfma_multi(int M, int K, const int* N, int n, int gs) {
+  if (!mfma_narrow_ok(M, K, gs, false)) return false;
+  for (int i = 0; i < n; ++i)
+    if ((size_t)(K / 8) * N[i] * 4 >= (1ull << 32)) return false;
+  return true;
+}
+
+bool gated_narrow(int M, int K, int N) {
+  return M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32);
+}
+bool gated_mfma(int M, int K, int N, int gs) {
+  return mfma_narrow_ok(M, K, gs, true) && (size_t)(K / 8) * N * 4 < (1ull << 32);
+}
+
 }  // namespace
 
 int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void* const* scales, const int* n_groups,
@@ -1134,11 +1232,11 @@ int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void
     if (st != GI_OK) return st;
   }
   if (M == 0) return GI_OK;
-  if (narrow_multi(M, K, N, n)) {
-    NarrowSeg sg[kMaxSegs];
-    for (int i = 0; i < n; ++i) sg[i] = NarrowSeg{B[i], (const uint16_t*)scales[i], (uint16_t*)C[i], N[i], n_groups[i], 0};
-    return launch_narrow(A, M, K, gs, 0.f, sg, n, false, stream);
-  }
+  NarrowSeg sg[kMaxSegs];
+  for (int i = 0; i < n; ++i) sg[i] = NarrowSeg{B[i], (const uint16_t*)scales[i], (uint16_t*)C[i], N[i], n_groups[i], 0};
+  if (narrow_multi(M, K, N, n)) return launch_narrow(A, M, K, gs, 0.f, sg, n, false, stream);
+  if (mfma_multi(M, K, N, n, gs))
+    return launch_mfma_narrow(A, M, K, gs, 0.f, sg, n, false, workspace, workspace_bytes, stream);
   for (int i = 0; i < n; ++i) {
     const int st = launch_w4a16(A, B[i], scales[i], n_groups[i], C[i], M, K, N[i], gs, 0.f, workspace,
                                 workspace_bytes, stream);
@@ -1147,10 +1245,22 @@ int launch_w4a16_multi(const void* A, int n, const int32_t* const* B, const void
   return GI_OK;
 }
 
+size_t w4a16_multi_workspace_bytes(int n, const int* N, int M, int K, int gs) {
+  if (n <= 0 || n > kMaxSegs || !N || M <= 0 || K <= 0) return 0;
+  if (narrow_multi(M, K, N, n)) return 0;
+  if (gs > 0 && mfma_multi(M, K, N, n, gs)) return mn_workspace_bytes(M, K, mn_tiles(N, n), gs, false);
+  size_t b = 0;
+  for (int i = 0; i < n; ++i) {
+    const size_t x = w4a16_workspace_bytes(M, K, N[i], gs);
+    if (x > b) b = x;
+  }
+  return b;
+}
+
 size_t w4a16_gated_workspace_bytes(int M, int K, int N, int gs) {
   if (M <= 0 || K <= 0 || N <= 0) return 0;
-  if (M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32)) return 0;
-  (void)gs;
+  if (gated_narrow(M, K, N)) return 0;
+  if (gs > 0 && gated_mfma(M, K, N, gs)) return mn_workspace_bytes(M, K, (N + kMnCols - 1) / kMnCols, gs, true);
   return gated_tmp_off(M, K, N) + 2 * round_up((size_t)M * N * 2);
 }
 
@@ -1162,11 +1272,11 @@ int launch_w4a16_gated(const void* A, const int32_t* gB, const void* gS, int gG,
   st = check_linear(A, uB, uS, uG, out, M, K, N, gs, "w4a16_gated_mlp");
   if (st != GI_OK) return st;
   if (M == 0) return GI_OK;
-  if (M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32)) {
-    const NarrowSeg sg[2] = {NarrowSeg{gB, (const uint16_t*)gS, (uint16_t*)out, N, gG, 0},
-                             NarrowSeg{uB, (const uint16_t*)uS, nullptr, N, uG, 0}};
-    return launch_narrow(A, M, K, gs, 0.f, sg, 2, true, stream);
-  }
+  const NarrowSeg sg[2] = {NarrowSeg{gB, (const uint16_t*)gS, (uint16_t*)out, N, gG, 0},
+                           NarrowSeg{uB, (const uint16_t*)uS, nullptr, N, uG, 0}};
+  if (gated_narrow(M, K, N)) return launch_narrow(A, M, K, gs, 0.f, sg, 2, true, stream);
+  if (gated_mfma(M, K, N, gs))
+    return launch_mfma_narrow(A, M, K, gs, 0.f, sg, 2, true, workspace, workspace_bytes, stream);
   const size_t need = w4a16_gated_workspace_bytes(M, K, N, gs);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "w4a16_gated_mlp: workspace missing, misaligned or smaller than "

@@ -413,9 +413,10 @@ def w4a16_linear_multi(A, weights, group_size):
     if m == 0:
         return outs
     lib = L.load()
-    nbytes = max(lib.gi_w4a16_workspace_bytes(m, k, B.shape[1], group_size) for B, _ in weights)
-    ws = _WS.get("w4a16", dev, nbytes) if nbytes else None
     n = len(weights)
+    nbytes = lib.gi_w4a16_linear_multi_workspace_bytes(n, (ctypes.c_int * n)(*[B.shape[1] for B, _ in weights]),
+                                                       m, k, int(group_size))
+    ws = _WS.get("w4a16", dev, nbytes) if nbytes else None
     arr = lambda vals: (ctypes.c_void_p * n)(*[v.data_ptr() for v in vals])  # noqa: E731
     L.check(lib.gi_w4a16_linear_multi(
         _ptr(A.contiguous()), L.DTYPE_BF16, n, arr([B for B, _ in weights]), arr([S for _, S in weights]),

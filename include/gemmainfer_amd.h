@@ -192,10 +192,13 @@ int gi_w4a16_linear(const void* A, int a_dtype,
  * Several W4A16 projections of the same rows A[M, K] in one launch: the q, k
  * and v projections of attention.py:115-122 (three marlin_w4a16 calls on one
  * input there).  C[i][M, N[i]] = A @ dequant(B_packed[i], scales[i]) for
- * i < n_proj <= 4.  One launch when M <= 2 and K <= 8192 (16-column tiles
- * of every projection in one grid); otherwise one gi_w4a16_linear per
- * projection, in order, sharing the workspace (size it with the largest
- * gi_w4a16_workspace_bytes of the projections).  Arrays are host memory.   */
+ * i < n_proj <= 4.  One launch for 1-2 rows (16-column tiles of every
+ * projection in one grid) and for 3-16 rows on the matrix-core path (64-column
+ * tiles); otherwise one gi_w4a16_linear per projection, in order.  Size the
+ * workspace with gi_w4a16_linear_multi_workspace_bytes.  Arrays are host
+ * memory.                                                                    */
+size_t gi_w4a16_linear_multi_workspace_bytes(int n_proj, const int* N, int M, int K,
+                                             int group_size);
 int gi_w4a16_linear_multi(const void* A, int a_dtype, int n_proj,
                           const int32_t* const* B_packed, const void* const* scales,
                           const int* n_groups, void* const* C, const int* N,
@@ -204,11 +207,11 @@ int gi_w4a16_linear_multi(const void* A, int a_dtype, int n_proj,
 
 /* The gated MLP's first half (activations.py:26-28):
  *   out[M, N] = bf16( bf16(gelu_tanh(bf16(A @ Wg))) * bf16(A @ Wu) )
- * with the bf16 roundings of the torch statements.  M <= 2, K <= 8192: one
- * launch (both projections per 16-column tile, the gelu and product in the
- * epilogue, no workspace).  Otherwise two linears into the workspace and an
- * elementwise launch; size the workspace with
- * gi_w4a16_gated_mlp_workspace_bytes (0 for the one-launch shapes).       */
+ * with the bf16 roundings of the torch statements.  One launch for 1-2 rows
+ * (16-column tiles) and for 3-16 rows on the matrix-core path (both
+ * projections per 64-column tile, the gelu and product in the epilogue).
+ * Otherwise two linears into the workspace and an elementwise launch; size
+ * the workspace with gi_w4a16_gated_mlp_workspace_bytes.                   */
 size_t gi_w4a16_gated_mlp_workspace_bytes(int M, int K, int N, int group_size);
 int gi_w4a16_gated_mlp(const void* A, int a_dtype,
                        const int32_t* gate_packed, const void* gate_scales, int gate_groups,

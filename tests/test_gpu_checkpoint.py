@@ -146,8 +146,10 @@ def test_dense_callers_gemma_gs64(name, m):
 
 @pytest.mark.parametrize("m", [1, 2, 7])
 def test_linear_multi_qkv(m):
-    """q, k, v of one input in one call: equal to three separate linears, and to
-    the oracle on sampled columns."""
+    """q, k, v of one input in one call: bit-identical to three separate linears
+    at 1-2 rows (same kernel, same sums), within tolerance of the oracle on
+    sampled columns at every M (3+ rows split K over the whole grid, so the
+    partial sums differ from separate calls)."""
     print(f"qkv m={m}", flush=True)
     shapes = [(2816, 4096), (2816, 2048), (2816, 2048)]
     W = [synth.linear_weights(k, n, 64, seed=50 + i) for i, (k, n) in enumerate(shapes)]
@@ -155,8 +157,9 @@ def test_linear_multi_qkv(m):
     A = synth.activations(m, 2816, seed=60 + m).to(DEV)
     outs = ops.w4a16_linear_multi(A, Wd, 64)
     for i, ((B, S), (Bd, Sd)) in enumerate(zip(W, Wd)):
-        sep = ops.w4a16_linear(A, Bd, Sd, 64)
-        assert torch.equal(outs[i], sep), f"projection {i}"
+        if m <= 2:
+            sep = ops.w4a16_linear(A, Bd, Sd, 64)
+            assert torch.equal(outs[i], sep), f"projection {i}"
         cols = torch.arange(0, B.shape[1], 17)
         ref = O.w4a16_linear(np64(A), B[:, cols].numpy(), np64(S[:, cols]), 64)
         assert_bf16_close(outs[i][:, cols.to(DEV)], ref, f"qkv[{i}] m={m}")
