@@ -806,20 +806,24 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MnArgs a)
   uint4 w1[GATED ? KBW : 1];
   uint2 s1[GATED ? KBW / KPG : 1];
   if constexpr (GATED) mn_issue<KBW, KPG>(a.seg[1], Kp, KB, col, kb0, lq, w1, s1);
-  // token rows in the matrix-core k order; row M (and rows past it) zero
+  // this K slice of the token rows in the matrix-core k order; row M (and
+  // rows past it, and packed rows past K) zero
   constexpr uint32_t kOob = 0xFFFFFFF0u;
-  uint4* xs = mf_lds;  // [M + 1][Kp]
+  constexpr int kSp = kMnWaves * KBW * 4;  // packed rows of a slice
+  const int r0 = slice * kSp;
+  uint4* xs = mf_lds;  // [M + 1][kSp]
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
-  for (int i = tid; i < (a.M + 1) * Kp; i += kMnThreads) {
-    const int n = i / Kp, r = i - n * Kp;
+  for (int i = tid; i < (a.M + 1) * kSp; i += kMnThreads) {
+    const int n = i / kSp, r = r0 + (i - n * kSp);
     const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-        ra, n < a.M ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
+        ra, (n < a.M && r < Kp) ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
     xs[i] = moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
   }
   __syncthreads();
 
   const uint32_t mq = q4_magic();
-  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
+  // k block kb of this wave sits at packed row 4 (kb - slice * 8 KBW) + lq of the slice
+  const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * kSp + lq - 4 * (slice * kMnWaves * KBW);
   f32x4_t y0[4], y1[4];
   mn_products<KBW, KPG>(w0, s0, xrow, kb0, KB, mq, y0);
   if constexpr (GATED) mn_products<KBW, KPG>(w1, s1, xrow, kb0, KB, mq, y1);
@@ -883,19 +887,27 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MnArgs a)
 constexpr size_t kMnMaxLds = 150 * 1024;
 constexpr int kMnKbw[] = {2, 4, 8, 12, 16, 24, 32};
 
-size_t mfma_narrow_lds(int M, int K, bool gated) {
-  const size_t xs = (size_t)(M + 1) * (K / 8) * 16;
+// LDS of a launch: the slice's token rows, then (reused) the waves' sums
+size_t mfma_narrow_lds(int M, int kbw, bool gated) {
+  const size_t xs = (size_t)(M + 1) * kMnWaves * kbw * 4 * 16;
   const size_t red = (size_t)(gated ? 2 : 1) * kMnWaves * 16 * kMnCols * 4;
   return xs > red ? xs : red;
 }
 
 // k blocks per wave at most: twice the weights (gated) or twice the scales
-// (group size 64) per wave would otherwise spill
-int mn_max_kbw(int gs, bool gated) { return gated ? 8 : (gs == 64 ? 16 : 32); }
+// (group size 64) per wave would otherwise spill, and the slice's token rows
+// must fit the LDS
+int mn_max_kbw(int gs, bool gated, int M) {
+  const int cap = gated ? 8 : (gs == 64 ? 16 : 32);
+  int best = 0;
+  for (int v : kMnKbw)
+    if (v <= cap && mfma_narrow_lds(M, v, gated) <= kMnMaxLds) best = v;
+  return best;
+}
 
 bool mfma_narrow_ok(int M, int K, int gs, bool gated) {
   return M >= 3 && M <= kMfMaxM && K % 32 == 0 && (gs == 64 || gs == 128) &&
-         K <= kMnWaves * 32 * mn_max_kbw(gs, gated) && mfma_narrow_lds(M, K, gated) <= kMnMaxLds;
+         mn_max_kbw(gs, gated, M) >= gs / 32;
 }
 
 bool mfma_narrow_path(int M, int K, int N, int gs) {
@@ -926,14 +938,15 @@ constexpr int kMnTargetWgs = 256;
 struct MnPlan {
   int kbw, ks;
 };
-MnPlan mn_plan(int K, int tiles, int gs, bool gated) {
+MnPlan mn_plan(int M, int K, int tiles, int gs, bool gated) {
   const int KB = K / 32, kpg = gs / 32;
   const int ks_want = (kMnTargetWgs + tiles - 1) / tiles;
   const int per_slice = (KB + ks_want - 1) / ks_want;
   const int need = (per_slice + kMnWaves - 1) / kMnWaves;  // k blocks per wave
-  MnPlan p{mn_max_kbw(gs, gated), 1};
+  const int vmax = mn_max_kbw(gs, gated, M);
+  MnPlan p{vmax, 1};
   for (int v : kMnKbw)
-    if (v >= need && v >= kpg && v <= mn_max_kbw(gs, gated)) {
+    if (v >= need && v >= kpg && v <= vmax) {
       p.kbw = v;
       break;
     }
@@ -946,7 +959,7 @@ int mn_tiles(const int* N, int n) {
   return t;
 }
 size_t mn_workspace_bytes(int M, int K, int tiles, int gs, bool gated) {
-  const MnPlan p = mn_plan(K, tiles, gs, gated);
+  const MnPlan p = mn_plan(M, K, tiles, gs, gated);
   return p.ks > 1 ? round_up(kCtrBytes + (size_t)p.ks * (gated ? 2 : 1) * M * tiles * kMnCols * sizeof(float)) : 0;
 }
 
@@ -968,7 +981,7 @@ int launch_mfma_narrow(const void* A, int M, int K, int gs, float cap, const Nar
   if (gated) tiles = (segs[0].N + kMnCols - 1) / kMnCols;
   for (int i = nseg; i < kMaxSegs; ++i) k.seg[i].tile0 = 0x7fffffff;
   k.ntot = tiles * kMnCols;
-  const MnPlan p = mn_plan(K, tiles, gs, gated);
+  const MnPlan p = mn_plan(M, K, tiles, gs, gated);
   k.ks = p.ks;
   if (p.ks > 1) {
     if ((size_t)tiles * sizeof(int) > kCtrBytes)
@@ -979,7 +992,7 @@ int launch_mfma_narrow(const void* A, int M, int K, int gs, float cap, const Nar
     k.ctr = (int*)workspace;
     k.part = (float*)((char*)workspace + kCtrBytes);
   }
-  const size_t lds = mfma_narrow_lds(M, K, gated);
+  const size_t lds = mfma_narrow_lds(M, p.kbw, gated);
   const int kpg = gs / 32;
   switch ((gated ? 10000 : 0) + p.kbw * 10 + kpg) {
 #define GI_MN_CASE(G, KBW, KPG)                      \
