@@ -272,7 +272,7 @@ def bench_front_end(copies, steps, device):
     and M=7, and the whole block from the hidden state at M=1."""
     res = {}
     n = min(steps, 200)
-    for m in (1, 7):
+    for m in (1, 7, 512):
         row = {}
         for mode in ("fused", "torch"):
             runner = FrontEndRunner(m, copies, device, mode)
