@@ -107,6 +107,47 @@ def test_other_entry_points_validate(lib):
     assert ei.value.code == L.GI_ERR_INVALID_ARG
 
 
+def test_router_ingest_and_dense_entry_points_validate(lib):
+    """The entry points added for the router front-end, checkpoint ingest and
+    the dense callers reject bad arguments on the host, before any launch."""
+    vp = ctypes.c_void_p(16)
+    R = lib.gi_moe_router_logits
+    assert R(vp, L.DTYPE_FP32, None, vp, 1e-6, vp, 1, 2816, 128, None) == L.GI_ERR_UNSUPPORTED  # fp32 x
+    assert R(vp, L.DTYPE_BF16, None, vp, 1e-6, vp, 1, 2812, 128, None) == L.GI_ERR_UNSUPPORTED  # H % 8
+    assert R(vp, L.DTYPE_BF16, None, vp, 1e-6, vp, 1, 8192, 128, None) == L.GI_ERR_UNSUPPORTED  # H > 4096
+    assert R(vp, L.DTYPE_BF16, None, None, 1e-6, vp, 1, 2816, 128, None) == L.GI_ERR_INVALID_ARG  # no gate
+    assert R(vp, L.DTYPE_BF16, None, vp, -1.0, vp, 1, 2816, 128, None) == L.GI_ERR_INVALID_ARG  # eps < 0
+    assert R(None, L.DTYPE_BF16, None, None, 1e-6, None, 0, 2816, 128, None) == L.GI_OK          # M = 0
+    lh = lib.gi_moe_layer_from_hidden
+    args = [vp, L.DTYPE_BF16, None, vp, 1e-6, None, None, vp, vp, 22, vp, vp, 6, vp, None, None,
+            1, 2816, 704, 128, 8, 128, vp, 1 << 20, 0, None]
+    assert lh(*args) == L.GI_ERR_INVALID_ARG                                  # no logits buffer
+    args[5], args[20] = vp, 129
+    assert lh(*args) == L.GI_ERR_INVALID_ARG                                  # top_k > E
+    I = lib.gi_w4a16_ingest
+    assert I(vp, vp, L.DTYPE_BF16, 64, 100, 1, vp, vp, 64, None) == L.GI_ERR_INVALID_ARG  # K % 8
+    assert I(vp, vp, L.DTYPE_BF16, 64, 128, 2, vp, vp, 32, None) == L.GI_ERR_INVALID_ARG  # ld < N
+    assert I(vp, vp, L.DTYPE_INT32, 64, 128, 2, vp, vp, 64, None) == L.GI_ERR_UNSUPPORTED  # scale dtype
+    assert I(None, None, L.DTYPE_BF16, 0, 128, 2, None, None, 0, None) == L.GI_OK          # N = 0
+    assert I(None, vp, L.DTYPE_BF16, 64, 128, 2, vp, vp, 64, None) == L.GI_ERR_INVALID_ARG  # null words
+    n5 = (ctypes.c_int * 5)(*[64] * 5)
+    p5 = (ctypes.c_void_p * 5)(*[16] * 5)
+    assert lib.gi_w4a16_linear_multi(vp, L.DTYPE_BF16, 5, p5, p5, n5, p5, n5, 1, 256, 64, None, 0,
+                                     None) == L.GI_ERR_INVALID_ARG            # more than 4 projections
+    n2 = (ctypes.c_int * 2)(64, 66)
+    assert lib.gi_w4a16_linear_multi(vp, L.DTYPE_BF16, 2, p5, p5, n2, p5, n2, 1, 256, 64, None, 0,
+                                     None) == L.GI_ERR_INVALID_ARG            # N % 4
+    assert lib.gi_w4a16_gated_mlp(vp, L.DTYPE_BF16, vp, vp, 4, vp, vp, 4, vp, 1, 256, 66, 64, None, 0,
+                                  None) == L.GI_ERR_INVALID_ARG               # N % 4
+    assert lib.gi_w4a16_gated_mlp(vp, L.DTYPE_FP16, vp, vp, 4, vp, vp, 4, vp, 1, 256, 64, 64, None, 0,
+                                  None) == L.GI_ERR_UNSUPPORTED               # fp16 activations
+    # workspace queries of the new calls are host-only
+    assert lib.gi_w4a16_gated_mlp_workspace_bytes(1, 2816, 2112, 64) == 0    # one launch, none
+    assert lib.gi_w4a16_gated_mlp_workspace_bytes(7, 2816, 2112, 64) > 0     # matrix cores, K split
+    assert lib.gi_w4a16_linear_multi_workspace_bytes(3, (ctypes.c_int * 3)(4096, 2048, 2048), 1, 2816,
+                                                     64) == 0
+
+
 def test_missing_library_raises_no_fallback(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "LIB_PATH", tmp_path / "absent.so")
     monkeypatch.setattr(L, "_lib", None)
