@@ -28,6 +28,7 @@
 #include "../../include/gemmainfer_amd.h"
 #include "gi_common.h"
 #include "gi_internal.h"
+#include "moe_shared.h"
 
 #include <cmath>
 
@@ -259,6 +260,150 @@ __global__ __launch_bounds__(512) void moe_router_rows_kernel(RouterArgs a) {
   }
 }
 
+// Prefill shape (M > 8, H % 32 == 0): the gate product on matrix cores.  A
+// workgroup of 8 waves owns 16 rows and 16 experts: its waves normalise 2 rows
+// each into LDS as bf16 (the same roundings as above), then each wave runs
+// v_mfma_f32_16x16x32_bf16 over an eighth of K with A = the 16 normalised rows
+// and B = the 16 gate rows (lane l: expert l % 16, 8 consecutive k at
+// 8 (l / 16)), all of its k blocks loaded before the first product; the eight
+// partial products are added in LDS.
+using moe::f32x4_t;
+constexpr int kRmRows = 16;
+constexpr int kRmWaves = 8;
+constexpr int kRmMaxKbq = 16;  // k blocks per wave: H <= 4096
+constexpr size_t kRmMaxLds = 132 * 1024;
+
+__global__ __launch_bounds__(512) void moe_router_mfma_kernel(RouterArgs a) {
+  extern __shared__ uint4 xn[];  // [16][H / 8] normalised rows (bf16)
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int hv = a.H >> 3, KB = a.H >> 5;
+  const int m0 = blockIdx.y * kRmRows;
+  const int e0 = blockIdx.x * 16;
+  constexpr uint32_t kOob = kRouterOob;
+
+  // rows m0 + wave + 8i, i < 2: every load first (router scale, then the two
+  // rows), then sum of squares, rsqrt, bf16(bf16(x r) s) into LDS
+  const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.rscale, a.rscale ? (uint32_t)(a.H * 2) : 0u);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (uint32_t)((size_t)a.M * a.H * 2));
+  constexpr int kRw = kRmRows / kRmWaves;  // rows per wave
+  uint4 sv[kRouterMaxJ];
+#pragma unroll
+  for (int j = 0; j < kRouterMaxJ; ++j) {
+    const int v = lane + kWave * j;
+    const u32x4_t t = __builtin_amdgcn_raw_buffer_load_b128(rs, v < hv ? (uint32_t)(16 * v) : kOob, 0, 0);
+    sv[j] = make_uint4(t.x, t.y, t.z, t.w);
+  }
+  uint4 xv[kRw][kRouterMaxJ];
+#pragma unroll
+  for (int i = 0; i < kRw; ++i) {
+    const int m = m0 + wave + kRmWaves * i;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; ++j) {
+      const int v = lane + kWave * j;
+      const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(
+          rx, (m < a.M && v < hv) ? (uint32_t)(((size_t)m * a.H + 8 * v) * 2) : kOob, 0, 0);
+      xv[i][j] = make_uint4(d.x, d.y, d.z, d.w);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // s = bf16(router_scale * c) as packed pairs; a missing router_scale is ones
+#pragma unroll
+  for (int j = 0; j < kRouterMaxJ; ++j) {
+    uint32_t w[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t src = a.rscale ? w[q] : 0x3f803f80u;
+      w[q] = pack_bf16x2(bf16lo(src) * a.c, bf16hi(src) * a.c);
+    }
+    sv[j] = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+#pragma unroll
+  for (int i = 0; i < kRw; ++i) {
+    const int r = wave + kRmWaves * i;
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; ++j) ss = sq8(xv[i][j], ss);
+    const float rr = rsqrtf(wave_sum_f32(ss) / (float)a.H + a.eps);
+#pragma unroll
+    for (int j = 0; j < kRouterMaxJ; ++j) {
+      const int v = lane + kWave * j;
+      if (v < hv) {
+        const uint32_t sw[4] = {sv[j].x, sv[j].y, sv[j].z, sv[j].w};
+        const uint32_t w[4] = {xv[i][j].x, xv[i][j].y, xv[i][j].z, xv[i][j].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t n = pack_bf16x2(bf16lo(w[q]) * rr, bf16hi(w[q]) * rr);
+          o[q] = pack_bf16x2(bf16lo(n) * bf16lo(sw[q]), bf16hi(n) * bf16hi(sw[q]));
+        }
+        xn[r * hv + v] = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // gate products: the 8 waves split K; lane l holds expert e0 + l % 16 at
+  // k = 32 kb + 8 (l / 16); every k block of a wave is loaded before the first
+  // product (the normalisation above has released its registers)
+  const int lr = lane & 15, lq = lane >> 4;
+  const int e = e0 + lr;
+  const int kbq = (KB + kRmWaves - 1) / kRmWaves, kbw0 = wave * kbq;
+  const __amdgpu_buffer_rsrc_t rg = buffer_rsrc(a.gate, (uint32_t)((size_t)a.E * a.H * 2));
+  const uint32_t gbase = (uint32_t)(((size_t)e * a.H + 8 * lq) * 2);
+  uint4 g[kRmMaxKbq];
+#pragma unroll
+  for (int s = 0; s < kRmMaxKbq; ++s) {
+    const int kb = kbw0 + s;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(
+        rg, (e < a.E && s < kbq && kb < KB) ? gbase + (uint32_t)(kb * 64) : kOob, 0, 0);
+    g[s] = make_uint4(d.x, d.y, d.z, d.w);
+  }
+  const uint4* arow = xn + lr * hv + lq;  // A: row lr, k = 32 kb + 8 lq
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t acc0 = zf, acc1 = zf;
+#pragma unroll
+  for (int s = 0; s < kRmMaxKbq; ++s) {
+    const int kb = kbw0 + s;
+    if (s < kbq && kb < KB) {
+      const uint4 A = arow[4 * kb];
+      if (s & 1) acc1 = moe::mfma_bf16(A, g[s], acc1);
+      else acc0 = moe::mfma_bf16(A, g[s], acc0);
+    }
+  }
+  // D: row 4 lq + j, expert lr; the 8 waves' K ranges summed in a fixed order
+  float* red = (float*)(xn + kRmRows * hv);  // [8 waves][16 rows][16 experts]
+#pragma unroll
+  for (int j = 0; j < 4; ++j) red[(wave * 16 + 4 * lq + j) * 16 + lr] = acc0[j] + acc1[j];
+  __syncthreads();
+  if (tid < 256) {
+    const int r = tid >> 4, c = tid & 15;
+    const int m = m0 + r, ee = e0 + c;
+    if (m < a.M && ee < a.E) {
+      float v = 0.f;
+#pragma unroll
+      for (int w2 = 0; w2 < kRmWaves; ++w2) v += red[(w2 * 16 + r) * 16 + c];
+      a.logits[(size_t)m * a.E + ee] = f32_to_bf16(v);
+    }
+  }
+}
+
+int launch_router_mfma(const RouterArgs& a, hipStream_t stream) {
+  static bool attr_set[64];
+  int dev = 0;
+  hipError_t e0 = hipGetDevice(&dev);
+  if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
+  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
+    e0 = hipFuncSetAttribute((const void*)moe_router_mfma_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)kRmMaxLds);
+    if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
+    attr_set[dev] = true;
+  }
+  const dim3 grid((unsigned)((a.E + 15) / 16), (unsigned)((a.M + kRmRows - 1) / kRmRows));
+  hipLaunchKernelGGL(moe_router_mfma_kernel, grid, dim3(kRmWaves * kWave), (size_t)kRmRows * a.H * 2 + kRmWaves * 256 * 4,
+                     stream, a);
+  return GI_OK;
+}
+
 template <int EPW, int J, int R>
 void launch_router_variant(const RouterArgs& a, hipStream_t stream) {
   const dim3 grid((unsigned)((a.E + kRouterWaves * EPW - 1) / (kRouterWaves * EPW)),
@@ -299,7 +444,10 @@ int launch_moe_router(const void* x, const void* router_scale, const void* gate,
   a.E = E;
   a.eps = eps;
   a.c = (float)std::pow((double)H, -0.5);  // hidden_size ** -0.5 as a float operand
-  if (M > 64) launch_router_j<4, 8>(a, stream);
+  if (M > 8 && H % 32 == 0) {
+    const int st = launch_router_mfma(a, stream);
+    if (st != GI_OK) return st;
+  } else if (M > 64) launch_router_j<4, 8>(a, stream);
   else if (M > 8) launch_router_j<1, 8>(a, stream);
   else hipLaunchKernelGGL(moe_router_rows_kernel, dim3((unsigned)E, (unsigned)M), dim3(512), 0, stream, a);
   const hipError_t e = hipGetLastError();

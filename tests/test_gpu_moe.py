@@ -252,7 +252,8 @@ def test_layer_from_logits_gemma(gemma128):
 
 # ---------------------------------------------------------------- router front-end
 ROUTER_SHAPES = [(1, 2816, 128), (7, 2816, 128), (8, 2816, 128), (13, 2816, 128),
-                 (100, 2816, 128), (3, 256, 8), (5, 1024, 1000), (2, 4096, 64), (9, 520, 36)]
+                 (100, 2816, 128), (3, 256, 8), (5, 1024, 1000), (2, 4096, 64), (9, 520, 36),
+                 (40, 1024, 72), (17, 4096, 130)]
 
 
 @pytest.mark.parametrize("m,h,e", ROUTER_SHAPES)
@@ -264,8 +265,9 @@ def test_router_logits_match_oracle(m, h, e):
     for rs in (W["router_scale"], None):
         print(f"router m={m} h={h} e={e} scale={rs is not None}", flush=True)
         got = ops.moe_router_logits(x.to(DEV), None if rs is None else rs.to(DEV), W["gate"].to(DEV))
-        ref, _ = O.router_logits(np64(x), None if rs is None else np64(rs), np64(W["gate"]), 1e-6)
-        assert_logits_close(got, ref, f"router m={m} h={h} e={e}")
+        ref, xr = O.router_logits(np64(x), None if rs is None else np64(rs), np64(W["gate"]), 1e-6)
+        assert_logits_close(got, ref, f"router m={m} h={h} e={e}",
+                            abs_terms=np.abs(xr) @ np.abs(np64(W["gate"])).T, k=h)
 
 
 def test_router_matches_reference_golden():
@@ -291,8 +293,9 @@ def test_layer_from_hidden_gemma(gemma128, m):
     out, idx, w, logits = ops.moe_layer_from_hidden(
         x, R["router_scale"].to(DEV), R["gate"].to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
         Wd["down_packed"], Wd["down_scales"], 8, 128, expert_scale=es)
-    ref_logits, _ = O.router_logits(np64(x), np64(R["router_scale"]), np64(R["gate"]), 1e-6)
-    assert_logits_close(logits, ref_logits, f"layer_from_hidden logits m={m}")
+    ref_logits, xr = O.router_logits(np64(x), np64(R["router_scale"]), np64(R["gate"]), 1e-6)
+    assert_logits_close(logits, ref_logits, f"layer_from_hidden logits m={m}",
+                        abs_terms=np.abs(xr) @ np.abs(np64(R["gate"])).T, k=2816)
     ref_out, ref_idx, ref_w, _ = O.moe_layer_from_logits(
         np64(x), np64(logits), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
         W["down_packed"].numpy(), np64(W["down_scales"]), 8, 128, expert_scale=np64(R["expert_scale"]))
