@@ -144,7 +144,7 @@ def test_dense_callers_gemma_gs64(name, m):
     assert_bf16_close(C_[:, cols.to(DEV)], ref, f"dense {name} m={m}")
 
 
-@pytest.mark.parametrize("m", [1, 2, 7])
+@pytest.mark.parametrize("m", [1, 2, 7, 64])
 def test_linear_multi_qkv(m):
     """q, k, v of one input in one call: bit-identical to three separate linears
     at 1-2 rows (same kernel, same sums), within tolerance of the oracle on
@@ -179,3 +179,20 @@ def test_gated_mlp_act(m):
     ref = O.gated_mlp_act(np64(A), (G[0][:, cols].numpy(), np64(G[1][:, cols])),
                           (U[0][:, cols].numpy(), np64(U[1][:, cols])), 64)
     assert_bf16_close(out[:, cols.to(DEV)], ref, f"gated mlp m={m}")
+
+
+@pytest.mark.parametrize("m,k,gs,floor", [(5, 2880, 128, True), (12, 4096, 128, False), (3, 8192, 64, False)])
+def test_matrix_core_narrow_group_sizes(m, k, gs, floor):
+    """The 3-16 row matrix-core path at group size 128 (floor-size scales: rows
+    past the last whole group dropped) and at a long K with group size 64."""
+    n = 2048
+    print(f"mfma narrow m={m} k={k} gs={gs} floor={floor}", flush=True)
+    g = torch.Generator().manual_seed(m + k)
+    B = torch.randint(-(2 ** 31), 2 ** 31 - 1, (k // 8, n), generator=g, dtype=torch.int64).to(torch.int32)
+    groups = k // gs if floor else -(-k // gs)
+    S = (torch.randn(groups, n, generator=g).abs() * 0.02).to(torch.bfloat16)
+    A = synth.activations(m, k, seed=m)
+    C = ops.w4a16_linear(A.to(DEV), B.to(DEV), S.to(DEV), gs)
+    cols = torch.arange(0, n, 5)
+    ref = O.w4a16_linear(np64(A), B[:, cols].numpy(), np64(S[:, cols]), gs)
+    assert_bf16_close(C[:, cols.to(DEV)], ref, f"mfma narrow m={m} k={k} gs={gs}")
