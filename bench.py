@@ -481,33 +481,31 @@ SLIDING = ("q", "k", "v", "o", "mlp_gate", "mlp_up", "mlp_down")
 
 
 def bench_ingest(device):
-    """gi_w4a16_ingest of one MoE layer's experts (128 x gate, up, down at
-    H=2816, I=704, gs 64) from checkpoint layout already in HBM: bytes read +
-    written per second, eager launches between HIP events."""
+    """gi_w4a16_ingest_batched of one MoE layer's experts (128 x gate, up, down
+    at H=2816, I=704, gs 64) from checkpoint layout already in HBM: one launch
+    per tensor kind (6 in all); bytes read + written per second between HIP
+    events."""
     lib = L.load()
     g = torch.Generator(device=device)
     g.manual_seed(1)
-    shapes = [(I, H), (I, H), (H, I)]  # (N, K): gate, up, down
-    src = [(torch.randint(-(2 ** 31), 2 ** 31, (n, k // 8), generator=g, device=device, dtype=torch.int64)
-            .to(torch.int32), torch.randn((n, k // DENSE_GS), generator=g, device=device).to(torch.bfloat16))
-           for n, k in shapes]
+    shapes = [(I, H, 0), (I, H, I), (H, I, 0)]  # (N, K, column offset): gate, up, down
+    src = [(torch.randint(-(2 ** 31), 2 ** 31, (E, n, k // 8), generator=g, device=device, dtype=torch.int64)
+            .to(torch.int32), torch.randn((E, n, k // DENSE_GS), generator=g, device=device).to(torch.bfloat16))
+           for n, k, _ in shapes]
     gu = torch.empty((E, H // 8, 2 * I), dtype=torch.int32, device=device)
     gus = torch.empty((E, H // DENSE_GS, 2 * I), dtype=torch.bfloat16, device=device)
     dn = torch.empty((E, I // 8, H), dtype=torch.int32, device=device)
     dns = torch.empty((E, I // DENSE_GS, H), dtype=torch.bfloat16, device=device)
     stream = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
-    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    dst = [(gu, gus, 2 * I), (gu, gus, 2 * I), (dn, dns, H)]
 
     def one_layer():
-        for e in range(E):
-            for j, (dst_p, dst_s, lo, ld) in enumerate(((gu[e], gus[e], 0, 2 * I), (gu[e], gus[e], I, 2 * I),
-                                                        (dn[e], dns[e], 0, H))):
-                n, k = shapes[j]
-                wp, ws = src[j]
-                st = lib.gi_w4a16_ingest(p(wp), p(ws), L.DTYPE_BF16, n, k, k // DENSE_GS,
-                                         ctypes.c_void_p(dst_p.data_ptr() + 4 * lo),
-                                         ctypes.c_void_p(dst_s.data_ptr() + 2 * lo), ld, stream)
-                L.check(st, "gi_w4a16_ingest")
+        for (n, k, lo), (wp, ws), (dp, ds, ld) in zip(shapes, src, dst):
+            L.check(lib.gi_w4a16_ingest_batched(
+                ctypes.c_void_p(wp.data_ptr()), ctypes.c_void_p(ws.data_ptr()), L.DTYPE_BF16, E, n, k,
+                k // DENSE_GS, n * (k // 8), n * (k // DENSE_GS), ctypes.c_void_p(dp.data_ptr() + 4 * lo),
+                ctypes.c_void_p(ds.data_ptr() + 2 * lo), ld, dp.stride(0), ds.stride(0), stream),
+                "gi_w4a16_ingest_batched")
 
     one_layer()
     torch.cuda.synchronize()
@@ -517,9 +515,9 @@ def bench_ingest(device):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1000.0
-    nbytes = 2 * E * sum(n * (k // 8) * 4 + n * (k // DENSE_GS) * 2 for n, k in shapes)
+    nbytes = 2 * E * sum(n * (k // 8) * 4 + n * (k // DENSE_GS) * 2 for n, k, _ in shapes)
     return {"us_per_moe_layer": us, "bytes_read_plus_written": nbytes, "gbps": nbytes / (us * 1e-6) / 1e9,
-            "launches": 2 * 3 * E}
+            "launches": 2 * len(shapes)}
 
 
 class FusedDenseRunner:

@@ -66,6 +66,8 @@ SIGNATURES = {
                                    c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_size_t, c_void_p]),
     "gi_w4a16_ingest": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
                                 c_void_p, c_int64, c_void_p]),
+    "gi_w4a16_ingest_batched": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_int64,
+                                        c_int64, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
     "gi_softcap_inplace": (c_int, [c_void_p, c_int, c_int64, c_float, c_void_p]),
     "gi_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int, c_float,
                            c_int, c_void_p]),

@@ -138,6 +138,33 @@ def ingest_linear(weight_packed: torch.Tensor, weight_scale: torch.Tensor,
     return packed_out, scales_out
 
 
+def ingest_batched(weight_packed: torch.Tensor, weight_scale: torch.Tensor, packed_out: torch.Tensor,
+                   scales_out: torch.Tensor) -> None:
+    """``B`` linears of one shape in one launch: weight_packed [B, N, K/8] and
+    weight_scale [B, N, G] (device tensors, checkpoint layout) into
+    packed_out [B, K/8, N] and scales_out [B, G, N] (unit column stride; views
+    such as the gate or up half of gate_up are fine)."""
+    dev = _on_device(weight_packed, weight_scale, packed_out, scales_out)
+    _require(weight_packed.dim() == 3 and weight_packed.dtype == torch.int32, "weight_packed must be int32 [B, N, K/8]")
+    _require(weight_scale.dim() == 3 and weight_scale.shape[:2] == weight_packed.shape[:2],
+             "weight_scale must be [B, N, groups]")
+    _require(weight_scale.dtype in (torch.bfloat16, torch.float16, torch.float32),
+             "weight_scale must be bf16, fp16 or fp32", TypeError)
+    b, n, kp = weight_packed.shape
+    g = weight_scale.shape[2]
+    _require(tuple(packed_out.shape) == (b, kp, n) and packed_out.dtype == torch.int32 and packed_out.stride(2) == 1,
+             f"packed_out must be int32 [{b}, {kp}, {n}] with unit column stride")
+    _require(tuple(scales_out.shape) == (b, g, n) and scales_out.dtype == torch.bfloat16 and scales_out.stride(2) == 1,
+             f"scales_out must be bf16 [{b}, {g}, {n}] with unit column stride")
+    ld = packed_out.stride(1)
+    _require(g <= 1 or scales_out.stride(1) == ld, "packed_out and scales_out must share one row stride")
+    wp = weight_packed.contiguous()
+    ws = weight_scale.contiguous()
+    L.check(L.load().gi_w4a16_ingest_batched(
+        _ptr(wp), _ptr(ws), _DTYPE_CODE[ws.dtype], b, n, kp * 8, g, n * kp, n * g, _ptr(packed_out),
+        _ptr(scales_out), ld, packed_out.stride(0), scales_out.stride(0), _stream(dev)), "w4a16_ingest_batched")
+
+
 def load_layer(paths: Iterable, layer: int, device, dtype=torch.bfloat16) -> dict:
     """One decoder layer's W4A16 tensors on ``device``:
 
@@ -151,9 +178,12 @@ def load_layer(paths: Iterable, layer: int, device, dtype=torch.bfloat16) -> dic
     idx = scan_layer(paths, layer)
     handles = {p: safe_open(p, framework="pt", device="cpu") for p in {v[0] for v in idx.values()}}
 
-    def read(c):
+    def read_cpu(c):
         path, key, _, _ = idx[c]
-        return handles[path].get_tensor(key).to(device)
+        return handles[path].get_tensor(key)
+
+    def read(c):
+        return read_cpu(c).to(device)
 
     out = {"dense": {}, "moe": {}}
     for name in DENSE_LINEARS.values():
@@ -178,15 +208,25 @@ def load_layer(paths: Iterable, layer: int, device, dtype=torch.bfloat16) -> dic
         moe["down_packed"] = torch.zeros((e_count, ip, h_size), dtype=torch.int32, device=device)
         moe["down_scales"] = torch.zeros((e_count, ds_shape[1], h_size), dtype=torch.bfloat16,
                                          device=device)
-        for e in experts:
-            for proj, lo in (("gate_proj", 0), ("up_proj", i_size)):
-                ingest_linear(read(("expert", e, proj, "weight_packed")),
-                              read(("expert", e, proj, "weight_scale")),
-                              moe["gate_up_packed"][e, :, lo:lo + i_size],
-                              moe["gate_up_scales"][e, :, lo:lo + i_size])
-            ingest_linear(read(("expert", e, "down_proj", "weight_packed")),
-                          read(("expert", e, "down_proj", "weight_scale")),
-                          moe["down_packed"][e], moe["down_scales"][e])
+        if experts == list(range(e_count)):
+            # every expert present: one batched transpose per tensor kind
+            for proj, lo, dp, ds in (("gate_proj", 0, "gate_up_packed", "gate_up_scales"),
+                                     ("up_proj", i_size, "gate_up_packed", "gate_up_scales"),
+                                     ("down_proj", 0, "down_packed", "down_scales")):
+                wp = torch.stack([read_cpu(("expert", e, proj, "weight_packed")) for e in experts]).to(device)
+                ws = torch.stack([read_cpu(("expert", e, proj, "weight_scale")) for e in experts]).to(device)
+                n = wp.shape[1]
+                ingest_batched(wp, ws, moe[dp][:, :, lo:lo + n], moe[ds][:, :, lo:lo + n])
+        else:
+            for e in experts:
+                for proj, lo in (("gate_proj", 0), ("up_proj", i_size)):
+                    ingest_linear(read(("expert", e, proj, "weight_packed")),
+                                  read(("expert", e, proj, "weight_scale")),
+                                  moe["gate_up_packed"][e, :, lo:lo + i_size],
+                                  moe["gate_up_scales"][e, :, lo:lo + i_size])
+                ingest_linear(read(("expert", e, "down_proj", "weight_packed")),
+                              read(("expert", e, "down_proj", "weight_scale")),
+                              moe["down_packed"][e], moe["down_scales"][e])
     for name in ROUTER_TENSORS.values():
         if ("router", name) in idx:
             out["moe"][name] = read(("router", name)).to(dtype).contiguous()

@@ -248,6 +248,15 @@ int gi_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int 
                                  scales_out, ld_out, as_stream(stream));
 }
 
+int gi_w4a16_ingest_batched(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int batch,
+                            int N, int K, int n_groups, int64_t src_stride_packed, int64_t src_stride_scale,
+                            int32_t* packed_out, void* scales_out, int64_t ld_out, int64_t dst_stride_packed,
+                            int64_t dst_stride_scale, void* stream) {
+  return gi::launch_w4a16_ingest_batched(weight_packed, weight_scale, scale_dtype, batch, N, K, n_groups,
+                                         src_stride_packed, src_stride_scale, packed_out, scales_out, ld_out,
+                                         dst_stride_packed, dst_stride_scale, as_stream(stream));
+}
+
 int gi_softcap_inplace(void* x, int dtype, int64_t n, float cap, void* stream) {
   return gi::launch_softcap(x, dtype, n, cap, as_stream(stream));
 }

@@ -80,6 +80,10 @@ size_t w4a16_multi_workspace_bytes(int n, const int* N, int M, int K, int gs);
 int launch_w4a16_gated(const void* A, const int32_t* gB, const void* gS, int gG, const int32_t* uB, const void* uS,
                        int uG, void* out, int M, int K, int N, int gs, void* workspace, size_t workspace_bytes,
                        hipStream_t stream);
+int launch_w4a16_ingest_batched(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int batch,
+                                int N, int K, int n_groups, int64_t src_stride_packed, int64_t src_stride_scale,
+                                int32_t* packed_out, void* scales_out, int64_t ld_out, int64_t dst_stride_packed,
+                                int64_t dst_stride_scale, hipStream_t stream);
 int launch_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype, int N,
                         int K, int n_groups, int32_t* packed_out, void* scales_out, int64_t ld_out,
                         hipStream_t stream);

@@ -25,7 +25,7 @@
  *   gi_moe_layer_from_hidden    <- gemma.py:75-98 (the MoE block's forward)
  *   gi_w4a16_linear_multi       <- the q/k/v marlin_w4a16 calls of attention.py:115-122
  *   gi_w4a16_gated_mlp          <- GemmaMLP gate/up + gelu * up (activations.py:26-28)
- *   gi_w4a16_ingest             <- gemmainfer/utils/weights.py:100-159 (checkpoint
+ *   gi_w4a16_ingest(_batched)   <- gemmainfer/utils/weights.py:100-159 (checkpoint
  *                                  transposition of weight_packed / weight_scale)
  *   gi_softcap_inplace          <- gemmainfer_csrc.softcapping
  *                                  csrc/pybind.cpp:169-180 -> csrc/softcapping.cu:21-47
@@ -231,6 +231,17 @@ int gi_w4a16_gated_mlp(const void* A, int a_dtype,
 int gi_w4a16_ingest(const int32_t* weight_packed, const void* weight_scale, int scale_dtype,
                     int N, int K, int n_groups, int32_t* packed_out, void* scales_out,
                     int64_t ld_out, void* stream);
+
+/* The same for `batch` linears of one shape in one launch (the experts of a
+ * layer): matrix b reads weight_packed + b*src_stride_packed and
+ * weight_scale + b*src_stride_scale and writes packed_out +
+ * b*dst_stride_packed and scales_out + b*dst_stride_scale (strides in
+ * elements).  batch <= 65535.                                              */
+int gi_w4a16_ingest_batched(const int32_t* weight_packed, const void* weight_scale, int scale_dtype,
+                            int batch, int N, int K, int n_groups,
+                            int64_t src_stride_packed, int64_t src_stride_scale,
+                            int32_t* packed_out, void* scales_out, int64_t ld_out,
+                            int64_t dst_stride_packed, int64_t dst_stride_scale, void* stream);
 
 /* ---- drop-in companions (not on the MoE hot path) ----------------------- */
 /* x <- cap * tanh(x / cap), n elements, bf16/fp16/fp32.                      */
