@@ -130,6 +130,10 @@ def test_router_ingest_and_dense_entry_points_validate(lib):
     assert I(vp, vp, L.DTYPE_INT32, 64, 128, 2, vp, vp, 64, None) == L.GI_ERR_UNSUPPORTED  # scale dtype
     assert I(None, None, L.DTYPE_BF16, 0, 128, 2, None, None, 0, None) == L.GI_OK          # N = 0
     assert I(None, vp, L.DTYPE_BF16, 64, 128, 2, vp, vp, 64, None) == L.GI_ERR_INVALID_ARG  # null words
+    IB = lib.gi_w4a16_ingest_batched
+    assert IB(vp, vp, L.DTYPE_BF16, 70000, 64, 128, 2, 0, 0, vp, vp, 64, 0, 0, None) == L.GI_ERR_INVALID_ARG
+    assert IB(None, None, L.DTYPE_BF16, 0, 64, 128, 2, 0, 0, None, None, 64, 0, 0, None) == L.GI_OK  # empty
+    assert IB(vp, None, L.DTYPE_BF16, 4, 64, 128, 2, 0, 0, vp, vp, 64, 0, 0, None) == L.GI_ERR_INVALID_ARG
     n5 = (ctypes.c_int * 5)(*[64] * 5)
     p5 = (ctypes.c_void_p * 5)(*[16] * 5)
     assert lib.gi_w4a16_linear_multi(vp, L.DTYPE_BF16, 5, p5, p5, n5, p5, n5, 1, 256, 64, None, 0,
