@@ -757,7 +757,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X "
-              f"(--gpus {args.gpus} is not supported; the sharding design is in DESIGN.md)",
+              f"(--gpus {args.gpus} is not supported: one process drives one GPU)",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

@@ -7,7 +7,7 @@ import torch
 from oracle import moe_oracle as O
 
 # Tolerance gate for bf16 outputs against the float64 oracle.
-#   * rel-L2 <= 1e-2: the BASELINE north-star bound, literally.
+#   * rel-L2 <= 1e-2: the bound of BASELINE.json's north_star, literally.
 #   * elementwise |got - ref| <= 2e-2 + 2^-7 |ref|: the north-star max-abs 2e-2
 #     made scale-aware.  A literal max-abs of 2e-2 is below the bf16 spacing of
 #     outputs this large (|out| reaches 50-85, spacing 0.25-0.5); 2^-7 |ref| is
