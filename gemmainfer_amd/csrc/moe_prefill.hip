@@ -60,6 +60,8 @@ struct PfArgs {
 // ---------------------------------------------------------------------------
 // align
 // ---------------------------------------------------------------------------
+constexpr int kAlignPer = 8;  // pairs per thread kept in registers
+
 __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
     const void* idx, int idx_is64, const void* w, int w_dtype, int P, int E, int* offsets, int* order,
     int* posmap, float* wts) {
@@ -72,9 +74,29 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
     fill[e] = 0;
   }
   __syncthreads();
-  for (int p = tid; p < P; p += kAlignThreads) {
-    const int e = load_expert_id(idx, idx_is64, p);
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  // Up to kAlignPer pairs per thread: every id and weight is loaded once, up
+  // front (indices clamped to the last pair, so no load sits under a per-lane
+  // condition), and both passes below reuse the registers.
+  const bool cached = P > 0 && P <= kAlignThreads * kAlignPer;
+  int ev[kAlignPer];
+  float wv[kAlignPer];
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kAlignPer; ++i) {
+      const int p = tid + kAlignThreads * i;
+      const int pc = p < P ? p : P - 1;
+      ev[i] = load_expert_id(idx, idx_is64, pc);
+      wv[i] = load_weight_as_bf16(w, w_dtype, pc);
+      if (p >= P) ev[i] = -1;
+    }
+#pragma unroll
+    for (int i = 0; i < kAlignPer; ++i)
+      if (ev[i] >= 0 && ev[i] < E) atomicAdd(&cnt[ev[i]], 1);
+  } else {
+    for (int p = tid; p < P; p += kAlignThreads) {
+      const int e = load_expert_id(idx, idx_is64, p);
+      if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
   }
   __syncthreads();
   // exclusive scan of the counts (E <= 1024: one expert per thread)
@@ -97,6 +119,23 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
   }
   if (tid == E - 1) offsets[E] = excl + c;
   __syncthreads();
+  if (cached) {
+#pragma unroll
+    for (int i = 0; i < kAlignPer; ++i) {
+      const int p = tid + kAlignThreads * i;
+      if (p < P) {
+        const int e = ev[i];
+        int pos = -1;
+        if (e >= 0 && e < E) {
+          pos = cnt[e] + atomicAdd(&fill[e], 1);
+          order[pos] = p;
+        }
+        posmap[p] = pos;
+        wts[p] = wv[i];
+      }
+    }
+    return;
+  }
   for (int p = tid; p < P; p += kAlignThreads) {
     const int e = load_expert_id(idx, idx_is64, p);
     int pos = -1;
