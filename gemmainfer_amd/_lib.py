@@ -54,6 +54,7 @@ SIGNATURES = {
                                          c_int, c_int, c_int, c_int, c_int, c_int,
                                          c_void_p, c_size_t, c_int, c_void_p]),
     "gi_workspace_status": (c_int, [c_void_p, c_size_t, POINTER(c_int32), c_void_p]),
+    "gi_device_error_flags": (c_int, [c_int, c_int]),
     "gi_w4a16_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "gi_w4a16_linear": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                 c_int, c_int, c_int, c_int, c_float, c_void_p, c_size_t,

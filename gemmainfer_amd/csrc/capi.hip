@@ -1,6 +1,7 @@
 // extern "C" entry points declared in include/gemmainfer_amd.h: argument
 // checks, dtype dispatch and error reporting around the gfx950 kernels.
 
+#include <mutex>
 #include <string>
 
 #include "../../include/gemmainfer_amd.h"
@@ -33,6 +34,55 @@ int device_cu_count() {
     cached[dev] = n;
   }
   return cached[dev];
+}
+
+// Error flags of up to 64 devices, one 128-byte line each, in host memory
+// mapped into every device (coherent: a kernel's store is visible to the
+// host without a synchronisation).  Allocated on first use.
+namespace {
+constexpr int kFlagStride = 32;  // ints
+std::mutex g_flag_mu;
+int* g_flags = nullptr;
+bool g_flags_failed = false;
+
+int* flags_host() {
+  std::lock_guard<std::mutex> lk(g_flag_mu);
+  if (!g_flags && !g_flags_failed) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 64 * kFlagStride * sizeof(int),
+                      hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) == hipSuccess && p) {
+      for (int i = 0; i < 64 * kFlagStride; ++i) ((volatile int*)p)[i] = 0;
+      g_flags = (int*)p;
+    } else {
+      (void)hipGetLastError();
+      g_flags_failed = true;
+    }
+  }
+  return g_flags;
+}
+}  // namespace
+
+int* device_error_flag() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  int* h = flags_host();
+  if (!h) return nullptr;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, h + dev * kFlagStride, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return (int*)d;
+}
+
+int read_device_error_flags(int device, int clear) {
+  if (device < 0 || device >= 64) return fail(GI_ERR_INVALID_ARG, "device_error_flags: device index out of range");
+  int* h = flags_host();
+  if (!h) return 0;
+  volatile int* f = h + device * kFlagStride;
+  const int v = *f;
+  if (clear && v) *f = 0;
+  return v;
 }
 
 }  // namespace gi
@@ -193,6 +243,8 @@ int gi_moe_layer_from_hidden(const void* x, int x_dtype, const void* router_scal
                                   out_idx, out_w, M, H, I, E, top_k, group_size, workspace,
                                   workspace_bytes, spin_limit, stream);
 }
+
+int gi_device_error_flags(int device, int clear) { return gi::read_device_error_flags(device, clear); }
 
 int gi_workspace_status(void* workspace, size_t workspace_bytes, int32_t* host_status,
                         void* stream) {

@@ -264,6 +264,15 @@ __device__ __forceinline__ void store_relaxed(int* p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A bounded wait gave up (never expected: every wait is for work of the same
+// launch): the workspace's status bit, and the library's host-visible
+// per-device flag when there is one (host memory mapped into the device; the
+// drop-in module reads it without a synchronisation).
+__device__ __forceinline__ void report_timeout(int* status, int* host_flag) {
+  atomicOr(status, 1);  // GI_DEVICE_SPIN_TIMEOUT
+  if (host_flag) __hip_atomic_store(host_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 __device__ __forceinline__ float gelu_tanh(float x) {
   // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))  (reference marlin.cu:7-11)
   float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);

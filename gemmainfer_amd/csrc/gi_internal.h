@@ -17,6 +17,13 @@ int hip_fail(hipError_t e, const char* what);
 // Multiprocessor count of the current device (cached per device).
 int device_cu_count();
 
+// Device address of the current device's error flag: an int in host memory
+// mapped into the device, which kernels set when a bounded wait gives up
+// (null if the mapping is unavailable).  Read and cleared by
+// gi_device_error_flags without any device synchronisation.
+int* device_error_flag();
+int read_device_error_flags(int device, int clear);
+
 // ---- fused MoE --------------------------------------------------------------
 struct MoeHostArgs {
   const void* x;

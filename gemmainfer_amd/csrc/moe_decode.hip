@@ -62,6 +62,9 @@
 // sizes are powers of two), and one buffer resource per tensor with a scalar
 // per-expert offset.
 
+#include <mutex>
+#include <vector>
+
 #include "../../include/gemmainfer_amd.h"
 #include "gi_common.h"
 #include "gi_internal.h"
@@ -120,6 +123,7 @@ struct DecArgs {
                                // order, inverted bf16, matrix-core k order
   float* part;                 // [2][units][kPartSlots][kRows][32] partial sums, inverted bits
   int* status;
+  int* host_flag;              // host-visible error flag of the device (may be null)
   uint32_t gu_bytes, gus_bytes, dn_bytes;  // one expert's packed gate/up, its scales, packed down
   uint32_t gu_total, gus_total, dn_total;  // whole tensors (buffer resource sizes)
   uint32_t dsc_total;                      // down scales tensor
@@ -141,6 +145,7 @@ struct DecPrologue {
   __attribute__((aligned(8))) int8_t rowpos[kSlots][kRows];  // row of (u, token), -1 if none
   __attribute__((aligned(16))) float roww[kSlots][kRows];    // routing weight of (u, token), 0 if none
   int n_unique;
+  int bad;  // a bounded wait of this workgroup gave up: its outputs are written as NaN
 };
 
 // ---------------------------------------------------------------------------
@@ -192,6 +197,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, c
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int S = a.S;
   if (tid < 32) P.bm[tid] = 0u;
+  if (tid == 0) P.bad = 0;
   if (tid < kSlots) P.tm[tid] = 0u;
   (&P.rowpos[0][0])[tid] = -1;  // kSlots * kRows == kThreads entries
   (&P.roww[0][0])[tid] = 0.f;
@@ -295,9 +301,13 @@ struct GuShape {
   static constexpr int KPM = 4 * kWaves * KBW;  // packed rows of x staged (>= H/8)
 };
 
-constexpr int kGuScales = 4;  // scale groups a wave's k blocks can span (group size >= 4 k blocks)
+// Scale groups a wave's k blocks can span: KBW = 11 k blocks of 32 meet at
+// most ceil(10 / 2) + 1 = 6 groups of 64 and 4 groups of 128 or more.  A
+// fixed count of loads per item keeps every wait count exact; the loads past
+// the wave's own group count read past the resource (zeros, no access).
+constexpr int kGuScales = 6;
 
-// One item in flight: this lane's words and the scales of the (at most four)
+// One item in flight: this lane's words and the scales of the (at most six)
 // groups its wave's k blocks fall in.
 template <int KBW>
 struct GuBuf {
@@ -324,6 +334,7 @@ __device__ __forceinline__ void gu_load(const DecArgs& a, int uexp_v, int item, 
   const int col = (lr < 8 ? 0 : a.I) + kCols * c + 4 * (lr & 7);
   const int kb0 = wave * KBW;
   const int g0 = kb0 >> a.gsh;
+  const int nsc = ((kb0 + KBW - 1) >> a.gsh) - g0 + 1;  // groups this wave's k blocks meet
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.gu_scales, real ? a.gus_total : 0u);
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.gu_packed, real ? a.gu_total : 0u);
   const int so_s = real ? e * (int)a.gus_bytes : 0, so_w = real ? e * (int)a.gu_bytes : 0;
@@ -331,7 +342,8 @@ __device__ __forceinline__ void gu_load(const DecArgs& a, int uexp_v, int item, 
 #pragma unroll
   for (int j = 0; j < kGuScales; ++j) {
     const int g = min(g0 + j, a.Ggu - 1);
-    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, (uint32_t)((g * twoI + col) * 2), so_s, 0);
+    const uint32_t off = j < nsc ? (uint32_t)((g * twoI + col) * 2) : kOob;
+    const u32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, off, so_s, 0);
     b.s[j] = make_uint2(v.x, v.y);
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -525,7 +537,9 @@ struct DnLds {
 struct DnLayout {
   size_t abias, dsc, total;
 };
-__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, size_t gu) {
+// nbmax: the most down blocks one workgroup owns (blk_lo spacing, rounded up).
+__host__ __device__ inline int dn_max_blocks(int units, int U, int G) { return (units * U + G - 1) / G; }
+__host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, size_t gu, int nbmax) {
   const size_t rows = (size_t)S + 1;
   size_t sact = align16(rows * I * 2);
   const size_t red = (size_t)2 * kWaves * kRows * 32 * 4 + (size_t)kPartSlots * kRows * 32 * 4;
@@ -534,7 +548,7 @@ __host__ __device__ inline DnLayout dn_layout(int S, int I, int Gd, size_t gu) {
   l.abias = sact;
   l.dsc = l.abias + align16(rows * (I / 8) * 4);
   if (l.dsc < gu) l.dsc = align16(gu);
-  l.total = l.dsc + align16((size_t)S * Gd * 64);  // a workgroup holds at most U <= S blocks
+  l.total = l.dsc + align16((size_t)nbmax * Gd * 64);
   return l;
 }
 
@@ -857,7 +871,7 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // the launch always ends).
 template <int CPT, bool BIAS>
 __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, const uint16_t* act, int c0, int c1,
-                                           int x0, int x1) {
+                                           int x0, int x1, int* bad) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(act, kActParity);
   uint32_t pending = 0u;
@@ -891,7 +905,10 @@ __device__ __forceinline__ void stage_acts(const DecArgs& a, const DnLds& L, con
     }
     if (__ballot(pending != 0u) == 0ull) break;
     if (++spins >= a.spin_limit) {
-      if ((threadIdx.x & (kWave - 1)) == 0) atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+      if ((threadIdx.x & (kWave - 1)) == 0) {
+        report_timeout(a.status, a.host_flag);
+        *bad = 1;
+      }
       break;
     }
     __builtin_amdgcn_s_sleep(2);
@@ -1041,7 +1058,8 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
   DnBlockF<NT> xb[BPW];
   if constexpr (MODE > 0) dn_blocks_valu<BPW, NT>(a, P, L, epos_v, tm_v, U, dp, xb);
-  stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1);  // waits for every load of the wave
+  int* bad = const_cast<int*>(&P.bad);
+  stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1, bad);  // waits for every load of the wave
   lds_barrier();
 
   float accv[2][NT][2];
@@ -1122,7 +1140,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     const __amdgpu_buffer_rsrc_t pr = buffer_rsrc(part, kPartParity);
     if (slot > 0) {
       // a partial sum for the unit's first workgroup: 16 bytes per (token, 4 columns)
-      if (writer) L.pbuf[wt * 32 + wc] = s;
+      if (writer) L.pbuf[wt * 32 + wc] = P.bad ? __uint_as_float(0x7fc00000u) : s;
       lds_barrier();
       if (tid < a.M * 8) {
         const int t = tid >> 3, q = tid & 7;
@@ -1145,13 +1163,17 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
         const int sl = 1 + tid / (a.M * 8), r = tid - (sl - 1) * a.M * 8;
         const int t = r >> 3, q = r & 7;
         const uint32_t off = (uint32_t)((((d * kPartSlots + sl) * kRows + t) * kUnitCols + 4 * q) * 4);
+        // with fewer blocks than workgroups some workgroups between the
+        // unit's first and last hold none and publish nothing: a zero term
+        const bool held = blk_lo(wf + sl, NB, G) < blk_lo(wf + sl + 1, NB, G);
         int spins = 0;
-        u32x4_t v;
-        while (true) {
+        u32x4_t v = {~0u, ~0u, ~0u, ~0u};  // inverted zeros
+        while (held) {
           v = __builtin_amdgcn_raw_buffer_load_b128(pr, off, 0, kCpolAgent);
           if (v.x != 0u && v.y != 0u && v.z != 0u && v.w != 0u) break;
           if (++spins >= a.spin_limit) {
-            atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+            report_timeout(a.status, a.host_flag);
+            *bad = 1;
             break;
           }
           __builtin_amdgcn_s_sleep(2);
@@ -1167,6 +1189,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     }
     if (writer) {
       if (!a.overwrite) s += bf16_to_f32((old[p] >> (16 * (wc & 1))) & 0xffffu);
+      if (P.bad) s = __uint_as_float(0x7fc00000u);  // never a wrong finite value
       a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_bf16(s);
     }
   }
@@ -1272,7 +1295,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   if (n_my > 0) stage_x<KBW>(a, L, xr);
   // the down scales of every block of the workgroup, ahead of the weights
   // (older than every weight load, they leave the weight waits exact)
-  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, gu_lds_bytes<KBW>());
+  const DnLayout ly = dn_layout(a.S, a.I, a.Gd, gu_lds_bytes<KBW>(), dn_max_blocks(a.units, a.S, G));
   dsc_load(a, (uint32_t*)(dyn_lds + ly.dsc), uexp_v, U, blo, bhi - blo);
   DnPlan dp;
   dp.blo = blo;
@@ -1300,27 +1323,50 @@ constexpr size_t kMaxDynLds = 160 * 1024 - 8 * 1024;  // room for the static pro
 
 int kbw_for(int H) { return H <= 512 ? 2 : 11; }
 
-size_t lds_for(int kbw, int S, int I, int Gd, int bpw) {
-  (void)bpw;
+size_t lds_for(int kbw, int S, int I, int Gd, int units, int G) {
   const size_t g = kbw == 2 ? gu_lds_bytes<2>() : gu_lds_bytes<11>();
-  return dn_layout(S, I, Gd, g).total;
+  return dn_layout(S, I, Gd, g, dn_max_blocks(units, S, G)).total;
 }
 
-template <int KBW, int MODE, int BPW, int CPT>
-int launch_variant(const DecArgs& k, size_t lds, int grid, hipStream_t stream) {
-  static bool attr_set[64];
+// Residency of a kernel variant with `lds` bytes of dynamic LDS: the
+// exchange between workgroups assumes that all workgroups of a launch (one
+// per CU) run at the same time, so a variant is used only when the
+// occupancy calculator puts at least one workgroup on every CU.  The
+// dynamic-LDS limit is raised once per device and kernel first.  Results are
+// cached per (device, kernel, LDS bytes).
+struct ResEntry {
+  int dev;
+  const void* fn;
+  size_t lds;
+  int blocks;
+};
+std::mutex g_res_mu;
+std::vector<ResEntry> g_res;
+
+int blocks_per_cu(const void* fn, size_t lds, int* blocks) {
   int dev = 0;
-  hipError_t e0 = hipGetDevice(&dev);
-  if (e0 != hipSuccess) return hip_fail(e0, "hipGetDevice");
-  if (dev >= 0 && dev < 64 && !attr_set[dev]) {
-    e0 = hipFuncSetAttribute((const void*)moe_decode_kernel<KBW, MODE, BPW, CPT>,
-                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
-    if (e0 != hipSuccess) return hip_fail(e0, "hipFuncSetAttribute(max dynamic LDS)");
-    attr_set[dev] = true;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lk(g_res_mu);
+  bool attr = false;
+  for (const ResEntry& r : g_res) {
+    if (r.dev == dev && r.fn == fn) {
+      attr = true;
+      if (r.lds == lds) {
+        *blocks = r.blocks;
+        return GI_OK;
+      }
+    }
   }
-  hipLaunchKernelGGL((moe_decode_kernel<KBW, MODE, BPW, CPT>), dim3(grid), dim3(kThreads), lds, stream, k);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");
+  if (!attr) {
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxDynLds);
+    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute(max dynamic LDS)");
+  }
+  int n = 0;
+  e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds);
+  if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
+  g_res.push_back(ResEntry{dev, fn, lds, n});
+  *blocks = n;
   return GI_OK;
 }
 
@@ -1346,12 +1392,14 @@ bool decode_plan(int M, int S, int H, int I, int cus, DecodePlan& pl) {
 }
 
 template <int KBW>
-int launch_plan(const DecArgs& k, const DecodePlan& pl, hipStream_t stream) {
-  const size_t lds = lds_for(KBW, k.S, k.I, k.Gd, pl.bpw);
-  if (pl.mode == 1 && pl.bpw == 4 && pl.cpt == 2) return launch_variant<KBW, 1, 4, 2>(k, lds, pl.grid, stream);
-  if (pl.mode == 1) return launch_variant<KBW, 1, 8, kMaxStage>(k, lds, pl.grid, stream);
-  if (pl.mode == 2) return launch_variant<KBW, 2, 8, kMaxStage>(k, lds, pl.grid, stream);
-  return launch_variant<KBW, 0, 8, kMaxStage>(k, lds, pl.grid, stream);
+const void* plan_kernel(const DecodePlan& pl) {
+  if (pl.mode == 1 && pl.bpw == 4 && pl.cpt == 2) return (const void*)moe_decode_kernel<KBW, 1, 4, 2>;
+  if (pl.mode == 1) return (const void*)moe_decode_kernel<KBW, 1, 8, kMaxStage>;
+  if (pl.mode == 2) return (const void*)moe_decode_kernel<KBW, 2, 8, kMaxStage>;
+  return (const void*)moe_decode_kernel<KBW, 0, 8, kMaxStage>;
+}
+const void* decode_kernel(int kbw, const DecodePlan& pl) {
+  return kbw == 2 ? plan_kernel<2>(pl) : plan_kernel<11>(pl);
 }
 
 int log2_exact(int v) {
@@ -1371,9 +1419,9 @@ int moe_decode_rows_per_launch(int top_k) {
 bool moe_decode_supported(const MoeHostArgs& h) {
   if (h.H % 32 || h.I % 32 || h.H > kMaxUnits * kUnitCols || h.I > kMaxI) return false;
   if (h.gs % 32 || log2_exact(h.gs / 32) < 0) return false;
-  // a scale group covers at least 4 k blocks: a wave's gate/up blocks span at
-  // most four groups, its down blocks (at most three) at most two
-  if (log2_exact(h.gs / 32) < 2) return false;
+  // a scale group covers at least 2 k blocks: a wave's gate/up blocks span at
+  // most six groups, its down blocks (at most three) at most two
+  if (log2_exact(h.gs / 32) < 1) return false;
   if ((((uintptr_t)h.gu_scales) | ((uintptr_t)h.d_scales) | ((uintptr_t)h.out)) % 16) return false;
   if (h.top_k > kSlots || (h.logits && h.top_k > 64) || h.E > kRouteMaxExperts) return false;
   // whole tensors addressed with 32-bit buffer offsets
@@ -1386,7 +1434,14 @@ bool moe_decode_supported(const MoeHostArgs& h) {
   DecodePlan pl;
   if (!decode_plan(r1, S, h.H, h.I, device_cu_count(), pl)) return false;
   if (pl.cpt > kMaxStage || S * (h.I / 8) > kMaxStage * kThreads) return false;
-  return lds_for(kbw_for(h.H), S, h.I, h.Gd, pl.bpw) <= kMaxDynLds;
+  // the down scales of a workgroup's blocks: at most kScaleLoads 16-byte chunks per thread
+  if (dn_max_blocks(h.H / kUnitCols, S, pl.grid) * h.Gd * 4 > kScaleLoads * kThreads) return false;
+  const size_t lds = lds_for(kbw_for(h.H), S, h.I, h.Gd, h.H / kUnitCols, pl.grid);
+  if (lds > kMaxDynLds) return false;
+  // every workgroup of the grid (one per CU) must be resident at once
+  int blocks = 0;
+  if (blocks_per_cu(decode_kernel(kbw_for(h.H), pl), lds, &blocks) != GI_OK || blocks < 1) return false;
+  return true;
 }
 
 size_t moe_decode_state_bytes() { return (size_t)kEpochSlots * 8 + 2 * kActParity + 2 * kPartParity; }
@@ -1421,6 +1476,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   k.overwrite = h.overwrite;
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
   k.status = status;
+  k.host_flag = device_error_flag();
   k.epochs = (unsigned long long*)state;
   k.act = (uint16_t*)((char*)state + (size_t)kEpochSlots * 8);
   k.part = (float*)((char*)state + (size_t)kEpochSlots * 8 + 2 * kActParity);
@@ -1443,8 +1499,15 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
                         : nullptr;
     k.out_idx = h.out_idx ? h.out_idx + (size_t)r0 * h.top_k : nullptr;
     k.out_w = h.out_w ? (uint16_t*)h.out_w + (size_t)r0 * h.top_k : nullptr;
-    const int st = kbw == 2 ? launch_plan<2>(k, pl, h.stream) : launch_plan<11>(k, pl, h.stream);
+    const size_t lds = lds_for(kbw, k.S, k.I, k.Gd, k.units, pl.grid);
+    const void* fn = decode_kernel(kbw, pl);
+    int blocks = 0;
+    int st = blocks_per_cu(fn, lds, &blocks);  // also raises the kernel's dynamic-LDS limit
     if (st != GI_OK) return st;
+    if (blocks < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: a workgroup does not fit on a CU");
+    void* args[] = {(void*)&k};
+    const hipError_t e = hipLaunchKernel(fn, dim3(pl.grid), dim3(kThreads), args, lds, h.stream);
+    if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");
   }
   return GI_OK;
 }

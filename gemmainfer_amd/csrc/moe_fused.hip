@@ -72,8 +72,10 @@ struct Args {
   uint16_t* out;
   float* part;      // [S][Tg][H] fp32 partials
   uint32_t part_bytes;
-  int* ctr;         // grid barrier: [0] launch epoch, [(1 + p) * kCtrStride] arrivals of parity p
+  int* ctr;         // grid barrier: [0] launch epoch, [(1 + p) * kCtrStride] arrivals of parity p,
+                    // [3 * kCtrStride] the last epoch whose barrier wait timed out
   int* status;
+  int* host_flag;   // host-visible error flag of the device (may be null)
   int idx_is64, w_dtype, logits_dtype;
   int M, H, I, E, top_k, gs, Ggu, Gd, S, Tg;
   int overwrite, spin_limit;
@@ -493,7 +495,7 @@ __device__ void run_task(const Args& a, Prologue& P, int u, int c, const TaskLds
 // reduction of the partials into out
 // ---------------------------------------------------------------------------
 template <int T>
-__device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratch) {
+__device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratch, bool bad) {
   constexpr int W = T / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int HQ = a.H >> 2, total = a.M * HQ;
@@ -561,6 +563,8 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
         sum.z += bf16lo(old.y);
         sum.w += bf16hi(old.y);
       }
+      if (bad) sum = make_float4(__uint_as_float(0x7fc00000u), __uint_as_float(0x7fc00000u),
+                                 __uint_as_float(0x7fc00000u), __uint_as_float(0x7fc00000u));
       *o = make_uint2((uint32_t)f32_to_bf16(sum.x) | ((uint32_t)f32_to_bf16(sum.y) << 16),
                       (uint32_t)f32_to_bf16(sum.z) | ((uint32_t)f32_to_bf16(sum.w) << 16));
     }
@@ -573,6 +577,8 @@ __device__ void reduce_partials(const Args& a, const Prologue& P, float4* scratc
 template <int T>
 __device__ __forceinline__ void finish_layer(const Args& a, const Prologue& P, int my_gen, float4* scratch) {
   const int tid = threadIdx.x;
+  __shared__ int s_bad;  // the wait gave up: this workgroup's outputs are written as NaN
+  if (tid == 0) s_bad = 0;
   // Grid-wide barrier (every partial of every task is written).  Launches
   // alternate between two arrival counters by the parity of the launch epoch
   // (read above, before this workgroup can arrive, so every workgroup of a
@@ -589,17 +595,23 @@ __device__ __forceinline__ void finish_layer(const Args& a, const Prologue& P, i
       store_relaxed(a.ctr + (1 + ((my_gen + 1) & 1)) * kCtrStride, 0);
       store_relaxed(a.ctr, my_gen + 1);
     } else {
+      // A waiter that gives up marks this launch's epoch so the others stop
+      // waiting too; the mark names the epoch, so a later launch (another
+      // epoch) is not cut short by it.
+      int* gave_up = a.ctr + 3 * kCtrStride;
       int spins = 0;
       while (load_relaxed(a.ctr) == my_gen) {
-        if (++spins >= a.spin_limit || load_relaxed(a.status) != 0) {
-          atomicOr(a.status, GI_DEVICE_SPIN_TIMEOUT);
+        if (++spins >= a.spin_limit || load_relaxed(gave_up) == my_gen + 1) {
+          store_relaxed(gave_up, my_gen + 1);
+          report_timeout(a.status, a.host_flag);
+          s_bad = 1;
           break;
         }
       }
     }
   }
   __syncthreads();
-  reduce_partials<T>(a, P, scratch);
+  reduce_partials<T>(a, P, scratch, s_bad != 0);
 }
 
 template <int CG, int NT, int JGM, int CPR>
@@ -968,10 +980,14 @@ WsLayout ws_layout(int S, int H, int I, int cg) {
   L.status = 0;
   L.state = kAlign;
   L.ctr = L.state + round_up(moe_decode_state_bytes());
-  L.part = L.ctr + round_up((size_t)3 * kCtrStride * sizeof(int));
+  L.part = L.ctr + round_up((size_t)4 * kCtrStride * sizeof(int));
   L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
   return L;
 }
+
+// Start of the prefill buffers: past the status word, the decode state and
+// the barrier counters (the partial slabs are scratch of one launch).
+size_t prefill_base(int H, int I) { return ws_layout(1, H, I, kTaskCols).part; }
 
 struct OccEntry {
   int device;
@@ -1115,9 +1131,9 @@ size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
   // take the grouped-GEMM prefill path instead
   const WsLayout L = ws_layout(r * top_k, H, I, kTaskCols);
   if (rows < kPrefillMinRows) return L.total;
-  // the prefill buffers follow the status word and the decode state, which
-  // later decode calls on the same workspace still need
-  const size_t pf = L.ctr + moe_prefill_workspace_bytes(rows, top_k, H, I, E);
+  // the prefill buffers follow the status word, the decode state and the
+  // barrier counters, which later calls on the same workspace still need
+  const size_t pf = prefill_base(H, I) + moe_prefill_workspace_bytes(rows, top_k, H, I, E);
   return pf > L.total ? pf : L.total;
 }
 
@@ -1138,7 +1154,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
   if (((uintptr_t)h.workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
   if (moe_prefill_supported(h)) {
-    const size_t base = ws_layout(1, h.H, h.I, kTaskCols).ctr;  // past the status word and decode state
+    const size_t base = prefill_base(h.H, h.I);
     return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base);
   }
   if (moe_decode_supported(h)) {
@@ -1171,6 +1187,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
   k.Gd = h.Gd;
   k.overwrite = h.overwrite;
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
+  k.host_flag = device_error_flag();
 
   const size_t idx_es = h.idx_is64 ? 8 : 4;
   const size_t w_es = h.w_dtype == GI_DTYPE_FP32 ? 4 : 2;

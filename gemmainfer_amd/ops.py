@@ -84,12 +84,19 @@ class _WorkspacePool:
 _WS = _WorkspacePool()
 
 
+def _device_index(device) -> int:
+    if device is None:
+        return torch.cuda.current_device()
+    d = torch.device(device)
+    return torch.cuda.current_device() if d.index is None else d.index
+
+
 def workspace_status(device=None) -> int:
-    """OR of the device status words of every MoE workspace on ``device``,
-    clearing them (synchronises).  0 means no kernel reported an error
-    (``gemmainfer_amd._lib.DEVICE_SPIN_TIMEOUT`` = a bounded wait gave up)."""
-    device = torch.device("cuda", torch.cuda.current_device() if device is None else
-                          torch.device(device).index or 0)
+    """OR of the device status words of every MoE workspace on ``device`` and
+    of the device's host-visible error flag, clearing them (synchronises).
+    0 means no kernel reported an error (``gemmainfer_amd._lib.DEVICE_SPIN_TIMEOUT``
+    = a bounded wait gave up)."""
+    device = torch.device("cuda", _device_index(device))
     lib = L.load()
     out = 0
     for buf in _WS.all("moe", device):
@@ -97,7 +104,24 @@ def workspace_status(device=None) -> int:
         L.check(lib.gi_workspace_status(_ptr(buf), buf.numel(), ctypes.byref(st), _stream(device)),
                 "workspace_status")
         out |= st.value
-    return out
+    flags = lib.gi_device_error_flags(device.index, 1)
+    return out | max(flags, 0)
+
+
+def raise_pending_device_error(device=None) -> None:
+    """Raise GIError(GI_ERR_DEVICE) if a kernel on ``device`` reported an error
+    since the last check.  Reads a host-memory flag the kernels write: no
+    synchronisation.  The MoE entry points call it before launching, so a
+    failure surfaces at the next call (the failed call's outputs that could
+    not be completed hold NaN).  The device's MoE workspaces are re-zeroed."""
+    idx = _device_index(device)
+    flags = L.load().gi_device_error_flags(idx, 1)
+    if flags > 0:
+        for buf in _WS.all("moe", torch.device("cuda", idx)):
+            buf.zero_()
+        raise L.GIError(L.GI_ERR_DEVICE,
+                        f"a MoE kernel on cuda:{idx} reported device error bits {flags:#x} "
+                        "(a bounded wait gave up; the outputs it could not complete hold NaN)")
 
 
 # ---------------------------------------------------------------------------
@@ -146,6 +170,7 @@ def fused_batched_moe(x, gate_up_packed, gate_up_scales, down_packed, down_scale
     """
     dev = _on_device(x, gate_up_packed, gate_up_scales, down_packed, down_scales,
                      expert_indices, expert_weights, out)
+    raise_pending_device_error(dev)
     _require_bf16(x, "fused_batched_moe")
     m, h, i, e = _moe_weight_shapes(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
     _require(isinstance(group_size, int) and group_size > 0 and group_size % 8 == 0,
@@ -193,6 +218,7 @@ def moe_layer(x, router_logits, gate_up_packed, gate_up_scales, down_packed, dow
     weights bf16 [M, top_k]).
     """
     dev = _on_device(x, router_logits, gate_up_packed, gate_up_scales, down_packed, down_scales)
+    raise_pending_device_error(dev)
     _require_bf16(x, "moe_layer")
     m, h, i, e = _moe_weight_shapes(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
     _require(router_logits.dim() == 2 and tuple(router_logits.shape) == (m, e),
@@ -268,6 +294,7 @@ def moe_layer_from_hidden(x, router_scale, gate_weight, gate_up_packed, gate_up_
     weights bf16 [M, top_k], logits bf16 [M, E]).
     """
     dev, m, h, e, rs = _router_inputs(x, router_scale, gate_weight, "moe_layer_from_hidden")
+    raise_pending_device_error(dev)
     _on_device(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
     m2, h2, i, e2 = _moe_weight_shapes(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
     _require(e2 == e, f"gate weight has {e} experts, the expert weights {e2}")

@@ -172,6 +172,17 @@ int gi_moe_layer_from_hidden(const void* x, int x_dtype, const void* router_scal
                              void* workspace, size_t workspace_bytes,
                              int spin_limit, void* stream);
 
+/* Device-side error bits (GI_DEVICE_*) that kernels on `device` have raised
+ * since the last clearing read, from a host-memory flag the kernels write
+ * directly: no synchronisation, no device work.  A bit is visible once the
+ * kernel that raised it has finished.  clear != 0 resets the flag.  A kernel
+ * whose bounded wait gave up writes NaN into the outputs it could not
+ * complete, so no wrong finite value is ever returned.  No counterpart in
+ * the reference, whose launches report no errors (csrc/marlin.cu:699-701):
+ * for callers that want such errors without a synchronisation of their own
+ * (gemmainfer_csrc checks it before each MoE call).                       */
+int gi_device_error_flags(int device, int clear);
+
 /* Copies the workspace's device status word to *host_status (synchronises
  * the stream) and clears it.  0 = no device-side error since last read.    */
 int gi_workspace_status(void* workspace, size_t workspace_bytes,
