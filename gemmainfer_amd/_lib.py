@@ -41,6 +41,10 @@ SIGNATURES = {
                                      c_void_p, c_int, c_void_p, c_int, c_void_p, c_int,
                                      c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                      c_void_p, c_size_t, c_int, c_void_p]),
+    "gi_fused_batched_moe_static": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p,
+                                            c_void_p, c_int, c_void_p, c_int, c_void_p, c_int,
+                                            c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
+                                            c_int, c_void_p]),
     "gi_moe_layer_from_logits": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p,
                                          c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
                                          c_void_p, c_void_p, c_void_p,

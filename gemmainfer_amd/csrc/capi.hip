@@ -45,9 +45,9 @@ std::mutex g_flag_mu;
 int* g_flags = nullptr;
 bool g_flags_failed = false;
 
-int* flags_host() {
+int* flags_host(bool allocate) {
   std::lock_guard<std::mutex> lk(g_flag_mu);
-  if (!g_flags && !g_flags_failed) {
+  if (allocate && !g_flags && !g_flags_failed) {
     void* p = nullptr;
     if (hipHostMalloc(&p, 64 * kFlagStride * sizeof(int),
                       hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) == hipSuccess && p) {
@@ -62,10 +62,10 @@ int* flags_host() {
 }
 }  // namespace
 
-int* device_error_flag() {
+int* device_error_flag(bool allocate) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  int* h = flags_host();
+  int* h = flags_host(allocate);
   if (!h) return nullptr;
   void* d = nullptr;
   if (hipHostGetDevicePointer(&d, h + dev * kFlagStride, 0) != hipSuccess) {
@@ -77,7 +77,7 @@ int* device_error_flag() {
 
 int read_device_error_flags(int device, int clear) {
   if (device < 0 || device >= 64) return fail(GI_ERR_INVALID_ARG, "device_error_flags: device index out of range");
-  int* h = flags_host();
+  int* h = flags_host(false);
   if (!h) return 0;
   volatile int* f = h + device * kFlagStride;
   const int v = *f;

@@ -20,8 +20,10 @@ int device_cu_count();
 // Device address of the current device's error flag: an int in host memory
 // mapped into the device, which kernels set when a bounded wait gives up
 // (null if the mapping is unavailable).  Read and cleared by
-// gi_device_error_flags without any device synchronisation.
-int* device_error_flag();
+// gi_device_error_flags without any device synchronisation.  The flags are
+// allocated (pinned host memory) on the first call with allocate = true;
+// allocate = false only returns them once they exist.
+int* device_error_flag(bool allocate = true);
 int read_device_error_flags(int device, int clear);
 
 // ---- fused MoE --------------------------------------------------------------
@@ -47,8 +49,13 @@ struct MoeHostArgs {
   size_t workspace_bytes;
   int spin_limit;
   hipStream_t stream;
+  int no_alloc;             // the caller cannot allocate: no pinned-memory set-up either
 };
 
+// Argument checks shared by every fused-MoE entry point (GI_OK or a failure code).
+int check_moe_args(const MoeHostArgs& h);
+// Byte offset of the decode kernel's state in a MoE workspace (the status word is at 0).
+size_t moe_decode_scratch_offset();
 // Largest number of token rows one fused launch handles (S = rows*top_k <= 256).
 int moe_rows_per_launch(int top_k);
 size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E);
@@ -58,6 +65,8 @@ bool moe_decode_supported(const MoeHostArgs& h);
 int moe_decode_rows_per_launch(int top_k);
 size_t moe_decode_state_bytes();        // epochs + exchange buffers: kept between calls
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status);
+// the same launches with the library's static per-GPU scratch (moe_static.hip)
+int launch_fused_moe_static(MoeHostArgs h);
 // prefill (moe_prefill.hip): sorted-by-expert grouped GEMM for M >= kPrefillMinRows
 constexpr int kPrefillMinRows = 64;
 bool moe_prefill_supported(const MoeHostArgs& h);

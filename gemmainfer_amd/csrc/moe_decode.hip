@@ -63,7 +63,6 @@
 // per-expert offset.
 
 #include <mutex>
-#include <vector>
 
 #include "../../include/gemmainfer_amd.h"
 #include "gi_common.h"
@@ -1340,8 +1339,10 @@ struct ResEntry {
   size_t lds;
   int blocks;
 };
+constexpr int kResCache = 256;
 std::mutex g_res_mu;
-std::vector<ResEntry> g_res;
+ResEntry g_res[kResCache];
+int g_res_n = 0;
 
 int blocks_per_cu(const void* fn, size_t lds, int* blocks) {
   int dev = 0;
@@ -1349,7 +1350,8 @@ int blocks_per_cu(const void* fn, size_t lds, int* blocks) {
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   std::lock_guard<std::mutex> lk(g_res_mu);
   bool attr = false;
-  for (const ResEntry& r : g_res) {
+  for (int i = 0; i < g_res_n; ++i) {
+    const ResEntry& r = g_res[i];
     if (r.dev == dev && r.fn == fn) {
       attr = true;
       if (r.lds == lds) {
@@ -1365,7 +1367,7 @@ int blocks_per_cu(const void* fn, size_t lds, int* blocks) {
   int n = 0;
   e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads, lds);
   if (e != hipSuccess) return hip_fail(e, "hipOccupancyMaxActiveBlocksPerMultiprocessor");
-  g_res.push_back(ResEntry{dev, fn, lds, n});
+  if (g_res_n < kResCache) g_res[g_res_n++] = ResEntry{dev, fn, lds, n};
   *blocks = n;
   return GI_OK;
 }
@@ -1476,7 +1478,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   k.overwrite = h.overwrite;
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
   k.status = status;
-  k.host_flag = device_error_flag();
+  k.host_flag = device_error_flag(!h.no_alloc);
   k.epochs = (unsigned long long*)state;
   k.act = (uint16_t*)((char*)state + (size_t)kEpochSlots * 8);
   k.part = (float*)((char*)state + (size_t)kEpochSlots * 8 + 2 * kActParity);

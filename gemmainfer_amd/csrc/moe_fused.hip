@@ -1120,6 +1120,10 @@ int check_moe_shapes(const MoeHostArgs& a) {
 
 }  // namespace
 
+int check_moe_args(const MoeHostArgs& h) { return check_moe_shapes(h); }
+
+size_t moe_decode_scratch_offset() { return ws_layout(1, 8, 8, kTaskCols).state; }
+
 int moe_rows_per_launch(int top_k) { return top_k > 0 ? kMaxSlots / top_k : 0; }
 
 size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {

@@ -127,6 +127,28 @@ int gi_fused_batched_moe(const void* x, int x_dtype,
                          void* workspace, size_t workspace_bytes,
                          int spin_limit, void* stream);
 
+/* gi_fused_batched_moe without a workspace argument: no counterpart in the
+ * reference (which allocates scratch per call, csrc/marlin.cu:638).  For
+ * callers that cannot allocate: code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The scratch is a static 2 MiB
+ * device array per GPU, held until the process ends (status word and the
+ * decode kernel's exchange state); the call itself allocates nothing (the
+ * first call on a device takes the array's address and zero-fills it with a
+ * kernel on `stream`; make that first call outside graph capture).  Every
+ * call on a GPU shares the array, so calls that overlap on one GPU (other
+ * streams, other host threads) race.  Serves the decode kernel's shapes
+ * (H, I multiples of 32, H <= 2816, I <= 768, group_size 64 * 2^k,
+ * top_k <= 64; any M as launches of up to 8 rows); other shapes return
+ * GI_ERR_WORKSPACE.  Results are bitwise those of gi_fused_batched_moe.   */
+int gi_fused_batched_moe_static(const void* x, int x_dtype,
+                                const int32_t* gu_packed, const void* gu_scales, int gu_groups,
+                                const int32_t* d_packed, const void* d_scales, int d_groups,
+                                const void* idx, int idx_dtype,
+                                const void* w, int w_dtype,
+                                void* out,
+                                int M, int H, int I, int E, int top_k, int group_size,
+                                int spin_limit, void* stream);
+
 /* Router + fused MoE: logits [M, E] (bf16/fp32) are routed as
  * gi_moe_route_topk_softmax does (weights rounded to bf16), out[M, H] is
  * OVERWRITTEN with the MoE output, and out_idx/out_w (may be NULL) receive

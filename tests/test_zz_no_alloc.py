@@ -1,0 +1,67 @@
+"""gi_fused_batched_moe_static (no workspace argument, static per-GPU scratch)
+against gi_fused_batched_moe (caller workspace), both through the C ABI.
+
+Two calls in a row, the second with fewer rows, each compared bitwise with
+the workspace entry point on the same inputs (the same kernels run, and their
+sums have a fixed order); then a shape the static scratch cannot serve is
+rejected with GI_ERR_WORKSPACE.
+"""
+import ctypes
+
+import pytest
+import torch
+
+from gemmainfer_amd import _lib as L
+from gemmainfer_amd import synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+E, H, I, TOP_K = 128, 2816, 704, 8
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _args(W, x, idx, w, out, m, gs):
+    return (_p(x), L.DTYPE_BF16, _p(W["gate_up_packed"]), _p(W["gate_up_scales"]), W["gate_up_scales"].shape[1],
+            _p(W["down_packed"]), _p(W["down_scales"]), W["down_scales"].shape[1], _p(idx), L.DTYPE_INT32,
+            _p(w), L.DTYPE_BF16, _p(out), m, H, I, E, TOP_K, gs)
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+def test_static_scratch_matches_workspace_entry_point(gs):
+    lib = L.load()
+    W = synth.device_moe_weights(E, H, I, gs, DEV, seed=800 + gs)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws = torch.zeros(lib.gi_fused_moe_workspace_bytes(8, TOP_K, H, I, E), dtype=torch.uint8, device=DEV)
+    for call, (m, noise) in enumerate(((7, 0.5), (1, 0.0))):
+        print(f"static scratch gs={gs} call={call} m={m}", flush=True)
+        x = synth.activations(m, H, seed=810 + m).to(DEV)
+        logits = synth.router_logits(m, E, seed=810 + m, verify_noise=noise)
+        top, idx = torch.topk(logits, TOP_K, dim=-1)
+        w = torch.softmax(top, dim=-1, dtype=torch.float32).to(torch.bfloat16).to(DEV)
+        idx = idx.to(torch.int32).to(DEV)
+        out_in = (torch.randn(m, H) * 0.1).to(torch.bfloat16).to(DEV)   # both accumulate into out
+        ref = out_in.clone()
+        got = out_in.clone()
+        L.check(lib.gi_fused_batched_moe(*_args(W, x, idx, w, ref, m, gs), _p(ws), ws.numel(), 0, stream),
+                "gi_fused_batched_moe")
+        L.check(lib.gi_fused_batched_moe_static(*_args(W, x, idx, w, got, m, gs), 0, stream),
+                "gi_fused_batched_moe_static")
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got, ref), f"call {call} (m={m}): static-scratch output differs"
+    assert lib.gi_device_error_flags(torch.cuda.current_device(), 0) == 0
+
+
+def test_static_scratch_rejects_shapes_it_cannot_serve():
+    lib = L.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    buf = torch.zeros(16, dtype=torch.int32, device=DEV)
+    p = _p(buf)
+    # group size 24: the general fused path, whose partial slabs need a caller workspace
+    st = lib.gi_fused_batched_moe_static(p, L.DTYPE_BF16, p, p, 11, p, p, 30, p, L.DTYPE_INT32, p, L.DTYPE_BF16,
+                                         p, 1, 256, 128, 8, 2, 24, 0, stream)
+    assert st == L.GI_ERR_WORKSPACE
+    assert "caller workspace" in lib.gi_last_error().decode()
