@@ -28,7 +28,8 @@ DTYPE_INT64 = 4
 
 DEVICE_SPIN_TIMEOUT = 1
 
-# name -> (restype, argtypes); mirrors include/gemmainfer_amd.h exactly.
+# name -> (restype, argtypes); mirrors include/gemmainfer_amd.h and
+# include/gemmainfer_amd_probe.h exactly.
 SIGNATURES = {
     "gi_last_error": (ctypes.c_char_p, []),
     "gi_abi_version": (c_int, []),
@@ -76,6 +77,8 @@ SIGNATURES = {
     "gi_softcap_inplace": (c_int, [c_void_p, c_int, c_int64, c_float, c_void_p]),
     "gi_rmsnorm": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int64, c_int, c_float,
                            c_int, c_void_p]),
+    "gi_probe_stream_read": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_void_p]),
+    "gi_probe_decode_timeline": (c_int, [c_void_p, c_size_t]),
     "gi_rope_inplace": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
                                 c_int, c_int, c_int, c_int, c_int,
                                 c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,

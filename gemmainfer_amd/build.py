@@ -4,6 +4,11 @@ Usage: ``python -m gemmainfer_amd.build`` (or ``build()`` from Python).  Each
 ``csrc/*.hip`` file compiles to an object in parallel; the objects link into
 ``gemmainfer_amd/lib/libgemmainfer_amd.so``.  No GPU is needed: hipcc cross
 compiles for the MI355X (gfx950) here.
+
+``python -m gemmainfer_amd.build --timeline`` builds the measurement variant
+``lib/libgemmainfer_amd_timeline.so`` (the same sources with -DGI_TIMELINE:
+the decode kernel records per-workgroup phase stamps, see
+include/gemmainfer_amd_probe.h); the product library never contains it.
 """
 from __future__ import annotations
 
@@ -17,6 +22,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "lib"
 LIBNAME = "libgemmainfer_amd.so"
+TIMELINE_LIBNAME = "libgemmainfer_amd_timeline.so"
 OBJDIR = PKG / "_build"
 ARCH = "gfx950"
 
@@ -38,13 +44,14 @@ COMMON_FLAGS = [
 ]
 
 
-def lib_path() -> Path:
-    return LIBDIR / LIBNAME
+def lib_path(timeline: bool = False) -> Path:
+    return LIBDIR / (TIMELINE_LIBNAME if timeline else LIBNAME)
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJDIR / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, timeline: bool = False) -> Path:
+    objdir = OBJDIR.with_name(OBJDIR.name + "_timeline") if timeline else OBJDIR
+    obj = objdir / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *(["-DGI_TIMELINE"] if timeline else []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (res.stdout + res.stderr).splitlines()
                     if "packed-fp32-ops" not in l)
@@ -55,23 +62,24 @@ def _compile(src: Path) -> Path:
     return obj
 
 
-def build(verbose: bool = True) -> Path:
+def build(verbose: bool = True, timeline: bool = False) -> Path:
     """Compile every csrc/*.hip and link the shared library; returns its path."""
-    OBJDIR.mkdir(exist_ok=True)
+    (OBJDIR.with_name(OBJDIR.name + "_timeline") if timeline else OBJDIR).mkdir(exist_ok=True)
     LIBDIR.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIBDIR / (LIBNAME + ".tmp")
+        objs = list(ex.map(lambda src: _compile(src, timeline), sources))
+    out = lib_path(timeline)
+    tmp = out.with_name(out.name + ".tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, lib_path())
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {lib_path()} from {len(sources)} sources")
-    return lib_path()
+        print(f"built {out} from {len(sources)} sources")
+    return out
 
 
 if __name__ == "__main__":
-    build()
+    build(timeline="--timeline" in sys.argv[1:])

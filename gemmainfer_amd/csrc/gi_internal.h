@@ -65,6 +65,8 @@ bool moe_decode_supported(const MoeHostArgs& h);
 int moe_decode_rows_per_launch(int top_k);
 size_t moe_decode_state_bytes();        // epochs + exchange buffers: kept between calls
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status);
+// timeline builds (-DGI_TIMELINE): per-workgroup phase stamps of every decode launch
+int set_decode_timeline(void* buf, size_t bytes);
 // the same launches with the library's static per-GPU scratch (moe_static.hip)
 int launch_fused_moe_static(MoeHostArgs h);
 // prefill (moe_prefill.hip): sorted-by-expert grouped GEMM for M >= kPrefillMinRows

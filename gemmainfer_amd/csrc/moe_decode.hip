@@ -104,6 +104,33 @@ __host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(siz
 // Orders LDS accesses of this wave before the next instruction (no vmcnt wait).
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Phase stamps (built with -DGI_TIMELINE only): thread 0 keeps the constant
+// 100 MHz clock (s_memrealtime) at each phase end in LDS; the workgroup
+// writes them out at its end.  Slots: 0 start, 1 routing and tables, 2 x in
+// LDS, 3 weight loads issued, 4 gate/up items done, 5 activations staged,
+// 6 down products, 7 wave sums, 8 output / partial sums, 9 end; 14 and 15
+// hold the workgroup's gate/up item and down block counts.
+constexpr int kStamps = 16;
+#ifdef GI_TIMELINE
+__shared__ unsigned long long tl_lds[kStamps];
+__device__ __forceinline__ void tl_init() {
+  if (threadIdx.x < kStamps) tl_lds[threadIdx.x] = 0ull;
+}
+__device__ __forceinline__ void tl_stamp(int i) {
+  if (threadIdx.x == 0) tl_lds[i] = __builtin_amdgcn_s_memrealtime();
+}
+__device__ __forceinline__ void tl_value(int i, unsigned long long v) {
+  if (threadIdx.x == 0) tl_lds[i] = v;
+}
+__device__ __forceinline__ void tl_flush(unsigned long long* dst) {
+  lds_barrier();
+  if (dst && threadIdx.x < kStamps) dst[blockIdx.x * kStamps + threadIdx.x] = tl_lds[threadIdx.x];
+}
+#define GI_STAMP(i) tl_stamp(i)
+#else
+#define GI_STAMP(i) ((void)0)
+#endif
+
 struct DecArgs {
   const uint16_t* x;
   const int32_t* gu_packed;
@@ -123,6 +150,7 @@ struct DecArgs {
   float* part;                 // [2][units][kPartSlots][kRows][32] partial sums, inverted bits
   int* status;
   int* host_flag;              // host-visible error flag of the device (may be null)
+  unsigned long long* timeline;  // [G][kStamps] per-workgroup stamps (timeline builds only; else null)
   uint32_t gu_bytes, gus_bytes, dn_bytes;  // one expert's packed gate/up, its scales, packed down
   uint32_t gu_total, gus_total, dn_total;  // whole tensors (buffer resource sizes)
   uint32_t dsc_total;                      // down scales tensor
@@ -1060,6 +1088,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   int* bad = const_cast<int*>(&P.bad);
   stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1, bad);  // waits for every load of the wave
   lds_barrier();
+  GI_STAMP(5);
 
   float accv[2][NT][2];
   f32x4_t accm[2][2];
@@ -1098,6 +1127,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   }
   // sums over the waves, fixed order (the per-wave sums alias the staged rows)
   lds_barrier();
+  GI_STAMP(6);
 #pragma unroll
   for (int p = 0; p < 2; ++p) {
     float* red = L.red + (size_t)p * kWaves * kRows * 32;
@@ -1126,6 +1156,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     }
   }
   lds_barrier();
+  GI_STAMP(7);
   for (int p = 0; p < n_units; ++p) {
     const int d = d_first + p;
     const int wf = blk_owner(d * U, NB, G), wl = blk_owner(d * U + U - 1, NB, G);
@@ -1192,6 +1223,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
       a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_bf16(s);
     }
   }
+  GI_STAMP(8);
 }
 
 // The workgroup's gate/up items (it0, it0 + G, ...) and the issue of its down
@@ -1209,6 +1241,7 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
   gu_load<KBW>(a, uexp_v, it0, n_items, b0);
   if constexpr (NI >= 2) gu_load<KBW>(a, uexp_v, it0 + G, n_items, b1);
   if constexpr (NI <= 2) dn_load<BPW>(a, uexp_v, U, dp, dw);
+  GI_STAMP(3);
   if constexpr (NI == 1) {
     gu_item<KBW>(a, P, it0, b0, L, act);
   } else if constexpr (NI == 2) {
@@ -1218,6 +1251,7 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
     gu_items<KBW, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
   }
+  GI_STAMP(4);
 }
 
 // ---------------------------------------------------------------------------
@@ -1260,6 +1294,10 @@ template <int KBW, int MODE, int BPW, int CPT>
 __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   __shared__ DecPrologue P;
   extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
+#ifdef GI_TIMELINE
+  tl_init();
+#endif
+  GI_STAMP(0);
   XRegs<KBW> xr;
   u32x2_t epr;
   if (a.E <= 2 * kWave) epr = dec_start<KBW, 2>(a, P, xr);
@@ -1271,6 +1309,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   float* part = a.part + (size_t)parity * (kPartParity / 4);
   const int U = uniform(P.n_unique);
   const int b = blockIdx.x, G = gridDim.x;
+  GI_STAMP(1);
   if (U == 0) {
     // no valid slot: a layer call still owns (overwrites) out
     if (a.overwrite)
@@ -1292,6 +1331,11 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
   // x into LDS first: its registers are free before the word buffers fill
   if (n_my > 0) stage_x<KBW>(a, L, xr);
+  GI_STAMP(2);
+#ifdef GI_TIMELINE
+  tl_value(14, (unsigned long long)n_my);
+  tl_value(15, (unsigned long long)(bhi - blo));
+#endif
   // the down scales of every block of the workgroup, ahead of the weights
   // (older than every weight load, they leave the weight waits exact)
   const DnLayout ly = dn_layout(a.S, a.I, a.Gd, gu_lds_bytes<KBW>(), dn_max_blocks(a.units, a.S, G));
@@ -1312,6 +1356,10 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   if (bhi > blo)
     down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4>(a, P, dyn_lds, ly, U, uexp_v, act, part, blo, bhi, dp, dw);
   dec_end(a, P, ep, parity);
+#ifdef GI_TIMELINE
+  GI_STAMP(9);
+  tl_flush(a.timeline);
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -1410,7 +1458,36 @@ int log2_exact(int v) {
   return (1 << s) == v ? s : -1;
 }
 
+// Timeline builds: the caller's stamp buffer, used in slots of kEpochSlots
+// workgroups x kStamps words, one slot per launch in rotation.
+std::mutex g_tl_mu;
+unsigned long long* g_tl_buf = nullptr;
+size_t g_tl_slots = 0, g_tl_next = 0;
+
+unsigned long long* next_timeline_slot() {
+  std::lock_guard<std::mutex> lk(g_tl_mu);
+  if (!g_tl_buf || g_tl_slots == 0) return nullptr;
+  unsigned long long* p = g_tl_buf + (g_tl_next % g_tl_slots) * (size_t)kEpochSlots * kStamps;
+  ++g_tl_next;
+  return p;
+}
+
 }  // namespace
+
+int set_decode_timeline(void* buf, size_t bytes) {
+#ifdef GI_TIMELINE
+  std::lock_guard<std::mutex> lk(g_tl_mu);
+  g_tl_buf = (unsigned long long*)buf;
+  g_tl_slots = buf ? bytes / ((size_t)kEpochSlots * kStamps * 8) : 0;
+  g_tl_next = 0;
+  return GI_OK;
+#else
+  (void)buf;
+  (void)bytes;
+  return fail(GI_ERR_UNSUPPORTED, "decode timeline: this library was built without the timeline option "
+                                  "(python -m gemmainfer_amd.build --timeline builds libgemmainfer_amd_timeline.so)");
+#endif
+}
 
 int moe_decode_rows_per_launch(int top_k) {
   if (top_k <= 0 || top_k > kSlots) return 0;
@@ -1507,6 +1584,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
     int st = blocks_per_cu(fn, lds, &blocks);  // also raises the kernel's dynamic-LDS limit
     if (st != GI_OK) return st;
     if (blocks < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: a workgroup does not fit on a CU");
+    k.timeline = next_timeline_slot();
     void* args[] = {(void*)&k};
     const hipError_t e = hipLaunchKernel(fn, dim3(pl.grid), dim3(kThreads), args, lds, h.stream);
     if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");

@@ -22,7 +22,7 @@ from oracle import cpu_baseline as CB
 from oracle import moe_oracle as O
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "gemmainfer_amd.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 REF_DIR = ROOT / "oracle" / "_ref"
 
 
@@ -35,9 +35,11 @@ def lib():
 
 
 def header_functions():
-    text = HEADER.read_text()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(gi_[a-z0-9_]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(re.findall(r"\b(gi_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
