@@ -279,8 +279,30 @@ def bench_stream(m, noise, seed, copies, steps, warmup, device, gs=None):
                      "bytes of one segment each, non-temporal 16-byte loads all issued before use"}
 
 
-TIMELINE_PHASES = ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
-                   "activations staged", "down products", "sums over waves", "output / partial sums", "end"]
+D1_ROUTING_PHASES = ["routing inputs landed (wave 0)", "top-k done (wave 0)", None, None, "x staged (wave 1)",
+                     "previous footprint cleared (wave 1)", "logit keys (wave 0)", "radix select (wave 0)",
+                     "selection ranked (wave 0)", "softmax (wave 0)"]
+TIMELINE_PHASES = {
+    # decode kernel (up to 8 rows per launch): roles by whether the workgroup holds gate/up items
+    (1, "item"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
+                  "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
+    (1, "down"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
+                  "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
+    # one-token kernel: item and unit workgroups
+    (2, "item"): ["start", "routing", "weight loads issued", None, "gate/up products",
+                  "activations published", "folded partial sums published", None, None, "end",
+                  *D1_ROUTING_PHASES],
+    (2, "unit"): ["start", "routing", "weight loads issued", "words unpacked", "activations staged",
+                  "down products", "unit output written", "folded unit output written", None, "end",
+                  *D1_ROUTING_PHASES],
+    (2, "idle"): ["start", "routing", None, None, None, None, None, None, None, "end", *D1_ROUTING_PHASES],
+}
+
+
+def _timeline_role(kernel, v14):
+    if kernel == 1:
+        return "item" if v14 > 0 else "down"
+    return {1: "item", 2: "unit"}.get(v14, "idle")
 
 
 def bench_timeline(copies, steps, warmup, device, gs):
@@ -291,7 +313,7 @@ def bench_timeline(copies, steps, warmup, device, gs):
     workgroups of each role (gate/up items held or not) are reported as the
     median over the launches."""
     lib = L.load()
-    slot = 1024 * 16
+    slot = 1024 * 32
     res = {}
     p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
     for m, noise, seed in ((1, 0.0, 1), (7, 0.5, 2)):
@@ -306,38 +328,42 @@ def bench_timeline(copies, steps, warmup, device, gs):
         us = time_graph(runner, order, device)  # slot 0: the launch before capture; 1..K: the graph
         L.check(lib.gi_probe_decode_timeline(None, 0), "gi_probe_decode_timeline")
         torch.cuda.synchronize()
-        st = buf.view(steps + 1, 1024, 16)[1:].cpu()
-        per = {"item": [], "down": []}
+        st = buf.view(steps + 1, 1024, 32)[1:].cpu()
+        per = {}
+        counts = {}
         spans = []
+        kernel = None
         for k in range(steps):
             a = st[k]
-            live = a[:, 0] != 0
-            a = a[live]
+            a = a[a[:, 0] != 0]
+            kernel = int(a[0, 29])
             t0 = int(a[:, 0].min())
-            rel = (a[:, :10] - t0).double() * 0.01  # 100 MHz -> us
-            rel[a[:, :10] == 0] = float("nan")
+            rel = (a[:, :24] - t0).double() * 0.01  # 100 MHz -> us
+            rel[a[:, :24] == 0] = float("nan")
             spans.append(float(rel[:, 9].max()))
-            for role, mask in (("item", a[:, 14] > 0), ("down", a[:, 14] == 0)):
-                if int(mask.sum()) == 0:
-                    continue
+            roles = [_timeline_role(kernel, int(v)) for v in a[:, 30]]
+            for role in set(roles):
+                mask = torch.tensor([r == role for r in roles])
                 r = rel[mask]
-                per[role].append([(float(torch.nanquantile(r[:, i], 0.5)) if not torch.isnan(r[:, i]).all()
-                                   else None,
-                                   float(r[:, i][~torch.isnan(r[:, i])].max()) if not torch.isnan(r[:, i]).all()
-                                   else None) for i in range(10)])
-        roles = {}
+                if k == 0:
+                    counts[role] = int(mask.sum())
+                row = []
+                for i in range(24):
+                    col = r[:, i][~torch.isnan(r[:, i])]
+                    row.append((float(col.median()), float(col.max())) if col.numel() else (None, None))
+                per.setdefault(role, []).append(row)
+        roles_out = {}
         for role, rows in per.items():
-            if not rows:
-                continue
             table = {}
-            for i, name in enumerate(TIMELINE_PHASES):
+            for i, name in enumerate(TIMELINE_PHASES[(kernel, role)]):
                 med = [r[i][0] for r in rows if r[i][0] is not None]
                 mx = [r[i][1] for r in rows if r[i][1] is not None]
-                if med:
+                if name and med:
                     table[name] = {"median_us": statistics.median(med), "max_us": statistics.median(mx)}
-            roles[role] = {"workgroups": int(((st[0][:, 0] != 0) & ((st[0][:, 14] > 0) == (role == "item")))
-                                             .sum()), "phases": table}
+            roles_out[role] = {"workgroups": counts.get(role, 0), "phases": table}
+        roles = roles_out
         res[f"M{m}"] = {"us_per_layer_graph": us, "kernel_span_us_median": statistics.median(spans),
+                        "kernel": "moe_decode1_kernel" if kernel == 2 else "moe_decode_kernel",
                         "roles": roles, "launches": steps}
         print(f"[timeline] M={m} graph {us:.2f} us, stamped span {statistics.median(spans):.2f} us",
               file=sys.stderr, flush=True)

@@ -67,6 +67,11 @@ size_t moe_decode_state_bytes();        // epochs + exchange buffers: kept betwe
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status);
 // timeline builds (-DGI_TIMELINE): per-workgroup phase stamps of every decode launch
 int set_decode_timeline(void* buf, size_t bytes);
+unsigned long long* decode_timeline_slot();  // null unless a timeline buffer is set
+// one-token decode kernel (moe_decode1.hip): M == 1, one wait between workgroups;
+// the same state (epochs, exchange buffers) as the decode kernel
+bool moe_decode1_supported(const MoeHostArgs& h);
+int launch_moe_decode1(const MoeHostArgs& h, void* state, int* status);
 // the same launches with the library's static per-GPU scratch (moe_static.hip)
 int launch_fused_moe_static(MoeHostArgs h);
 // prefill (moe_prefill.hip): sorted-by-expert grouped GEMM for M >= kPrefillMinRows

@@ -49,10 +49,12 @@
 // read again.  Each launch's down workgroups clear the other parity's buffer
 // for the next launch (the workspace starts zero-filled).
 //
-// Launch epochs: the workspace holds kEpochSlots 64-bit epoch words, all
-// equal.  Workgroup b reads word b at launch start, adds one, and stores the
-// result to every word j with j % G == b, so all words advance by one per
-// launch whatever the grid size.  No contended atomics are used anywhere:
+// Launch epochs (moe_state.h): the workspace holds kEpochSlots 64-bit epoch
+// words, all equal.  Workgroup b reads word b at launch start, adds one to
+// its count, and stores the result to every word j with j % G == b, so all
+// words advance by one per launch whatever the grid size (the one-token
+// kernel of moe_decode1.hip shares the words and the exchange buffers).  No
+// contended atomics are used anywhere:
 // on this part a returning atomic on one address costs microseconds when 256
 // workgroups issue it.
 //
@@ -68,18 +70,22 @@
 #include "gi_common.h"
 #include "gi_internal.h"
 #include "moe_shared.h"
+#include "moe_state.h"
+#include "moe_timeline.h"
 
 namespace gi {
 
 namespace {
 
 using namespace moe;
+using moe_state::kActParity;
+using moe_state::kEpochSlots;
+using moe_state::kPartParity;
 
 constexpr int kThreads = 512;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRows = 8;              // tokens per launch (matrix-core rows used)
 constexpr int kSlots = 64;            // slots per launch
-constexpr int kEpochSlots = 1024;     // also the largest grid
 constexpr int kCols = 32;             // intermediate columns per item == down k block
 constexpr int kUnitCols = 32;         // output columns of a down unit
 constexpr int kDefaultSpin = 1 << 20;
@@ -88,7 +94,7 @@ constexpr int kMaxItems = 9;          // gate/up items per workgroup and launch
 constexpr int kDownKpw = 3;           // down k blocks per wave: Tk <= 24 (I <= 768)
 constexpr int kDownPreMfma = 4;       // matrix-core path: blocks unpacked before the activations arrive
 constexpr int kMaxI = kCols * kDownKpw * kWaves;  // 768
-constexpr size_t kActParity = (size_t)kSlots * kMaxI * 2;  // bytes of one exchange buffer
+static_assert(kActParity == (size_t)kSlots * kMaxI * 2, "activation exchange buffer size");
 constexpr int kScaleLoads = 4;        // 16-byte down-scale chunks per thread (2048 per workgroup)
 constexpr int kMaxStage = 12;         // exchange chunks per thread: 64 rows of I/8 <= 96 chunks
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // buffer offset past any resource: the load returns zeros
@@ -104,32 +110,11 @@ __host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(siz
 // Orders LDS accesses of this wave before the next instruction (no vmcnt wait).
 __device__ __forceinline__ void lds_fence() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// Phase stamps (built with -DGI_TIMELINE only): thread 0 keeps the constant
-// 100 MHz clock (s_memrealtime) at each phase end in LDS; the workgroup
-// writes them out at its end.  Slots: 0 start, 1 routing and tables, 2 x in
-// LDS, 3 weight loads issued, 4 gate/up items done, 5 activations staged,
-// 6 down products, 7 wave sums, 8 output / partial sums, 9 end; 14 and 15
-// hold the workgroup's gate/up item and down block counts.
-constexpr int kStamps = 16;
-#ifdef GI_TIMELINE
-__shared__ unsigned long long tl_lds[kStamps];
-__device__ __forceinline__ void tl_init() {
-  if (threadIdx.x < kStamps) tl_lds[threadIdx.x] = 0ull;
-}
-__device__ __forceinline__ void tl_stamp(int i) {
-  if (threadIdx.x == 0) tl_lds[i] = __builtin_amdgcn_s_memrealtime();
-}
-__device__ __forceinline__ void tl_value(int i, unsigned long long v) {
-  if (threadIdx.x == 0) tl_lds[i] = v;
-}
-__device__ __forceinline__ void tl_flush(unsigned long long* dst) {
-  lds_barrier();
-  if (dst && threadIdx.x < kStamps) dst[blockIdx.x * kStamps + threadIdx.x] = tl_lds[threadIdx.x];
-}
-#define GI_STAMP(i) tl_stamp(i)
-#else
-#define GI_STAMP(i) ((void)0)
-#endif
+// Phase stamps of the timeline build (moe_timeline.h).  Slots: 0 start,
+// 1 routing and tables, 2 x in LDS, 3 weight loads issued, 4 gate/up items
+// done, 5 activations staged, 6 down products, 7 wave sums, 8 output /
+// partial sums, 9 end; 29 kernel id (1), 30 and 31 the workgroup's gate/up
+// item and down block counts.
 
 struct DecArgs {
   const uint16_t* x;
@@ -315,9 +300,12 @@ __device__ __forceinline__ u32x2_t load_epoch(const DecArgs& a) {
   return __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(a.epochs, (uint32_t)kEpochSlots * 8u), blockIdx.x * 8u, 0,
                                               kCpolAgent);
 }
+// The next epoch word: this kernel clears the whole other parity at its end
+// and may write all of its own, so its footprint is both whole buffers.
 __device__ __forceinline__ void advance_epoch(const DecArgs& a, unsigned long long ep) {
+  const unsigned long long wv = moe_state::epoch_word(ep, moe_state::kActUnitsAll, moe_state::kPartUnitsAll);
   for (int j = blockIdx.x; j < kEpochSlots; j += gridDim.x)
-    __hip_atomic_store(a.epochs + j, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(a.epochs + j, wv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -542,7 +530,7 @@ __device__ __forceinline__ void stage_x(const DecArgs& a, const GuLds& L, const 
 // ---------------------------------------------------------------------------
 constexpr int kMaxUnits = 88;          // H <= 2816
 constexpr int kPartSlots = 8;          // workgroups sharing one unit
-constexpr size_t kPartParity = (size_t)kMaxUnits * kPartSlots * kRows * kUnitCols * 4;  // bytes
+static_assert(kPartParity == (size_t)kMaxUnits * kPartSlots * kRows * kUnitCols * 4, "partial buffer size");
 
 // Workgroup w owns blocks [blk_lo(w), blk_lo(w + 1)); the workgroup holding
 // block b is the largest w with blk_lo(w) <= b.
@@ -1303,7 +1291,7 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   if (a.E <= 2 * kWave) epr = dec_start<KBW, 2>(a, P, xr);
   else if (a.E <= 4 * kWave) epr = dec_start<KBW, 4>(a, P, xr);
   else epr = dec_start<KBW, kRouteMaxExperts / kWave>(a, P, xr);
-  const unsigned long long ep = (((unsigned long long)epr.y << 32) | epr.x) + 1ull;
+  const unsigned long long ep = moe_state::epoch_count(((unsigned long long)epr.y << 32) | epr.x) + 1ull;
   const int parity = (int)(ep & 1ull);
   uint16_t* act = a.act + (size_t)parity * (kActParity / 2);
   float* part = a.part + (size_t)parity * (kPartParity / 4);
@@ -1333,8 +1321,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   if (n_my > 0) stage_x<KBW>(a, L, xr);
   GI_STAMP(2);
 #ifdef GI_TIMELINE
-  tl_value(14, (unsigned long long)n_my);
-  tl_value(15, (unsigned long long)(bhi - blo));
+  tl_value(29, 1ull);
+  tl_value(30, (unsigned long long)n_my);
+  tl_value(31, (unsigned long long)(bhi - blo));
 #endif
   // the down scales of every block of the workgroup, ahead of the weights
   // (older than every weight load, they leave the weight waits exact)
@@ -1458,21 +1447,23 @@ int log2_exact(int v) {
   return (1 << s) == v ? s : -1;
 }
 
+}  // namespace
+
 // Timeline builds: the caller's stamp buffer, used in slots of kEpochSlots
 // workgroups x kStamps words, one slot per launch in rotation.
+namespace {
 std::mutex g_tl_mu;
 unsigned long long* g_tl_buf = nullptr;
 size_t g_tl_slots = 0, g_tl_next = 0;
+}  // namespace
 
-unsigned long long* next_timeline_slot() {
+unsigned long long* decode_timeline_slot() {
   std::lock_guard<std::mutex> lk(g_tl_mu);
   if (!g_tl_buf || g_tl_slots == 0) return nullptr;
   unsigned long long* p = g_tl_buf + (g_tl_next % g_tl_slots) * (size_t)kEpochSlots * kStamps;
   ++g_tl_next;
   return p;
 }
-
-}  // namespace
 
 int set_decode_timeline(void* buf, size_t bytes) {
 #ifdef GI_TIMELINE
@@ -1523,7 +1514,7 @@ bool moe_decode_supported(const MoeHostArgs& h) {
   return true;
 }
 
-size_t moe_decode_state_bytes() { return (size_t)kEpochSlots * 8 + 2 * kActParity + 2 * kPartParity; }
+size_t moe_decode_state_bytes() { return moe_state::state_bytes(); }
 
 int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   const int rows_per = moe_decode_rows_per_launch(h.top_k);
@@ -1557,8 +1548,8 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   k.status = status;
   k.host_flag = device_error_flag(!h.no_alloc);
   k.epochs = (unsigned long long*)state;
-  k.act = (uint16_t*)((char*)state + (size_t)kEpochSlots * 8);
-  k.part = (float*)((char*)state + (size_t)kEpochSlots * 8 + 2 * kActParity);
+  k.act = (uint16_t*)((char*)state + moe_state::act_offset());
+  k.part = (float*)((char*)state + moe_state::part_offset());
 
   const int kbw = kbw_for(h.H);
   const int cus = device_cu_count();
@@ -1584,7 +1575,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
     int st = blocks_per_cu(fn, lds, &blocks);  // also raises the kernel's dynamic-LDS limit
     if (st != GI_OK) return st;
     if (blocks < 1) return fail(GI_ERR_UNSUPPORTED, "fused MoE decode: a workgroup does not fit on a CU");
-    k.timeline = next_timeline_slot();
+    k.timeline = decode_timeline_slot();
     void* args[] = {(void*)&k};
     const hipError_t e = hipLaunchKernel(fn, dim3(pl.grid), dim3(kThreads), args, lds, h.stream);
     if (e != hipSuccess) return hip_fail(e, "fused MoE decode launch");

@@ -1161,11 +1161,12 @@ int launch_fused_moe(const MoeHostArgs& h) {
     const size_t base = prefill_base(h.H, h.I);
     return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base);
   }
-  if (moe_decode_supported(h)) {
+  if (moe_decode1_supported(h) || moe_decode_supported(h)) {
     // the same layout as the size query (gi_fused_moe_workspace_bytes)
     const int per = moe_rows_per_launch(h.top_k);
     const WsLayout L = ws_layout((h.M < per ? h.M : per) * h.top_k, h.H, h.I, kTaskCols);
     char* ws0 = (char*)h.workspace;
+    if (h.M == 1 && moe_decode1_supported(h)) return launch_moe_decode1(h, ws0 + L.state, (int*)(ws0 + L.status));
     return launch_moe_decode(h, ws0 + L.state, (int*)(ws0 + L.status));
   }
 

@@ -82,6 +82,37 @@ __device__ __forceinline__ void route_issue(const A& a, int t, int lane, RouteIn
     r.es[v] = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)(lane + v * kWave) * 4u, 0, 0);
 }
 
+// Softmax over the selected top-k (gemma.py:78-80), one wave: lane r < top_k
+// holds the r-th expert, its key and its expert scale; writes idx_out[r] and
+// w_out[r] = softmax_fp32(values)[r] * expert_scale.
+template <class A>
+__device__ __forceinline__ void route_softmax(const A& a, int lane, int my_idx, uint32_t my_key, float my_es,
+                                              int* idx_out, float* w_out) {
+  const float my_val = key_value(my_key);
+  const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), 0));
+  const float ex = lane < a.top_k ? expf(my_val - vmax) : 0.f;
+  // sum of the weights in the order of a butterfly over xor 32, 16, .., 1;
+  // with top_k <= 8 every lane past 7 holds zero and the first three steps
+  // add exact zeros, so lanes 0-3 need only lane + 4, then the quad swaps
+  float sum;
+  if (a.top_k <= 8) {
+    float s = ex + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ex), 0x104, 0xF, 0xF, false));  // row_shl:4
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
+    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
+    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
+  } else {
+    sum = ex;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  }
+  if (lane < a.top_k) {
+    float p = ex / sum;
+    p *= my_es;
+    idx_out[lane] = my_idx;
+    w_out[lane] = p;
+  }
+}
+
 // Top-k + softmax of one token by one wave (gemma.py:77-80) from the loaded
 // inputs.  Each round takes the largest remaining key and, among equal keys,
 // the lowest expert index, then retires it (key 0; every real value has a
@@ -159,29 +190,7 @@ __device__ __forceinline__ void route_finish(const A& a, int lane, const RouteIn
       }
     }
   }
-  const float my_val = key_value(my_key);
-  const float vmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_val), 0));
-  const float ex = lane < a.top_k ? expf(my_val - vmax) : 0.f;
-  // sum of the weights in the order of a butterfly over xor 32, 16, .., 1;
-  // with top_k <= 8 every lane past 7 holds zero and the first three steps
-  // add exact zeros, so lanes 0-3 need only lane + 4, then the quad swaps
-  float sum;
-  if (a.top_k <= 8) {
-    float s = ex + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(ex), 0x104, 0xF, 0xF, false));  // row_shl:4
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0x4E, 0xF, 0xF, false));  // quad [2,3,0,1]
-    s += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(s), 0xB1, 0xF, 0xF, false));  // quad [1,0,3,2]
-    sum = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(s), 0));
-  } else {
-    sum = ex;
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
-  }
-  if (lane < a.top_k) {
-    float p = ex / sum;
-    p *= my_es;
-    idx_out[lane] = my_idx;
-    w_out[lane] = p;
-  }
+  route_softmax(a, lane, my_idx, my_key, my_es, idx_out, w_out);
 }
 
 // Loads and selection in one step (kernels with nothing to overlap).

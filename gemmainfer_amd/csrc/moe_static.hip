@@ -78,7 +78,8 @@ int launch_fused_moe_static(MoeHostArgs h) {
   h.no_alloc = 1;
   h.workspace = nullptr;
   h.workspace_bytes = 0;
-  if (!moe_decode_supported(h))
+  const bool one = h.M == 1 && moe_decode1_supported(h);
+  if (!one && !moe_decode_supported(h))
     return fail(GI_ERR_WORKSPACE,
                 "fused MoE (static): this shape needs a caller workspace (gi_fused_batched_moe); the static "
                 "2 MiB scratch serves the decode kernel's shapes only (hidden and intermediate sizes multiples "
@@ -90,6 +91,7 @@ int launch_fused_moe_static(MoeHostArgs h) {
   unsigned char* base = nullptr;
   st = static_scratch(h.stream, &base);
   if (st != GI_OK) return st;
+  if (one) return launch_moe_decode1(h, base + off, (int*)base);
   return launch_moe_decode(h, base + off, (int*)base);
 }
 

@@ -33,15 +33,15 @@ int gi_probe_stream_read(const void* const* seg_ptr, const uint64_t* seg_bytes, 
 /* Phase timeline of the decode kernel.  In a library built with the
  * timeline option (python -m gemmainfer_amd.build --timeline, which writes
  * libgemmainfer_amd_timeline.so beside the product library) every later
- * decode-kernel launch writes, per workgroup, 16 uint64 words into the next
- * slot of `buf` (device memory; slots of 1024 x 16 words, used in rotation,
- * bytes / 131072 of them; NULL stops the recording): words 0-9 are the
+ * decode-kernel launch writes, per workgroup, 32 uint64 words into the next
+ * slot of `buf` (device memory; slots of 1024 x 32 words, used in rotation,
+ * bytes / 262144 of them; NULL stops the recording): words 0-23 are the
  * constant 100 MHz clock (s_memrealtime) at the ends of the kernel's phases
- * (0 start, 1 routing and tables, 2 x in LDS, 3 weight loads issued,
- * 4 gate/up items done, 5 activations staged, 6 down products, 7 sums over
- * the waves, 8 output or partial sums written, 9 end), words 14 and 15 the
- * workgroup's gate/up item and down block counts.  The product library
- * returns GI_ERR_UNSUPPORTED.                                              */
+ * (zero for phases the workgroup skips), word 29 names the kernel (1: the
+ * decode kernel, up to 8 rows per launch; 2: the one-token kernel), words 30
+ * and 31 the workgroup's role and index.  The phase numbering of each kernel
+ * is stated beside its stamps in the kernel source and in bench.py
+ * (TIMELINE_PHASES).  The product library returns GI_ERR_UNSUPPORTED.     */
 int gi_probe_decode_timeline(void* buf, size_t bytes);
 
 #ifdef __cplusplus
