@@ -132,7 +132,7 @@ int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
 
 size_t gi_fused_moe_workspace_bytes(int M, int top_k, int H, int I, int E) {
   if (top_k <= 0 || H <= 0 || I <= 0 || E <= 0) return 0;
-  return gi::moe_workspace_bytes(M, top_k, H, I, E);
+  return gi::moe_workspace_bytes_any(M, top_k, H, I, E);
 }
 
 int gi_fused_batched_moe(const void* x, int x_dtype, const int32_t* gu_packed,
@@ -141,9 +141,9 @@ int gi_fused_batched_moe(const void* x, int x_dtype, const int32_t* gu_packed,
                          const void* w, int w_dtype, void* out, int M, int H, int I, int E,
                          int top_k, int group_size, void* workspace, size_t workspace_bytes,
                          int spin_limit, void* stream) {
-  int st = check_bf16_x(x_dtype, "fused_batched_moe");
-  if (st != GI_OK) return st;
-  st = check_idx_dtype(idx_dtype);
+  if (x_dtype != GI_DTYPE_BF16 && x_dtype != GI_DTYPE_FP16 && x_dtype != GI_DTYPE_FP32)
+    return fail(GI_ERR_UNSUPPORTED, "fused_batched_moe: activations must be bf16, fp16 or fp32");
+  int st = check_idx_dtype(idx_dtype);
   if (st != GI_OK) return st;
   if (w_dtype != GI_DTYPE_BF16 && w_dtype != GI_DTYPE_FP16 && w_dtype != GI_DTYPE_FP32)
     return fail(GI_ERR_UNSUPPORTED, "fused_batched_moe: expert weights must be bf16, fp16 or fp32");
@@ -171,6 +171,7 @@ int gi_fused_batched_moe(const void* x, int x_dtype, const int32_t* gu_packed,
   a.workspace_bytes = workspace_bytes;
   a.spin_limit = spin_limit;
   a.stream = as_stream(stream);
+  a.x_dtype = x_dtype;
   return gi::launch_fused_moe(a);
 }
 
@@ -260,6 +261,9 @@ size_t gi_w4a16_workspace_bytes(int M, int K, int N, int group_size) {
 int gi_w4a16_linear(const void* A, int a_dtype, const int32_t* B_packed, const void* scales,
                     int n_groups, void* C, int M, int K, int N, int group_size, float softcap,
                     void* workspace, size_t workspace_bytes, void* stream) {
+  if (a_dtype == GI_DTYPE_FP16 || a_dtype == GI_DTYPE_FP32)
+    return gi::launch_w4a16_generic(A, a_dtype, B_packed, scales, n_groups, C, M, K, N, group_size, softcap,
+                                    as_stream(stream));
   int st = check_bf16_x(a_dtype, "w4a16_linear");
   if (st != GI_OK) return st;
   return gi::launch_w4a16(A, B_packed, scales, n_groups, C, M, K, N, group_size, softcap,

@@ -50,6 +50,7 @@ struct MoeHostArgs {
   int spin_limit;
   hipStream_t stream;
   int no_alloc;             // the caller cannot allocate: no pinned-memory set-up either
+  int x_dtype;              // activations, scales and out: GI_DTYPE_BF16 (0), FP16 or FP32
 };
 
 // Argument checks shared by every fused-MoE entry point (GI_OK or a failure code).
@@ -58,7 +59,8 @@ int check_moe_args(const MoeHostArgs& h);
 size_t moe_decode_scratch_offset();
 // Largest number of token rows one fused launch handles (S = rows*top_k <= 256).
 int moe_rows_per_launch(int top_k);
-size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E);
+size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E);      // bf16 activations
+size_t moe_workspace_bytes_any(int rows, int top_k, int H, int I, int E);  // any activation dtype
 int launch_fused_moe(const MoeHostArgs& a);
 // decode/verify kernel (moe_decode.hip): <= 8 rows per launch, no grid barrier
 bool moe_decode_supported(const MoeHostArgs& h);
@@ -88,6 +90,14 @@ int launch_route(const void* logits, int logits_dtype, const float* expert_scale
 int read_workspace_status(void* workspace, int32_t* host_status, hipStream_t stream);
 int launch_moe_router(const void* x, const void* router_scale, const void* gate, void* logits, int M,
                       int H, int E, float eps, hipStream_t stream);
+
+// fp16 / fp32 activations (generic_dtype.hip): VALU kernels, fp32 arithmetic,
+// the reference's rounding points in the activation dtype; the activations
+// of the MoE go through an fp32 buffer [M*top_k][I] in the workspace
+size_t moe_generic_workspace_bytes(int M, int top_k, int I);
+int launch_moe_generic(const MoeHostArgs& h, int x_dtype, void* act_ws, size_t act_bytes);
+int launch_w4a16_generic(const void* A, int a_dtype, const int32_t* B, const void* scales, int n_groups, void* C,
+                         int M, int K, int N, int gs, float softcap, hipStream_t stream);
 
 // ---- W4A16 linear -------------------------------------------------------------
 size_t w4a16_workspace_bytes(int M, int K, int N, int gs);

@@ -1141,6 +1141,14 @@ size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
   return pf > L.total ? pf : L.total;
 }
 
+// The same workspace serves every activation dtype: fp16 / fp32 calls keep
+// their activations after the decode state and the barrier counters.
+size_t moe_workspace_bytes_any(int rows, int top_k, int H, int I, int E) {
+  const size_t b = moe_workspace_bytes(rows, top_k, H, I, E);
+  const size_t g = prefill_base(H, I) + moe_generic_workspace_bytes(rows, top_k, I);
+  return g > b ? g : b;
+}
+
 int launch_fused_moe(const MoeHostArgs& h) {
   int st = check_moe_shapes(h);
   if (st != GI_OK) return st;
@@ -1152,11 +1160,15 @@ int launch_fused_moe(const MoeHostArgs& h) {
   const bool mfma = h.gs % 32 == 0 && h.M > 1;
   const int rows_vl = moe_rows_per_launch(h.top_k);
   const int rows_per = mfma ? (rows_vl < kResidentTokens ? rows_vl : kResidentTokens) : rows_vl;
-  if (!h.workspace || h.workspace_bytes < moe_workspace_bytes(h.M, h.top_k, h.H, h.I, h.E))
+  if (!h.workspace || h.workspace_bytes < moe_workspace_bytes_any(h.M, h.top_k, h.H, h.I, h.E))
     return fail(GI_ERR_WORKSPACE,
                 "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
   if (((uintptr_t)h.workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
+  if (h.x_dtype != GI_DTYPE_BF16) {
+    const size_t base = prefill_base(h.H, h.I);
+    return launch_moe_generic(h, h.x_dtype, (char*)h.workspace + base, h.workspace_bytes - base);
+  }
   if (moe_prefill_supported(h)) {
     const size_t base = prefill_base(h.H, h.I);
     return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base);

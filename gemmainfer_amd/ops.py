@@ -157,6 +157,16 @@ def _require_bf16(x: torch.Tensor, who: str) -> None:
             f"{who}: the gfx950 kernels implement bf16 activations; got {x.dtype}")
 
 
+_ACT_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+
+
+def _require_act_dtype(x: torch.Tensor, who: str) -> None:
+    """bf16, fp16 or fp32 activations (the reference's dispatch, marlin.cu:694-700,
+    :764-842): bf16 runs the tuned kernels, fp16 and fp32 VALU kernels."""
+    if x.dtype not in _ACT_DTYPES:
+        raise TypeError(f"{who}: activations must be bf16, fp16 or fp32; got {x.dtype}")
+
+
 def fused_batched_moe(x, gate_up_packed, gate_up_scales, down_packed, down_scales,
                       expert_indices, expert_weights, out, group_size, *, spin_limit: int = 0):
     """out += sum over slots of w * expert(x)  (drop-in for gemmainfer_csrc.fused_batched_moe).
@@ -166,12 +176,13 @@ def fused_batched_moe(x, gate_up_packed, gate_up_scales, down_packed, down_scale
     weights are cast to x's dtype, and the result is ADDED to ``out`` (the
     caller zeroes it, gemma.py:82).  Unlike the reference there is no cap on
     how many slots share an expert (marlin.cu:325) and no 128-slot limit
-    (:300); the combine is a fixed-order fp32 sum with one bf16 rounding.
+    (:300); the combine is a fixed-order fp32 sum with one rounding to x's
+    dtype.  x, the scales and out are bf16, fp16 or fp32 (all the same).
     """
     dev = _on_device(x, gate_up_packed, gate_up_scales, down_packed, down_scales,
                      expert_indices, expert_weights, out)
     raise_pending_device_error(dev)
-    _require_bf16(x, "fused_batched_moe")
+    _require_act_dtype(x, "fused_batched_moe")
     m, h, i, e = _moe_weight_shapes(x, gate_up_packed, gate_up_scales, down_packed, down_scales)
     _require(isinstance(group_size, int) and group_size > 0 and group_size % 8 == 0,
              f"group_size must be a positive multiple of 8, got {group_size}")
@@ -199,7 +210,7 @@ def fused_batched_moe(x, gate_up_packed, gate_up_scales, down_packed, down_scale
     nbytes = lib.gi_fused_moe_workspace_bytes(m, top_k, h, i, e)
     ws = _WS.get("moe", dev, nbytes)
     L.check(lib.gi_fused_batched_moe(
-        _ptr(xc), L.DTYPE_BF16, _ptr(gate_up_packed), _ptr(gate_up_scales),
+        _ptr(xc), _DTYPE_CODE[x.dtype], _ptr(gate_up_packed), _ptr(gate_up_scales),
         gate_up_scales.shape[1], _ptr(down_packed), _ptr(down_scales), down_scales.shape[1],
         _ptr(idx), _DTYPE_CODE[idx.dtype], _ptr(w), _DTYPE_CODE[w.dtype], _ptr(oc),
         m, h, i, e, top_k, int(group_size), _ptr(ws), ws.numel(), int(spin_limit),
@@ -382,7 +393,7 @@ def marlin_w4a16(A, B_packed, scales, C, group_size, softcap: float = 0.0):
     final-logit softcap cap*tanh(C/cap) (gemma.py:356-357).
     """
     dev = _on_device(A, B_packed, scales, C)
-    _require_bf16(A, "marlin_w4a16")
+    _require_act_dtype(A, "marlin_w4a16")
     _require(A.dim() == 2, f"A must be [M, K], got {tuple(A.shape)}")
     m, k = A.shape
     _require(B_packed.dim() == 2 and B_packed.dtype == torch.int32 and B_packed.shape[0] * 8 == k,
@@ -403,7 +414,7 @@ def marlin_w4a16(A, B_packed, scales, C, group_size, softcap: float = 0.0):
     nbytes = lib.gi_w4a16_workspace_bytes(m, k, n, group_size)
     ws = _WS.get("w4a16", dev, nbytes) if nbytes else None
     L.check(lib.gi_w4a16_linear(
-        _ptr(Ac), L.DTYPE_BF16, _ptr(B_packed), _ptr(scales), scales.shape[0], _ptr(Cc), m, k, n,
+        _ptr(Ac), _DTYPE_CODE[A.dtype], _ptr(B_packed), _ptr(scales), scales.shape[0], _ptr(Cc), m, k, n,
         int(group_size), float(softcap), _ptr(ws), 0 if ws is None else ws.numel(), _stream(dev)),
         "marlin_w4a16")
     if Cc is not C:

@@ -102,11 +102,15 @@ int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
  * out[M, H] += sum_slots bf16(w[slot]) * down(gelu_tanh(gate) * up)(x[token])
  *   x          bf16 [M, H]
  *   gu_packed  int32 [E, H/8, 2I]     gate in columns [0, I), up in [I, 2I)
- *   gu_scales  bf16 [E, gu_groups, 2I]
+ *   gu_scales  T [E, gu_groups, 2I]
  *   d_packed   int32 [E, I/8, H]
- *   d_scales   bf16 [E, d_groups, H]
+ *   d_scales   T [E, d_groups, H]
  *   idx        int32|int64 [M*top_k]  w  bf16|fp16|fp32 [M*top_k]
- *   out        bf16 [M, H]            accumulated into (caller zeroes it)
+ *   out        T [M, H]               accumulated into (caller zeroes it)
+ * T = x_dtype: bf16, fp16 or fp32 (marlin.cu:694-700).  bf16 runs the paths
+ * below; fp16 and fp32 run VALU kernels (fp32 arithmetic, the weights cast
+ * to T, the activation stored in T, one rounding of the output in T; two
+ * launches).
  * One kernel launch per 256/top_k rows (8 rows on the decode kernel); from
  * 64 rows with top_k <= 64, a power-of-two multiple of 32 as group size,
  * H % 64 == 0 and I % 32 == 0, the grouped-GEMM prefill path (align,
@@ -213,8 +217,10 @@ int gi_workspace_status(void* workspace, size_t workspace_bytes,
 /* ---- a8 / a11: W4A16 linear ---------------------------------------------
  * C[M, N] = A[M, K] @ dequant(B_packed[K/8, N], scales[n_groups, N]),
  * optionally followed by C = softcap*tanh(C/softcap) when softcap > 0 (the
- * lm_head epilogue, gemma.py:356-357).  A, scales, C bf16.  C is
- * overwritten.  Requirements: K % 8 == 0, N % 4 == 0, group_size % 8 == 0. */
+ * lm_head epilogue, gemma.py:356-357).  A, scales, C of a_dtype: bf16, fp16
+ * or fp32 (marlin.cu:764-842; fp16 and fp32 run a VALU kernel with fp32
+ * arithmetic and one rounding of C).  C is overwritten.  Requirements:
+ * K % 8 == 0, N % 4 == 0 (bf16), group_size % 8 == 0.                       */
 size_t gi_w4a16_workspace_bytes(int M, int K, int N, int group_size);
 int gi_w4a16_linear(const void* A, int a_dtype,
                     const int32_t* B_packed, const void* scales, int n_groups,

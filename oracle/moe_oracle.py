@@ -10,6 +10,8 @@ Pinning (what checks this restatement, see tests/test_oracle.py):
 
   bf16_round            exhaustive-ish: torch's own float32->bfloat16 cast on
                         ~10^6 values incl. ties, subnormals, inf/nan.
+  round_to              torch's own float32->float16 cast (fp16) and the
+                        float32 cast (fp32) on the same values; bf16 = bf16_round.
   unpack_int4/dequant   exhaustive over 16 nibble values x 8 positions x scale
                         sign; packer round trip (pack_int4); reference C++
                         fallback ``cpu_marlin_w4a16`` from oracle/_ref.
@@ -88,6 +90,23 @@ def bf16_round(a) -> np.ndarray:
     res[over] = np.copysign(np.inf, res[over])
     out[finite] = res
     return out
+
+
+def round_to(a, dtype: str = "bf16") -> np.ndarray:
+    """Round float64 values to the activation dtype of a call: "bf16"
+    (bf16_round), "fp16" (nearest IEEE half, ties to even: numpy's correctly
+    rounded float64 -> float16 cast) or "fp32" (float64 -> float32 cast);
+    returned as float64.  The reference dispatches these three dtypes
+    (marlin.cu:694-700, :764-842) and rounds to the one of x at the same
+    points for each."""
+    x = np.asarray(a, dtype=np.float64)
+    if dtype == "bf16":
+        return bf16_round(x)
+    if dtype == "fp16":
+        return x.astype(np.float16).astype(np.float64)
+    if dtype == "fp32":
+        return x.astype(np.float32).astype(np.float64)
+    raise ValueError(f"dtype {dtype!r}")
 
 
 def bf16_bits_to_f64(bits) -> np.ndarray:
@@ -341,11 +360,12 @@ def token_union_align(idx, num_experts) -> Alignment:
 # fused MoE (marlin.cu:262-702; pybind.cpp:198-245; gemma.py:82-113)
 # --------------------------------------------------------------------------
 def expert_forward(x_rows, gu_packed_e, gu_scales_e, d_packed_e, d_scales_e,
-                   group_size, act_round=True):
+                   group_size, act_round=True, dtype="bf16"):
     """One expert on a block of rows: gate_up -> gelu_tanh(gate)*up -> down.
 
     gate/up are float64 sums of x*(q-8)*s (marlin.cu:371-416); the activation
-    is rounded to bf16 as the reference stores it (marlin.cu:421-423) when
+    is rounded to the activation dtype (bf16 by default) as the reference
+    stores it (``static_cast<scalar_t>``, marlin.cu:421-423) when
     ``act_round``; down is a float64 sum over I (marlin.cu:538-576).
     Returns (act [n, I], y [n, H]) float64.
     """
@@ -354,14 +374,15 @@ def expert_forward(x_rows, gu_packed_e, gu_scales_e, d_packed_e, d_scales_e,
     gu = np.asarray(x_rows, dtype=np.float64) @ wgu
     act = gelu_tanh(gu[:, :n_inter]) * gu[:, n_inter:]
     if act_round:
-        act = bf16_round(act)
+        act = round_to(act, dtype)
     y = act @ dequant(d_packed_e, d_scales_e, group_size)
     return act, y
 
 
 def fused_batched_moe(x, gu_packed, gu_scales, d_packed, d_scales, idx, w,
-                      out_in, group_size, act_round=True):
-    """out = out_in + sum over slots of bf16(w[slot]) * expert(x[token])[slot].
+                      out_in, group_size, act_round=True, dtype="bf16"):
+    """out = out_in + sum over slots of T(w[slot]) * expert(x[token])[slot],
+    T the activation dtype ("bf16" default, "fp16", "fp32").
 
     Semantics of ``gemmainfer_csrc.fused_batched_moe`` (pybind.cpp:247-271 ->
     marlin.cu:612-702): top_k = numel(idx)/M (:628-629); routing weights are
@@ -379,7 +400,7 @@ def fused_batched_moe(x, gu_packed, gu_scales, d_packed, d_scales, idx, w,
     s_total = flat_idx.shape[0]
     assert s_total % m == 0
     top_k = s_total // m
-    w_used = bf16_round(np.asarray(w, dtype=np.float64).reshape(-1))
+    w_used = round_to(np.asarray(w, dtype=np.float64).reshape(-1), dtype)
     num_experts = np.asarray(gu_packed).shape[0]
     al = token_union_align(flat_idx, num_experts)
     contrib = np.zeros((s_total, x.shape[1]), dtype=np.float64)
@@ -388,7 +409,7 @@ def fused_batched_moe(x, gu_packed, gu_scales, d_packed, d_scales, idx, w,
         sl = al.slots[al.offsets[u]:al.offsets[u + 1]]
         toks = sl // top_k
         _, y = expert_forward(x[toks], gu_packed[e], gu_scales[e], d_packed[e],
-                              d_scales[e], group_size, act_round)
+                              d_scales[e], group_size, act_round, dtype)
         contrib[sl] = y * w_used[sl][:, None]
     out = np.asarray(out_in, dtype=np.float64).copy()
     for t in range(m):

@@ -63,6 +63,32 @@ def moe_case(name, m, h, i, e, top_k, gs, seed, idx=None):
         out_bf16=bits(out), group_size=np.int32(gs))
 
 
+def dtype_cases():
+    """fp16 and fp32 activations (the reference dispatches all three dtypes,
+    marlin.cu:694-700 and :764-842; its CPU fallback computes in float32 and
+    stores in the tensors' dtype, pybind.cpp:46-85,198-245): one linear and
+    one MoE call with duplicate ids per dtype, stored as float16 / float32
+    arrays."""
+    for dt, tag in ((torch.float16, "fp16"), (torch.float32, "fp32")):
+        B, S = synth.linear_weights(512, 128, 128, seed=11)
+        A = synth.activations(3, 512, seed=11).to(dt)
+        S = S.to(dt)
+        C = torch.empty(3, 128, dtype=dt)
+        R.marlin_w4a16(A, B, S, C, 128)
+        np.savez_compressed(OUT / f"linear_m3_k512_n128_gs128_{tag}.npz", A=A.numpy(), B_packed=B.numpy(),
+                            scales=S.numpy(), C=C.numpy(), group_size=np.int32(128))
+        W = synth.moe_weights(8, 256, 128, 64, seed=12)
+        x = synth.activations(3, 256, seed=12).to(dt)
+        idx = torch.tensor([[1, 1, 2, 3], [2, 5, 5, 5], [0, 7, 1, 2]], dtype=torch.int32)
+        w = torch.softmax(torch.randn(idx.shape, generator=torch.Generator().manual_seed(12)), dim=-1).to(dt)
+        gus, dns = W["gate_up_scales"].to(dt), W["down_scales"].to(dt)
+        out = torch.zeros(3, 256, dtype=dt)
+        R.fused_batched_moe(x, W["gate_up_packed"], gus, W["down_packed"], dns, idx, w, out, 64)
+        np.savez_compressed(OUT / f"moe_m3_dups_gs64_{tag}.npz", x=x.numpy(), gate_up_packed=W["gate_up_packed"].numpy(),
+                            gate_up_scales=gus.numpy(), down_packed=W["down_packed"].numpy(), down_scales=dns.numpy(),
+                            idx=idx.numpy(), w=w.numpy(), out=out.numpy(), group_size=np.int32(64))
+
+
 def elementwise_case():
     g = torch.Generator().manual_seed(5)
     x = (torch.randn(3, 256, generator=g) * 3).to(torch.bfloat16)
@@ -108,6 +134,7 @@ def main():
              idx=[[1, 1, 2, 3], [2, 5, 5, 5], [0, 7, 1, 2]])
     elementwise_case()
     router_case("router_m3_h512_e16", 3, 512, 16, seed=8)
+    dtype_cases()
     for p in sorted(OUT.glob("*.npz")):
         print(p.name, p.stat().st_size)
 

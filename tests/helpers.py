@@ -77,3 +77,28 @@ def assert_logits_close(got: torch.Tensor, ref64: np.ndarray, what: str = "",
     assert not bad.any(), f"{what}: {int(bad.sum())} logits more than one bf16 ulp off; max diff {diff.max():.3e}"
     exact = float(np.mean(g == ref64))
     assert exact >= min_exact, f"{what}: only {exact:.4f} of logits bit-identical"
+
+
+def assert_dtype_close(got: torch.Tensor, ref64: np.ndarray, dtype: str, what: str = "") -> dict:
+    """The tolerance gate for outputs in the activation dtype of a call.
+
+    bf16: assert_bf16_close.  fp16: rel-L2 <= 1e-2 and every element within
+    2e-2 + 2^-10 |ref| (the north-star max-abs plus one fp16 ulp; fp16 keeps 3
+    more mantissa bits than bf16).  fp32 (nothing is rounded but the float32
+    sums): rel-L2 <= 2e-5 and max |got - ref| <= 1e-4 * RMS(ref)."""
+    if dtype == "bf16":
+        return assert_bf16_close(got, ref64, what)
+    g = np64(got)
+    stats = O.error_stats(g, ref64)
+    assert np.isfinite(g).all(), f"{what}: non-finite outputs"
+    if dtype == "fp16":
+        assert stats["rel_l2"] <= REL_L2, f"{what}: rel-L2 {stats['rel_l2']:.3e} ({stats})"
+        bound = ATOL + 2.0 ** -10 * np.abs(ref64)
+        bad = np.abs(g - ref64) > bound
+        assert not bad.any(), f"{what}: {int(bad.sum())} elements outside 2e-2 + 2^-10|ref| ({stats})"
+    elif dtype == "fp32":
+        assert stats["rel_l2"] <= 2e-5, f"{what}: rel-L2 {stats['rel_l2']:.3e} ({stats})"
+        assert stats["max_abs_over_rms"] <= 1e-4, f"{what}: max-abs/RMS too large ({stats})"
+    else:
+        raise ValueError(dtype)
+    return stats

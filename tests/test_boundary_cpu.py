@@ -76,7 +76,7 @@ def _moe_call(lib, **over):
 
 
 @pytest.mark.parametrize("over,code,frag", [
-    (dict(xd=L.DTYPE_FP32), L.GI_ERR_UNSUPPORTED, "bf16"),
+    (dict(xd=L.DTYPE_INT32), L.GI_ERR_UNSUPPORTED, "bf16, fp16 or fp32"),
     (dict(idt=L.DTYPE_FP32), L.GI_ERR_UNSUPPORTED, "int32 or int64"),
     (dict(H=2820), L.GI_ERR_INVALID_ARG, "multiples of 8"),
     (dict(gs=12), L.GI_ERR_INVALID_ARG, "group_size"),
@@ -98,7 +98,9 @@ def test_other_entry_points_validate(lib):
     assert lib.gi_w4a16_linear(None, L.DTYPE_BF16, None, None, 1, None, 1, 2812, 2816, 128, 0.0,
                                None, 0, None) == L.GI_ERR_INVALID_ARG       # K % 8
     assert lib.gi_w4a16_linear(None, L.DTYPE_FP16, None, None, 1, None, 1, 2816, 2816, 128, 0.0,
-                               None, 0, None) == L.GI_ERR_UNSUPPORTED
+                               None, 0, None) == L.GI_ERR_INVALID_ARG       # fp16: null pointers
+    assert lib.gi_w4a16_linear(None, L.DTYPE_INT32, None, None, 1, None, 1, 2816, 2816, 128, 0.0,
+                               None, 0, None) == L.GI_ERR_UNSUPPORTED       # int32 activations
     assert lib.gi_moe_route_topk_softmax(None, L.DTYPE_FP32, None, 1, 128, 65, None, None, 0,
                                          None) == L.GI_ERR_UNSUPPORTED      # top_k > 64
     assert lib.gi_moe_align(None, L.DTYPE_INT32, 40, 8, 128, None, None, None, None, None,

@@ -1,0 +1,137 @@
+"""fp16 and fp32 activations through the drop-in module on the GPU.
+
+The reference dispatches all three activation dtypes for the MoE
+(csrc/marlin.cu:694-700) and the linear (:764-770, :816-822, :831-842), and
+its CLIs offer them (scripts/chat.py:53, scripts/serve.py:293).  x (A), the
+scales and out (C) share the dtype; the routing weights are cast to it.
+Checked against the float64 oracle with the reference's rounding points in
+that dtype (oracle/moe_oracle.py round_to) and against the golden vectors of
+the reference's own CPU fallback in fp16 and fp32 (tests/golden).
+"""
+import numpy as np
+import pytest
+import torch
+
+import gemmainfer_csrc
+from gemmainfer_amd import ops, synth
+from oracle import moe_oracle as O
+from tests.helpers import assert_dtype_close, np64
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+DT = {"fp16": torch.float16, "fp32": torch.float32}
+GOLDEN = __import__("pathlib").Path(__file__).resolve().parent / "golden"
+E, H, I = 128, 2816, 704
+
+
+def _moe_weights(e, h, i, gs, seed, dt):
+    W = synth.moe_weights(e, h, i, gs, seed=seed)
+    g = torch.Generator().manual_seed(seed + 3)
+    for k in ("gate_up_scales", "down_scales"):   # signed scales of a checkpoint's size
+        W[k] = (torch.randn(W[k].shape, generator=g) * 0.02).to(dt)
+    return W
+
+
+def _oracle(W, x, idx, w, out_in, gs, tag):
+    ref, _ = O.fused_batched_moe(np64(x), W["gate_up_packed"].numpy(), np64(W["gate_up_scales"]),
+                                 W["down_packed"].numpy(), np64(W["down_scales"]), idx.numpy(), np64(w),
+                                 np64(out_in), gs, dtype=tag)
+    return ref
+
+
+@pytest.fixture(scope="module", params=[(64, "fp16"), (128, "fp16"), (64, "fp32"), (128, "fp32")],
+                ids=lambda p: f"gs{p[0]}-{p[1]}")
+def gemma(request):
+    gs, tag = request.param
+    W = _moe_weights(E, H, I, gs, seed=800 + gs, dt=DT[tag])
+    return gs, tag, W, {k: v.to(DEV) for k, v in W.items()}
+
+
+@pytest.mark.parametrize("m,noise", [(1, 0.0), (7, 0.5), (9, 0.5)])
+def test_moe_gemma_shape(gemma, m, noise):
+    gs, tag, W, Wd = gemma
+    dt = DT[tag]
+    x = synth.activations(m, H, seed=810 + m).to(dt)
+    logits = synth.router_logits(m, E, seed=810 + m, verify_noise=noise)
+    top, idx = torch.topk(logits, 8, dim=-1)
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(dt)   # gemma.py:78-80, .type_as(x)
+    idx = idx.to(torch.int32)
+    out_in = (torch.randn(m, H, generator=torch.Generator().manual_seed(m)) * 0.1).to(dt)
+    out = out_in.to(DEV).clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert out.dtype == dt
+    assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, tag), tag, f"moe {tag} gs={gs} m={m}")
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+def test_moe_duplicates_invalid_ids_and_many_rows(tag):
+    dt = DT[tag]
+    e, h, i, k, gs = 8, 256, 128, 4, 64
+    W = _moe_weights(e, h, i, gs, seed=820, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    for m in (3, 64):
+        g = torch.Generator().manual_seed(821 + m)
+        idx = torch.randint(-1, e + 1, (m, k), generator=g, dtype=torch.int64)   # duplicates, -1 and E
+        w = torch.rand((m, k), generator=g).to(dt)
+        x = synth.activations(m, h, seed=822 + m).to(dt)
+        out = torch.zeros(m, h, dtype=dt, device=DEV)
+        gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                          Wd["down_packed"], Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+        torch.cuda.synchronize()
+        assert_dtype_close(out, _oracle(W, x, idx, w, torch.zeros(m, h), gs, tag), tag, f"dups {tag} m={m}")
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+def test_moe_reference_golden(tag):
+    g = np.load(GOLDEN / f"moe_m3_dups_gs64_{tag}.npz")
+    dt = DT[tag]
+    t = lambda k: torch.from_numpy(g[k]).to(DEV)  # noqa: E731
+    out = torch.zeros(g["x"].shape, dtype=dt, device=DEV)
+    gemmainfer_csrc.fused_batched_moe(t("x"), t("gate_up_packed"), t("gate_up_scales"), t("down_packed"),
+                                      t("down_scales"), t("idx"), t("w"), out, int(g["group_size"]))
+    torch.cuda.synchronize()
+    ref = g["out"].astype(np.float64)
+    st = O.error_stats(np64(out), ref)
+    # the reference rounds gate/up, each expert output and each accumulation to the dtype
+    assert st["rel_l2"] < (1e-5 if tag == "fp32" else 3e-3), st
+    assert st["max_abs_over_rms"] < (1e-4 if tag == "fp32" else 2e-2), st
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+@pytest.mark.parametrize("m,k,n,gs", [(1, 2816, 2816, 128), (6, 2816, 4096, 64), (33, 512, 200, 64),
+                                      (3, 2816, 64, 128)])
+def test_linear(tag, m, k, n, gs):
+    dt = DT[tag]
+    B, S = synth.linear_weights(k, n, gs, seed=830 + m)
+    A = synth.activations(m, k, seed=831 + m).to(dt)
+    S = S.to(dt)
+    C = torch.full((m, n), float("nan"), dtype=dt, device=DEV)   # overwritten
+    gemmainfer_csrc.marlin_w4a16(A.to(DEV), B.to(DEV), S.to(DEV), C, gs)
+    torch.cuda.synchronize()
+    ref = O.w4a16_linear(np64(A), B.numpy(), np64(S), gs)
+    assert_dtype_close(C, ref, tag, f"linear {tag} m={m} k={k} n={n} gs={gs}")
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+def test_linear_reference_golden_and_softcap(tag):
+    g = np.load(GOLDEN / f"linear_m3_k512_n128_gs128_{tag}.npz")
+    dt = DT[tag]
+    A, B, S = (torch.from_numpy(g[k]).to(DEV) for k in ("A", "B_packed", "scales"))
+    C = torch.empty(g["C"].shape, dtype=dt, device=DEV)
+    gemmainfer_csrc.marlin_w4a16(A, B, S, C, int(g["group_size"]))
+    torch.cuda.synchronize()
+    ref = g["C"].astype(np.float64)
+    got = np64(C)
+    if tag == "fp32":
+        np.testing.assert_allclose(got, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    else:
+        ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(ref), 2.0 ** -14))[1] - 11)
+        assert np.all(np.abs(got - ref) <= ulp), "more than one fp16 ulp from the reference"
+    # the lm_head epilogue cap * tanh(y / cap) (gemma.py:356-357) in the same dtype
+    y = ops.w4a16_linear(A * 8, B, S, int(g["group_size"]), softcap=30.0)
+    ref_c = O.softcap(O.w4a16_linear(np64(A * 8), g["B_packed"], g["scales"].astype(np.float64),
+                                     int(g["group_size"])), 30.0)
+    assert y.dtype == dt and float(y.abs().max()) <= 30.0
+    assert_dtype_close(y, ref_c, tag, f"softcap {tag}")

@@ -444,3 +444,54 @@ def test_oracle_against_reference_fallback_live():
     R.marlin_w4a16(A, B, S, C, 128)
     st = O.error_stats(t64(C), O.w4a16_linear(t64(A), B.numpy(), t64(S), 128))
     assert st["rel_l2"] < 4e-3, st
+
+
+# --------------------------------------------------------------------------- fp16 / fp32
+def test_round_to_matches_torch_casts():
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([
+        rng.standard_normal(100_000) * 10.0 ** rng.integers(-9, 6, 100_000),
+        # exact ties between two fp16 values, normal and subnormal
+        (np.arange(-3000, 3000) + 0.5).astype(np.float64) * 2.0 ** -10,
+        (np.arange(-300, 300) + 0.5).astype(np.float64) * 2.0 ** -24,
+        np.array([0.0, -0.0, 65504.0, 65520.0, -65520.0, 1e-9]),
+    ]).astype(np.float32).astype(np.float64)
+    theirs16 = torch.from_numpy(vals.astype(np.float32)).to(torch.float16).float().numpy().astype(np.float64)
+    np.testing.assert_array_equal(O.round_to(vals, "fp16"), theirs16)
+    np.testing.assert_array_equal(O.round_to(vals, "fp32"), vals)
+    np.testing.assert_array_equal(O.round_to(vals, "bf16"), O.bf16_round(vals))
+    with pytest.raises(ValueError):
+        O.round_to(vals, "fp8")
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+def test_linear_matches_reference_golden_other_dtypes(tag):
+    g = load(f"linear_m3_k512_n128_gs128_{tag}")
+    gs = int(g["group_size"])
+    y = O.round_to(O.w4a16_linear(g["A"].astype(np.float64), g["B_packed"], g["scales"].astype(np.float64), gs),
+                   tag)
+    ref = g["C"].astype(np.float64)
+    if tag == "fp32":   # float32 sums in the reference, float64 here
+        np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5 * np.abs(ref).max())
+    else:               # within one fp16 ulp
+        ulp = np.ldexp(1.0, np.frexp(np.maximum(np.abs(ref), 2.0 ** -14))[1] - 11)
+        assert np.all(np.abs(y - ref) <= ulp)
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
+def test_moe_matches_reference_golden_other_dtypes(tag):
+    g = load(f"moe_m3_dups_gs64_{tag}")
+    gs = int(g["group_size"])
+    x = g["x"].astype(np.float64)
+    out, _ = O.fused_batched_moe(x, g["gate_up_packed"], g["gate_up_scales"].astype(np.float64), g["down_packed"],
+                                 g["down_scales"].astype(np.float64), g["idx"], g["w"].astype(np.float64),
+                                 np.zeros_like(x), gs, dtype=tag)
+    ref = g["out"].astype(np.float64)
+    st = O.error_stats(O.round_to(out, tag), ref)
+    # the reference fallback also rounds gate/up, each expert output and each
+    # accumulation to the dtype; in fp32 only the sum order differs
+    if tag == "fp32":
+        assert st["rel_l2"] < 1e-5, st
+    else:
+        assert st["rel_l2"] < 3e-3, st
+        assert st["max_abs_over_rms"] < 2e-2, st
