@@ -180,14 +180,15 @@ def test_decode_kernel_small_hidden(gs, m):
     assert_bf16_close(out, ref, f"small hidden gs={gs} m={m}")
 
 
-def test_decode_kernel_wait_timeout_surfaces(signed128):
-    """spin_limit=1 makes the decode kernel's own bounded waits give up from the
-    host (every kernel still ends).  Outputs are then either right or NaN,
-    never a wrong finite value; the next call through the drop-in raises the
-    device error once (no synchronisation of its own), and the call after it
-    is right without any explicit status read or clear."""
+@pytest.mark.parametrize("m", [1, 7])
+def test_decode_kernel_wait_timeout_surfaces(signed128, m):
+    """spin_limit=1 makes the decode kernels' own bounded waits give up from the
+    host (every kernel still ends): the one-token kernel at M=1 (activation and
+    folded-unit waits), the 8-row kernel at M=7.  Outputs are then either right
+    or NaN, never a wrong finite value; the next call through the drop-in
+    raises the device error once (no synchronisation of its own), and the
+    call after it is right without any explicit status read or clear."""
     W, Wd = signed128
-    m = 7
     x = synth.activations(m, H, seed=600)
     idx, w = _routing(m, seed=600, noise=0.5)
     ref, _ = _oracle(W, x, idx, w, torch.zeros(m, H), 128)
