@@ -831,7 +831,7 @@ def pmc_reduce(fetch_csv, write_csv, out_path):
                 names[d] = r["Kernel_Name"]
         ids = sorted(vals)
         cal = [vals[d] for d in ids if "neg" in names[d].lower()][-3:]
-        lay = [vals[d] for d in ids if "moe_decode_kernel" in names[d] or "fused_moe" in names[d]]
+        lay = [vals[d] for d in ids if any(k in names[d] for k in ("moe_decode1_kernel", "moe_decode_kernel", "fused_moe"))]
         if len(cal) != 3 or not lay:
             raise SystemExit(f"{path}: expected 3 calibration and >= 1 layer dispatches")
         return cal, lay
