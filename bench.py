@@ -850,20 +850,22 @@ def pmc_reduce(fetch_csv, write_csv, out_path):
     print(json.dumps(res))
 
 
-def cpu_baseline(budget_s, max_reps):
-    """The reference's PyTorch CPU path on the same workload (M=1 layer),
-    bounded to about budget_s seconds of CPU work."""
+def cpu_baseline(budget_s, max_reps, m=1, noise=0.0, seed=1, warmup=True, W=None):
+    """The reference's PyTorch CPU path on the same workload (an M-row layer;
+    the headline line uses M=1), bounded to about budget_s seconds of CPU work."""
     from oracle import cpu_baseline as CB
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    W = synth.moe_weights(E, H, I, GS, seed=1)
-    x = synth.activations(1, H, seed=1)
-    logits = synth.router_logits(1, E, seed=1)
+    if W is None:
+        W = synth.moe_weights(E, H, I, GS, seed=1)
+    x = synth.activations(m, H, seed=seed)
+    logits = synth.router_logits(m, E, seed=seed, verify_noise=noise)
     top, idx = torch.topk(logits, TOP_K, dim=-1)           # gemma.py:77-80
     w = torch.softmax(top, dim=-1, dtype=torch.float32).to(torch.bfloat16)
     args = (x, idx, w, W["gate_up_packed"], W["gate_up_scales"], W["down_packed"], W["down_scales"], GS)
-    CB.moe_forward(*args)  # warmup
+    if warmup:
+        CB.moe_forward(*args)
     times = []
     t_start = time.perf_counter()
     while len(times) < max_reps and (time.perf_counter() - t_start) < budget_s:
@@ -883,10 +885,30 @@ def cpu_baseline(budget_s, max_reps):
         "us_per_layer": t * 1e6,
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{len(times)} timed reps (median) of one M=1 layer (U={u}) through "
+        "sample": (f"{len(times)} timed reps (median) of one M={m} layer (U={u}) through "
                    f"oracle/cpu_baseline.moe_forward, restating quant.py:67-75 + gemma.py:115-147; "
                    f"host {model}, torch {torch.__version__}"),
     }
+
+
+def cpu_table(budget_s):
+    """The reference's CPU path (oracle/cpu_baseline) on every BASELINE config,
+    each bounded to about budget_s seconds: the MoE layer at M=1, 7 and 512
+    (configs[1]-[3], the same routing draws as the GPU lines) and the W4A16
+    linear at configs[0] and configs[4] (lm_head on a column sample)."""
+    W = synth.moe_weights(E, H, I, GS, seed=1)
+    rows = {}
+    for key, m, noise, seed, warm in (("cfg1_M1", 1, 0.0, 1, True), ("cfg2_M7", 7, 0.5, 2, True),
+                                      ("cfg3_M512", 512, 0.0, 3, False)):
+        rows[key] = cpu_baseline(budget_s, 100000, m=m, noise=noise, seed=seed, warmup=warm, W=W)
+        print(f"[cpu] {key} {rows[key]['us_per_layer']:.0f} us ({rows[key]['cores']} cores)",
+              file=sys.stderr, flush=True)
+    del W
+    for key, name in (("cfg0_linear", "linear"), ("cfg4_lm_head", "lm_head")):
+        rows[key] = cpu_baseline_linear(name, budget_s)
+        print(f"[cpu] {key} {rows[key]['us_per_launch_sample']:.0f} us per sample launch",
+              file=sys.stderr, flush=True)
+    return {"cpu_table": rows}
 
 
 def main():
@@ -900,7 +922,7 @@ def main():
                     help="scale group size of the MoE weights of the headline line (configs[1]/[2] use 128; "
                          "the engine's checkpoints use 64, reported beside it in the default run)")
     ap.add_argument("--workload", choices=["moe", "prefill", "dense", "router", "stream", "timeline",
-                                           *LINEAR_WORKLOADS],
+                                           "cpu_table", *LINEAR_WORKLOADS],
                     default="moe",
                     help="moe (default: the BASELINE metric, M=1 value with M=7 beside it), prefill "
                          "(configs[3], M=512) or a dense W4A16 shape (linear = configs[0], "
@@ -912,6 +934,9 @@ def main():
     args = ap.parse_args()
     if args.pmc_reduce:
         pmc_reduce(*args.pmc_reduce)
+        return
+    if args.workload == "cpu_table":
+        print(json.dumps(cpu_table(args.cpu_budget_s)))
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's path runs on a single MI355X "

@@ -1,4 +1,4 @@
-"""Shared test helpers: tolerance gate and tensor conversion."""
+"""Shared test helpers: tolerance gate, tensor conversion and the parity record."""
 from __future__ import annotations
 
 import numpy as np
@@ -102,3 +102,13 @@ def assert_dtype_close(got: torch.Tensor, ref64: np.ndarray, dtype: str, what: s
     else:
         raise ValueError(dtype)
     return stats
+
+
+# Error statistics of the BASELINE configs' parity tests, by config name;
+# tests/conftest.py writes them to the JSON file named by GI_PARITY_STATS
+# at the end of the session (when that variable is set).
+PARITY_RECORD: dict = {}
+
+
+def record_parity(config: str, stats: dict, **extra) -> None:
+    PARITY_RECORD[config] = {**{k: float(v) for k, v in stats.items()}, **extra}

@@ -10,7 +10,7 @@ import torch
 from gemmainfer_amd import ops, synth
 from gemmainfer_amd import _lib as L
 from oracle import moe_oracle as O
-from tests.helpers import assert_bf16_close, assert_logits_close, np64
+from tests.helpers import assert_bf16_close, assert_logits_close, np64, record_parity
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -170,6 +170,8 @@ def test_fused_gemma_shapes_gs128(gemma128, m, noise):
     ref, al = _oracle_moe(x, W, idx_t, w_t, torch.zeros(m, 2816), 128)
     stats = assert_bf16_close(out, ref, f"gemma m={m}")
     print(f"m={m} U={al.num_unique} {stats}")
+    if (m, noise) in ((1, 0.0), (7, 0.5)):
+        record_parity("cfg1_M1" if m == 1 else "cfg2_M7", stats, unique_experts=al.num_unique)
 
 
 @pytest.mark.parametrize("m", [64, 512])
@@ -189,6 +191,8 @@ def test_prefill_grouped_gemm_gemma(gemma128, m):
     ref, al = _oracle_moe(x, W, idx_t, w_t, out_in, 128)
     stats = assert_bf16_close(out, ref, f"prefill m={m}")
     print(f"m={m} U={al.num_unique} {stats}")
+    if m == 512:
+        record_parity("cfg3_M512", stats, unique_experts=al.num_unique)
 
 
 def test_prefill_duplicates_invalid_skewed(small):
