@@ -279,9 +279,9 @@ def bench_stream(m, noise, seed, copies, steps, warmup, device, gs=None):
                      "bytes of one segment each, non-temporal 16-byte loads all issued before use"}
 
 
-D1_ROUTING_PHASES = ["routing inputs landed (wave 0)", "top-k done (wave 0)", None, None, "x staged (wave 1)",
-                     "previous footprint cleared (wave 1)", "logit keys (wave 0)", "radix select (wave 0)",
-                     "selection ranked (wave 0)", "softmax (wave 0)"]
+D1_ROUTING_PHASES = ["routing inputs landed (wave 0)", "wave 0 routing work done", None, None,
+                     "x staged (wave 1)", "previous footprint cleared", "logit keys in LDS (wave 0)",
+                     "top-k selected (wave 0)", None, "softmax (wave 0)"]
 TIMELINE_PHASES = {
     # decode kernel (up to 8 rows per launch): roles by whether the workgroup holds gate/up items
     (1, "item"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
@@ -290,11 +290,12 @@ TIMELINE_PHASES = {
                   "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
     # one-token kernel: item and unit workgroups
     (2, "item"): ["start", "routing", "weight loads issued", None, "gate/up products",
-                  "activations published", "folded partial sums published", None, None, "end",
-                  *D1_ROUTING_PHASES],
-    (2, "unit"): ["start", "routing", "weight loads issued", "words unpacked", "activations staged",
-                  "down products", "unit output written", "folded unit output written", None, "end",
-                  *D1_ROUTING_PHASES],
+                  "activations published", "folded partial sums published",
+                  "folded unit output written (items 0-7)", None, "end", *D1_ROUTING_PHASES],
+    (2, "unit"): ["start", "routing", "weight loads issued", "words unpacked", "activations staged (wave 0)",
+                  "down products", "unit output written", None, None, "end", *D1_ROUTING_PHASES,
+                  "activations staged (last expert's wave)", "products issued (wave 0)",
+                  "products done (wave 0)"],
     (2, "idle"): ["start", "routing", None, None, None, None, None, None, None, "end", *D1_ROUTING_PHASES],
 }
 

@@ -8,14 +8,16 @@
 //   down + combine csrc/marlin.cu:507-586
 //
 // A launch has G workgroups of 512 threads, one per CU, all resident.  Every
-// workgroup routes the token itself (wave 0; or reads the caller's ids) and
-// derives the same split of the work from the number U of unique experts
-// (in ascending id order), Tk = I/32 intermediate column tiles and
-// units = H/32 output column units:
+// workgroup routes the token itself (its threads rank the router logits, or
+// wave 0 reads the caller's ids) and derives the same split of the work from
+// the number U of unique experts (in rank order, for ids in the order of
+// their first slot), Tk = I/32 intermediate column tiles and units = H/32
+// output column units:
 //
 //   items   workgroups w < U*Tk.  Item (u, c): expert u's gate and up columns
 //           [32c, 32c+32) over all of H.  The words (16-byte loads, 11 per
-//           lane) go out right after the routing, then x is staged in LDS;
+//           lane) go out right after the routing, then x (loaded at the
+//           start) is staged in LDS;
 //           products on the matrix cores, the waves' sums added in LDS,
 //           act = bf16(gelu_tanh(gate) * up) (where the reference stores its
 //           activation, marlin.cu:421-423) published for the unit workgroups.
@@ -29,12 +31,12 @@
 //           arrived, the products run on the matrix cores (two (expert, k
 //           block) pairs per product: A rows 0 and 1 are the two pairs'
 //           activations, B columns 0-7 and 8-15 their words), the waves'
-//           sums are added in LDS and out is written once.  Unit d < n_left
-//           then also sums folded unit n_whole + d from the items' partial
-//           sums, which are ready by then.
+//           sums are added in LDS and out is written once.
 //   folded  units [n_whole, units) have no workgroup of their own (8 of 88 at
-//           U = 8 on 256 CUs); their products come from the items, so no
-//           second wait is added.
+//           U = 8 on 256 CUs); their products come from the items, and item
+//           f < n_left, once its own work is done, sums folded unit
+//           n_whole + f from every item's partial sums (a wait between
+//           items, off the units' path).
 //
 // At U = 8, 176 items of 92.9 KB (+ 4.5 KB of folded down words) and 80 units
 // of 93.2 KB: every CU streams about the same bytes (24.56 MB / 256 = 95.9 KB).
@@ -46,9 +48,10 @@
 // of I values, matrix-core k order within each 8); partial sums, inverted,
 // into the partial buffer ([item][n_left * 32] fp32).  A stored 16-bit (32-bit)
 // value is never all ones (canonical NaN), so all-zero means "not written
-// yet" and readers poll the data itself, with a bounded wait.  At its start
-// every workgroup clears its share of what the previous launch wrote into the
-// other parity (the footprint in the epoch word), during the routing wait.
+// yet" and readers poll the data itself, with a bounded wait.  The idle
+// workgroups (else the units, while they wait for the activations; else all)
+// clear what the previous launch wrote into the other parity (the footprint
+// in the epoch word).
 
 #include <mutex>
 
@@ -122,14 +125,16 @@ struct D1Args {
   int overwrite, spin_limit;
 };
 
+constexpr int kRankKeys = 128;  // router logits ranked by all threads up to this many experts
+
 struct D1Pro {
   int slot_e[kSlots];
   float slot_w[kSlots];
-  uint32_t sel_key[kSlots];   // routing from logits: the selected keys, expert scales and places
-  float sel_es[kSlots];       // in the id order, by rank
-  int sel_pos[kSlots];
-  uint32_t id_key[kSlots];    // the same in id order
+  uint32_t sel_key[kSlots];   // routing from logits: the selected keys and expert scales by rank
+  float sel_es[kSlots];
+  uint32_t id_key[kSlots];    // the same in id order (radix select)
   float id_es[kSlots];
+  int rpart[kW][kRankKeys];   // rank select: wave w's count of its keys above each key
   int uexp[kMaxU];
   float uw[kMaxU];
   float cb[kMaxH / 8];        // -24 * the sum of each 8-value chunk of x (zero past the scale groups)
@@ -143,14 +148,13 @@ struct ItemLds {
   float4 red[kW][16];             // per-wave sums: lane lr holds 4 gate (lr < 8) or up columns
   uint4 sa[4];                    // the item's 32 activations, matrix-core k order
   float4 fr[4][kMaxLeft * 8];     // folded products per packed row
+  float4 rr[kW][8];               // folded unit reduction: each wave's sums (8 column quads)
 };
 struct UnitLds {
   uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 in matrix-core k order
   float cbias[kMaxU * kMaxTk * 4];  // -24 * each chunk's sum
-  float kbias[kMaxU * kMaxTk];      // the same per k block (4 chunks)
   uint4 dsc[kMaxU * kMaxGd * 4];    // down scales of the unit's columns [u][g][32]
   float4 red[kW][16];
-  float4 rr[kW][8];                 // folded unit: each wave's partial sums (8 column quads)
 };
 union D1Lds {
   ItemLds it;
@@ -226,22 +230,77 @@ __device__ __forceinline__ void d1_issue(const D1Args& a, D1In<VPL>& in) {
   }
 }
 
-// Router logits, wave 0 (gemma.py:77-80; the tie rule of route_finish: value
-// descending, then index ascending, NaN highest), in two parts.
+// Router logits (gemma.py:77-80; the tie rule of route_finish: value
+// descending, then index ascending, NaN highest).  Both forms leave the
+// top_k experts in rank order: P.uexp (the unique experts, which is all the
+// weight loads need), P.slot_e, P.sel_key and P.sel_es, and P.U = top_k.
+// The softmax waits until the weight loads are in flight (d1_weights).
 //
-// d1_select (before the weight loads): a radix select finds the top_k-th
-// largest key T, two bits per step (three candidate prefixes counted at once
-// with ballots and popcounts), first over the high 16 bits of the keys and,
-// only when that leaves a tie at the boundary, over the low 16; the
-// selection is every key above T and the lowest-index keys equal to T.  The
-// unique experts are the selection in ascending id order (P.uexp), which is
-// all the weight loads need.
+// Up to kRankKeys experts (d1_rank_count, d1_rank_pick): every wave loads the
+// router row (lane l: experts l and l + 64) and forms each expert's composite
+// key (key << 10 | (1023 - expert): a higher value, then the lower index, is
+// larger; padding experts past E get key 0, below every real key).  Wave w
+// broadcasts its 16 keys j = 16w .. 16w+15 (readlane) and counts, for all 128
+// keys, how many of its 16 are larger; after a barrier thread i < 128 adds the
+// 8 waves' counts, the rank of key i, and writes expert i at its rank when
+// that is below top_k.
 //
-// d1_weights (while the loads are in flight): the selection ranked by key
-// (top_k steps over the selected keys in LDS), route_softmax over it in rank
-// order (the arithmetic of route_finish), each weight stored at its expert's
-// place in the id order (P.uw) and the rank order kept for the routing report
-// (P.slot_e, P.slot_w).
+// More experts (d1_select, d1_rank_radix; wave 0): a radix select finds the
+// top_k-th largest key T, two bits per step (three candidate prefixes counted
+// at once with ballots and popcounts), first over the high 16 bits of the
+// keys and, only when that leaves a tie at the boundary, over the low 16; the
+// selection is every key above T and the lowest-index keys equal to T, which
+// top_k steps over the selected keys then rank.
+struct RankKeys {
+  unsigned long long c[2];  // composite keys of experts lane, lane + 64
+  float es[2];              // their expert scales
+};
+
+__device__ __forceinline__ void d1_rank_count(const D1Args& a, D1Pro& P, const RouteIn<2>& r, RankKeys& k) {
+  const int lane = threadIdx.x & (kWave - 1), wave = uniform(threadIdx.x >> 6);
+  const bool bf = a.logits_dtype == GI_DTYPE_BF16;
+#pragma unroll
+  for (int v = 0; v < 2; ++v) {
+    const int e = lane + v * kWave;
+    const float f = __uint_as_float(bf ? r.raw[v] << 16 : r.raw[v]);
+    const uint32_t key = e < a.E ? orderable_key(f) : 0u;  // a real key is never 0
+    k.c[v] = ((unsigned long long)key << 10) | (unsigned long long)(1023 - e);
+    k.es[v] = a.expert_scale ? __uint_as_float(r.es[v]) : 1.f;
+  }
+  // keys j = 16w + jj: lane (16w + jj) % 64 of c[w / 4]
+  const unsigned long long src = wave < 4 ? k.c[0] : k.c[1];
+  const uint32_t src_lo = (uint32_t)src, src_hi = (uint32_t)(src >> 32);
+  const int l0 = (wave & 3) * 16;
+  int n0 = 0, n1 = 0;
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)src_lo, l0 + jj);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)src_hi, l0 + jj);
+    const unsigned long long cj = ((unsigned long long)hi << 32) | lo;
+    n0 += cj > k.c[0] ? 1 : 0;
+    n1 += cj > k.c[1] ? 1 : 0;
+  }
+  P.rpart[wave][lane] = n0;
+  P.rpart[wave][kWave + lane] = n1;
+}
+
+// Threads i < 128 (waves 0 and 1: key i is c[i / 64] of lane i % 64), after
+// the barrier that published P.rpart.
+__device__ __forceinline__ void d1_rank_pick(const D1Args& a, D1Pro& P, const RankKeys& k) {
+  const int i = threadIdx.x;
+  int rank = 0;
+#pragma unroll
+  for (int w = 0; w < kW; ++w) rank += P.rpart[w][i];
+  const int v = i >> 6;
+  const unsigned long long ci = v ? k.c[1] : k.c[0];
+  if (i < a.E && rank < a.top_k) {
+    P.uexp[rank] = i;
+    P.slot_e[rank] = i;
+    P.sel_key[rank] = (uint32_t)(ci >> 10);
+    P.sel_es[rank] = v ? k.es[1] : k.es[0];
+  }
+}
+
 template <int VPL>
 __device__ __forceinline__ int count_ge(const uint32_t (&key)[VPL], uint32_t t) {
   int c = 0;
@@ -276,7 +335,6 @@ __device__ __forceinline__ void d1_select(const D1Args& a, D1Pro& P, const Route
       else break;
     }
   }
-  GI_STAMP(17);
   // the selection: keys above T, then keys equal to T in index order; in
   // ascending id order, with each one's key and expert scale
   int n_gt = 0;
@@ -300,12 +358,15 @@ __device__ __forceinline__ void d1_select(const D1Args& a, D1Pro& P, const Route
     pos_base += __popcll(m);
   }
   if (lane == 0) P.U = K;
+  GI_STAMP(17);
 }
 
-// Wave 0, after the barrier that published P.uexp / id_key / id_es.
-__device__ __forceinline__ void d1_weights(const D1Args& a, D1Pro& P) {
+// Wave 0, after d1_select: the selection (in id order) ranked by key; a lower
+// place in the id order is a lower index.
+__device__ __forceinline__ void d1_rank_radix(const D1Args& a, D1Pro& P) {
   const int lane = threadIdx.x & (kWave - 1);
   const int K = a.top_k;
+  lds_fence();
   const int j = lane < K ? lane : 0;
   const uint32_t kj = P.id_key[j];
   const int ej = P.uexp[j];
@@ -313,31 +374,41 @@ __device__ __forceinline__ void d1_weights(const D1Args& a, D1Pro& P) {
   int rank = 0;
   for (int i = 0; i < K; ++i) {
     const uint32_t ki = (uint32_t)__builtin_amdgcn_readlane((int)kj, i);
-    rank += (ki > kj) + (ki == kj && i < lane);  // id order: a lower place is a lower index
+    rank += (ki > kj) + (ki == kj && i < lane);
   }
-  if (lane < K) {
+  if (lane < K) {  // every lane has read P.uexp above (one wave, program order)
+    P.uexp[rank] = ej;
     P.slot_e[rank] = ej;
     P.sel_key[rank] = kj;
     P.sel_es[rank] = esj;
-    P.sel_pos[rank] = lane;
   }
-  lds_fence();
-  GI_STAMP(18);
+}
+
+// Wave 0, while the weight loads are in flight: route_softmax over the
+// selection in rank order (the arithmetic of route_finish); each weight,
+// rounded to bf16, is the weight of the unique expert at the same place
+// (P.uw) and is kept for the routing report (P.slot_w).
+__device__ __forceinline__ void d1_weights(const D1Args& a, D1Pro& P) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int K = a.top_k;
   const int rr = lane < K ? lane : 0;
   route_softmax(a, lane, P.slot_e[rr], P.sel_key[rr], P.sel_es[rr], P.slot_e, P.slot_w);
   lds_fence();
   if (lane < K) {
     const float w = round_to_bf16(P.slot_w[lane]);
     P.slot_w[lane] = w;  // reported by workgroup 0 at the end
-    P.uw[P.sel_pos[lane]] = w;
+    P.uw[lane] = w;
   }
   GI_STAMP(19);
 }
 
 // Wave 0, the caller's ids: the slots' experts and weights, then the
 // unique experts; a slot whose expert an earlier slot has is merged into that
-// one (weights added in slot order), invalid ids are dropped.  The weights are rounded to bf16 (the reference
-// casts them to the activation dtype, marlin.cu:634-636).
+// one (weights added in slot order), invalid ids are dropped.  The weights are
+// rounded to bf16 (the reference casts them to the activation dtype,
+// marlin.cu:634-636).  The unique experts are in the order of their first
+// slot: for ids from a sorted top-k (gemma.py:77-80) that is the rank order
+// of the router-logits form, so both forms split the work alike.
 template <int VPL>
 __device__ __forceinline__ void d1_route_ids(const D1Args& a, D1Pro& P, const D1In<VPL>& in) {
   const int lane = threadIdx.x & (kWave - 1);
@@ -376,18 +447,9 @@ __device__ __forceinline__ void d1_route_ids(const D1Args& a, D1Pro& P, const D1
       }
     }
   }
-  // the unique experts in ascending id order (as with router logits, so
-  // that both entry points split the work alike): place = the number of
-  // unique experts with a lower id
   const bool keep = lane < S && e >= 0 && first;
   const unsigned long long bal = __ballot(keep);
-  int u = 0;
-  unsigned long long m = bal;
-  while (m) {
-    const int j = __builtin_ctzll(m);
-    m &= m - 1ull;
-    u += __builtin_amdgcn_readlane(e, j) < e;
-  }
+  const int u = __popcll(bal & ((1ull << lane) - 1ull));
   if (keep && u < kMaxU) {
     P.uexp[u] = e;
     P.uw[u] = ws;
@@ -395,66 +457,81 @@ __device__ __forceinline__ void d1_route_ids(const D1Args& a, D1Pro& P, const D1
   if (lane == 0) P.U = __popcll(bal);
 }
 
-// This workgroup's share of what the previous launch wrote into the other
-// parity's buffers (16-byte stores by threads t0 .. t0 + nthr - 1).
-__device__ __forceinline__ void clear_prev(const D1Args& a, unsigned long long ew, int parity, int t0, int nthr) {
-  const int b = blockIdx.x, G = gridDim.x;
+// Share `slot` of `nslots` of what the previous launch wrote into the other
+// parity's buffers (16-byte stores by all threads; the footprint is in the
+// epoch word ew, stores past it fall outside the buffer resources).
+__device__ __forceinline__ void clear_prev(const D1Args& a, unsigned long long ew, int parity, int slot,
+                                           int nslots) {
   const uint32_t act_b = moe_state::epoch_act_units(ew) * moe_state::kUnit;
   const uint32_t part_b = moe_state::epoch_part_units(ew) * moe_state::kUnit;
   const u32x4_t z = {0u, 0u, 0u, 0u};
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.act + (size_t)(parity ^ 1) * kActParity, act_b);
   const __amdgpu_buffer_rsrc_t rp = buffer_rsrc(a.part + (size_t)(parity ^ 1) * kPartParity, part_b);
   const int na = (int)(act_b / 16), np = (int)(part_b / 16);
-  const int pa = (na + G - 1) / G, pp = (np + G - 1) / G;
-  for (int i = (int)threadIdx.x - t0; i < pa; i += nthr)
-    __builtin_amdgcn_raw_buffer_store_b128(z, ra, (uint32_t)(b * pa + i) * 16u, 0, kCpolAgent);
-  for (int i = (int)threadIdx.x - t0; i < pp; i += nthr)
-    __builtin_amdgcn_raw_buffer_store_b128(z, rp, (uint32_t)(b * pp + i) * 16u, 0, kCpolAgent);
+  const int pa = (na + nslots - 1) / nslots, pp = (np + nslots - 1) / nslots;
+  for (int i = (int)threadIdx.x; i < pa; i += kT)
+    __builtin_amdgcn_raw_buffer_store_b128(z, ra, (uint32_t)(slot * pa + i) * 16u, 0, kCpolAgent);
+  for (int i = (int)threadIdx.x; i < pp; i += kT)
+    __builtin_amdgcn_raw_buffer_store_b128(z, rp, (uint32_t)(slot * pp + i) * 16u, 0, kCpolAgent);
 }
 
 // The start of every workgroup: the routing inputs go out first (wave 0),
-// then the epoch word and x (which do not depend on the routing).  Waves 1-7
-// stage x in LDS in the matrix-core k order with each chunk's offset sum
-// (every workgroup: the role is not known yet) and clear the previous
-// launch's footprint while wave 0 routes.  Ends with the routing in LDS
-// (P.U, uexp, uw) after one barrier.
+// then the epoch word and x, which do not depend on the routing (x stays in
+// registers, thread c holding 16-byte chunk c, until the workgroup knows its
+// role).  Ends with the routing in LDS (P.U, P.uexp; from router logits also
+// the selection in rank order) after the last barrier.
 template <int VPL>
-__device__ __forceinline__ void d1_start(const D1Args& a, D1Pro& P, ItemLds& LI, int* parity_out) {
+__device__ __forceinline__ void d1_start(const D1Args& a, D1Pro& P, u32x4_t* xv_out, int* parity_out) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
+  constexpr bool kRank = VPL * kWave <= kRankKeys;
   D1In<VPL> in;
-  if (wave == 0) d1_issue<VPL>(a, in);
+  if (wave == 0 || (kRank && a.logits)) d1_issue<VPL>(a, in);  // from logits, every wave ranks
   const u32x2_t ev = __builtin_amdgcn_raw_buffer_load_b64(buffer_rsrc(a.epochs, (uint32_t)kEpochSlots * 8u),
                                                           blockIdx.x * 8u, 0, kCpolAgent);
-  // x: thread 64 + c loads 16-byte chunk c of the row (past H: zeros)
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.x, (uint32_t)a.H * 2u);
-  const u32x4_t xv = __builtin_amdgcn_raw_buffer_load_b128(rx, tid >= kWave ? (uint32_t)(tid - kWave) * 16u : kOob, 0, 0);
+  *xv_out = __builtin_amdgcn_raw_buffer_load_b128(rx, tid < kMaxH / 8 ? (uint32_t)tid * 16u : kOob, 0, 0);
+  RankKeys rk;
+  if constexpr (kRank) {
+    if (a.logits) {
+#ifdef GI_TIMELINE
+      __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): the routing inputs (the epoch word and x are younger)
+      GI_STAMP(10);
+#endif
+      d1_rank_count(a, P, in.r, rk);
+      GI_STAMP(16);
+    }
+  }
   if (wave == 0) {
 #ifdef GI_TIMELINE
-    __builtin_amdgcn_s_waitcnt(0x0F72);  // vmcnt(2): the routing inputs (the epoch word and x are younger)
-    GI_STAMP(10);
+    if (!(kRank && a.logits)) {
+      __builtin_amdgcn_s_waitcnt(0x0F72);
+      GI_STAMP(10);
+    }
 #endif
-    if (a.logits) d1_select<VPL>(a, P, in.r);
-    else d1_route_ids<VPL>(a, P, in);
+    if (a.logits) {
+      if constexpr (!kRank) {
+        d1_select<VPL>(a, P, in.r);
+        d1_rank_radix(a, P);
+      } else if (tid == 0) {
+        P.U = a.top_k;
+      }
+    } else {
+      d1_route_ids<VPL>(a, P, in);
+    }
     GI_STAMP(11);
     if (tid == 0) {
       P.bad = 0;
       P.epoch = ((unsigned long long)ev.y << 32) | ev.x;
     }
-  } else {
-    const int c = tid - kWave;
-    const int Kv8 = min(a.H >> 3, a.Ggu << (a.gsh + 2));  // packed rows inside the gate/up scale groups
-    if (c < kMaxH / 8) {
-      const uint4 v = make_uint4(xv.x, xv.y, xv.z, xv.w);
-      LI.xs[c] = c < Kv8 ? mfma_k_order(v) : make_uint4(0u, 0u, 0u, 0u);
-      P.cb[c] = c < Kv8 ? q4_bias(v) : 0.f;
-    }
-    GI_STAMP_BY(14, kWave);
-    const unsigned long long ew = ((unsigned long long)ev.y << 32) | ev.x;
-    const int parity = (int)((moe_state::epoch_count(ew) + 1ull) & 1ull);
-    clear_prev(a, ew, parity, kWave, kT - kWave);
-    GI_STAMP_BY(15, kWave);
   }
   lds_barrier();
+  if constexpr (kRank) {
+    if (a.logits) {
+      if (tid < kRankKeys) d1_rank_pick(a, P, rk);
+      GI_STAMP(17);
+      lds_barrier();
+    }
+  }
   *parity_out = (int)((moe_state::epoch_count(P.epoch) + 1ull) & 1ull);
 }
 
@@ -466,11 +543,18 @@ struct ItemRegs {
   uint4 w[kKbw];    // this lane's words: packed rows 4kb + lq of the wave's k blocks
   uint4 fw;         // folded down word: 4 columns x 8 rows
   uint2 fs;         // its scales
+  uint32_t old;     // folded unit `item` (item < n_left, accumulating calls): previous output bits (t < 32)
 };
 
-__device__ __forceinline__ void item_load(const D1Args& a, int e, int c, int Kv8, int n_whole, int n_left,
+__device__ __forceinline__ void item_load(const D1Args& a, int e, int it, int c, int Kv8, int n_whole, int n_left,
                                           ItemRegs& r) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  {
+    // folded unit n_whole + it, summed by this item (it < n_left)
+    const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(a.out, a.overwrite ? 0u : (uint32_t)a.H * 2u);
+    const uint32_t off = (tid < 32 && it < n_left) ? (uint32_t)(32 * (n_whole + it) + tid) * 2u : kOob;
+    r.old = __builtin_amdgcn_raw_buffer_load_b16(ro, off, 0, 0);
+  }
   const int lq = lane >> 4, lr = lane & 15;
   const int twoI = 2 * a.I;
   const int col = (lr < 8 ? 0 : a.I) + 32 * c + 4 * (lr & 7);
@@ -630,7 +714,7 @@ template <int NS>
 struct UnitRegs {
   uint4 w[NS];
   uint4 sc;      // one down-scale chunk (staged into LDS)
-  uint32_t old;  // previous output bits (accumulating calls): this unit's (t < 32), the folded unit's (32 <= t < 64)
+  uint32_t old;  // previous output bits of this unit (accumulating calls, t < 32)
 };
 
 template <int NS>
@@ -640,9 +724,7 @@ __device__ __forceinline__ void unit_load(const D1Args& a, const D1Pro& P, int d
   const int lq = lane >> 4, lr = lane & 15;
   const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(a.out, a.overwrite ? 0u : (uint32_t)a.H * 2u);
   {
-    const int colm = 32 * d + (tid & 31);
-    const int colf = 32 * (n_whole + d) + (tid & 31);
-    const uint32_t off = tid < 32 ? (uint32_t)colm * 2u : (tid < 64 && d < n_left) ? (uint32_t)colf * 2u : kOob;
+    const uint32_t off = tid < 32 ? (uint32_t)(32 * d + tid) * 2u : kOob;
     r.old = __builtin_amdgcn_raw_buffer_load_b16(ro, off, 0, 0);
   }
   // down scales of the unit's columns: chunk ch = (u * Gd + g) * 4 + q holds columns 8q .. 8q+7
@@ -670,37 +752,37 @@ __device__ __forceinline__ void unit_load(const D1Args& a, const D1Pro& P, int d
   __builtin_amdgcn_sched_barrier(0);
 }
 
-// Polls n chunks (16 bytes each, tid + kT*j) of `src` into dst (all of them
-// present: no 16-bit half zero), inverted back, with each chunk's -24 * sum
-// of its 8 values into bias.  Bounded: on timeout the status word and host
-// flag are set, *bad is set and the wave goes on.
+// One wave polls the n chunks (16 bytes each, lane + 64j) of `src` into dst
+// (all of them present: no 16-bit half zero), inverted back, with each
+// chunk's -24 * sum of its 8 values into bias.  Bounded: on timeout the status
+// word and host flag are set, *bad is set and the wave goes on.
 template <int CPT>
 __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buffer_rsrc_t src, uint4* dst,
                                             float* bias, int n, int* bad) {
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
   uint32_t pending = 0u;
 #pragma unroll
   for (int j = 0; j < CPT; ++j)
-    if (tid + j * kT < n) pending |= 1u << j;
+    if (lane + j * kWave < n) pending |= 1u << j;
   int spins = 0;
   while (true) {
     u32x4_t v[CPT];
 #pragma unroll
     for (int j = 0; j < CPT; ++j)
-      v[j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((pending >> j) & 1u) ? (uint32_t)(tid + j * kT) * 16u : kOob,
+      v[j] = __builtin_amdgcn_raw_buffer_load_b128(src, ((pending >> j) & 1u) ? (uint32_t)(lane + j * kWave) * 16u : kOob,
                                                    0, kCpolAgent);
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
       if (((pending >> j) & 1u) && chunk_ready(v[j])) {
         const uint4 x = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
-        dst[tid + j * kT] = x;
-        bias[tid + j * kT] = q4_bias(x);
+        dst[lane + j * kWave] = x;
+        bias[lane + j * kWave] = q4_bias(x);
         pending &= ~(1u << j);
       }
     }
     if (__ballot(pending != 0u) == 0ull) break;
     if (++spins >= a.spin_limit) {
-      if ((threadIdx.x & (kWave - 1)) == 0) {
+      if (lane == 0) {
         report_timeout(a.status, a.host_flag);
         *bad = 1;
       }
@@ -721,10 +803,18 @@ __device__ __forceinline__ void folded_poll(const __amdgpu_buffer_rsrc_t rp, int
         rp, ((pending >> j) & 1u) ? (uint32_t)(((st + 64 * j) * stride + 32 * d + 4 * cq) * 4) : kOob, 0, kCpolAgent);
 }
 
+// The products of one scale group, finished: y += scale * (the group's sum +
+// its -24 * sum of activations); lanes lr < 8 take A row 0 (k block 2s),
+// lanes lr >= 8 row 1 (k block 2s + 1).
+__device__ __forceinline__ void group_epilogue(float (&y)[4], const f32x4_t (&D)[4], uint2 s2, float bacc, int h) {
+  const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i] += sc[i] * ((h ? D[i][1] : D[i][0]) + bacc);
+}
+
 template <int NS, int GSH>
-__device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, int d, int U, int n_items,
-                                         int n_whole, int n_left, const char* act, const char* part,
-                                         const UnitRegs<NS>& r) {
+__device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, int d, int U, const char* act,
+                                         const UnitRegs<NS>& r, int parity, int cslot, int nslots) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int lq = lane >> 4, lr = lane & 15, h = lr >> 3;
   const int Tk = a.Tk, cps = a.I >> 3;
@@ -746,74 +836,81 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(B[s][i].x), "+v"(B[s][i].y), "+v"(B[s][i].z), "+v"(B[s][i].w));
   }
   GI_STAMP(3);
-  // every activation of the U experts, and each k block's -24 * sum
-  poll_chunks<2>(a, buffer_rsrc(act, (uint32_t)(U * a.I * 2)), L.sact, L.cbias, U * cps, bad);
-  lds_barrier();
-  if (tid < U * Tk) {
-    const float* cb = L.cbias + 4 * tid;
-    L.kbias[tid] = ((cb[0] + cb[1]) + cb[2]) + cb[3];
+  // the previous launch's footprint (clearing workgroups): the stores go out
+  // while the activations are computed elsewhere
+  if (cslot >= 0) {
+    clear_prev(a, P.epoch, parity, cslot, nslots);
+    GI_STAMP(15);
   }
-  lds_barrier();
-  GI_STAMP(4);
-  // folded unit (d < n_left): the first poll of the items' partial sums goes
-  // out now, its answer is read after the products
-  const int fcq = tid & 7, fst = tid >> 3;
-  const int fstride = n_left * 32;  // floats per item
-  const __amdgpu_buffer_rsrc_t frp = buffer_rsrc(part, d < n_left ? (uint32_t)(n_items * fstride * 4) : 0u);
-  uint32_t fpend = 0u;
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    if (d < n_left && fst + 64 * j < n_items) fpend |= 1u << j;
-  u32x4_t fv[4];
-  folded_poll(frp, fst, d, fcq, fstride, fpend, fv);
+  lds_barrier();  // the down scales staged by every wave
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
   const int u = wave;
   const int uc = min(u, kMaxU - 1);
   const int gsh = gsh_of<GSH>(a);
   const int gpb_m1 = (1 << gsh) - 1;  // k blocks per scale group - 1 (odd: groups hold whole steps)
-  f32x4_t D[4] = {zf, zf, zf, zf};
-  float bacc = 0.f;
   float y[4] = {0.f, 0.f, 0.f, 0.f};
   if (u < U) {
-    // lane l holds k block l's -24 * sum of the expert's activations
-    const float kv = L.kbias[uc * Tk + min(lane, Tk - 1)];
-    // A rows 0, 1: k blocks 2s, 2s+1 (lanes lr < 2), read one step ahead
+    // wave u waits for expert u's activations only (its products start as
+    // soon as they are there), with each chunk's -24 * sum
+    poll_chunks<2>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps,
+                   L.cbias + u * cps, cps, bad);
+    GI_STAMP(4);
+    GI_STAMP_BY(20, (U - 1) * kWave);
+    // lane l holds k block l's -24 * sum of the expert's activations (this
+    // wave's own LDS writes, read back in order)
+    const float* cb = L.cbias + u * cps + 4 * min(lane, Tk - 1);
+    const float kv = ((cb[0] + cb[1]) + cb[2]) + cb[3];
+    // A rows 0, 1: k blocks 2s, 2s+1 (lanes lr < 2), read three steps ahead
     const int rowoff = uc * cps + lq;
-    uint4 an = L.sact[rowoff + min(4 * (lr & 1), cps - 4)];
-    uint2 s2 = make_uint2(0u, 0u);
+    constexpr int kAhead = 3;
+    uint4 an[kAhead];
+#pragma unroll
+    for (int s = 0; s < kAhead; ++s) an[s] = L.sact[rowoff + min(4 * (2 * s + (lr & 1)), cps - 4)];
+    // two accumulator sets, alternating by scale group: a group's scale is
+    // applied after the next group's products are issued, so that the
+    // epilogue does not wait for the matrix cores (the sets are named, not
+    // indexed, so that they stay in registers when the group size is a
+    // run-time value)
+    f32x4_t D0[4], D1[4];
+    uint2 s20 = make_uint2(0u, 0u), s21 = make_uint2(0u, 0u);
+    float bacc0 = 0.f, bacc1 = 0.f;
+    auto step = [&](int s, const uint4& A, bool gstart, bool epi, int g, f32x4_t(&Dc)[4], uint2& s2c, float& bc,
+                    const f32x4_t(&Dp)[4], uint2 s2p, float bp) {
+      if (gstart) {
+        const int gg = min(g, a.Gd - 1);
+        s2c = *(const uint2*)((const uint16_t*)&L.dsc[(uc * a.Gd + gg) * 4] + 4 * (lr & 7));
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Dc[i] = mfma_bf16(A, B[s][i], gstart ? zf : Dc[i]);
+      const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
+      const float b1 = 2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
+      bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
+      if (epi) group_epilogue(y, Dp, s2p, bp, h);
+    };
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int kba = 2 * s + (lr & 1);
-      const uint4 A = (lr < 2 && kba < Tk) ? an : z4;
-      if (s + 1 < NS) an = L.sact[rowoff + min(4 * (kba + 2), cps - 4)];
-      if (((2 * s) & gpb_m1) == 0) {  // a scale group starts: its scales, used at its end
-        const int g = min((2 * s) >> gsh, a.Gd - 1);
-        s2 = *(const uint2*)((const uint16_t*)&L.dsc[(uc * a.Gd + g) * 4] + 4 * (lr & 7));
-      }
-      D[0] = mfma_bf16(A, B[s][0], D[0]);
-      D[1] = mfma_bf16(A, B[s][1], D[1]);
-      D[2] = mfma_bf16(A, B[s][2], D[2]);
-      D[3] = mfma_bf16(A, B[s][3], D[3]);
-      const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
-      const float b1 = 2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
-      bacc += h ? b1 : b0;
-      if (((2 * s + 1) & gpb_m1) == gpb_m1 || s == NS - 1) {  // the scale group ends with this step
-        const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          y[i] += sc[i] * ((h ? D[i][1] : D[i][0]) + bacc);
-          D[i] = zf;
-        }
-        bacc = 0.f;
-      }
+      const uint4 A = (lr < 2 && kba < Tk) ? an[s % kAhead] : z4;
+      if (s + kAhead < NS) an[s % kAhead] = L.sact[rowoff + min(4 * (kba + 2 * kAhead), cps - 4)];
+      const int g = (2 * s) >> gsh;
+      const bool gstart = ((2 * s) & gpb_m1) == 0;
+      const bool epi = gstart && g > 0;
+      if ((g & 1) == 0) step(s, A, gstart, epi, g, D0, s20, bacc0, D1, s21, bacc1);
+      else step(s, A, gstart, epi, g, D1, s21, bacc1, D0, s20, bacc0);
     }
+    GI_STAMP(21);
+    if ((((2 * (NS - 1)) >> gsh) & 1) == 0) group_epilogue(y, D0, s20, bacc0, h);
+    else group_epilogue(y, D1, s21, bacc1, h);
+#ifdef GI_TIMELINE
+    asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
+#endif
+    GI_STAMP(22);
   }
   const float wu = u < U ? P.uw[uc] : 0.f;
   if (lq == 0) L.red[wave][lr] = make_float4(wu * y[0], wu * y[1], wu * y[2], wu * y[3]);
   lds_barrier();
   GI_STAMP(5);
-  const float nan = __uint_as_float(0x7fc00000u);
   if (tid < 32) {
     float sacc = 0.f;
 #pragma unroll
@@ -822,19 +919,34 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
       sacc += ((const float*)&L.red[w2][8 + (tid >> 2)])[tid & 3];
     }
     if (!a.overwrite) sacc += bf16_to_f32(r.old & 0xffffu);
-    if (P.bad) sacc = nan;  // never a wrong finite value
+    if (P.bad) sacc = __uint_as_float(0x7fc00000u);  // never a wrong finite value
     a.out[32 * d + tid] = f32_to_bf16(sacc);
   }
   GI_STAMP(6);
-  if (d >= n_left) return;
-  // folded unit n_whole + d: the items' partial sums of its 32 columns, 64
-  // item streams (items st, st + 64, ...) x 8 column quads, fixed order; the
-  // first poll went out before the products
+}
+
+// Folded unit n_whole + f (item f < n_left, after its own work): the items'
+// partial sums of its 32 columns, 64 item streams (items st, st + 64, ...) x
+// 8 column quads, polled with a bounded wait and added in a fixed order: each
+// thread's items in order, then the wave's 8 streams (xor 8, 16, 32), then
+// the 8 waves in order; one bf16 rounding (plus the previous output).
+__device__ __forceinline__ void folded_reduce(const D1Args& a, D1Pro& P, float4 (&rr)[kW][8], int f, int n_items,
+                                              int n_whole, int n_left, const char* part, uint32_t old) {
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int fcq = tid & 7, fst = tid >> 3;
+  const int fstride = n_left * 32;  // floats per item
+  const __amdgpu_buffer_rsrc_t frp = buffer_rsrc(part, (uint32_t)(n_items * fstride * 4));
+  uint32_t fpend = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (fst + 64 * j < n_items) fpend |= 1u << j;
+  u32x4_t fv[4];
   float4 got[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) got[j] = make_float4(0.f, 0.f, 0.f, 0.f);
   int spins = 0;
   while (true) {
+    folded_poll(frp, fst, f, fcq, fstride, fpend, fv);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (((fpend >> j) & 1u) && fv[j].x != 0u && fv[j].y != 0u && fv[j].z != 0u && fv[j].w != 0u) {
@@ -845,18 +957,15 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
     }
     if (__ballot(fpend != 0u) == 0ull) break;
     if (++spins >= a.spin_limit) {
-      if ((threadIdx.x & (kWave - 1)) == 0) {
+      if (lane == 0) {
         report_timeout(a.status, a.host_flag);
-        *bad = 1;
+        P.bad = 1;
       }
       break;
     }
     __builtin_amdgcn_s_sleep(2);
     asm volatile("" ::: "memory");
-    folded_poll(frp, fst, d, fcq, fstride, fpend, fv);
   }
-  // each thread's items in order, then the wave's 8 streams (xor 8, 16, 32),
-  // then the 8 waves in order
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -874,15 +983,15 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
     acc.z += __shfl_xor(acc.z, off, kWave);
     acc.w += __shfl_xor(acc.w, off, kWave);
   }
-  if (lane < 8) L.rr[wave][lane] = acc;
+  if (lane < 8) rr[wave][lane] = acc;
   lds_barrier();
   if (tid < 32) {
     float sacc = 0.f;
 #pragma unroll
-    for (int w2 = 0; w2 < kW; ++w2) sacc += ((const float*)&L.rr[w2][tid >> 2])[tid & 3];
-    if (!a.overwrite) sacc += bf16_to_f32((uint32_t)__shfl((int)r.old, 32 + tid, kWave) & 0xffffu);
-    if (P.bad) sacc = nan;
-    a.out[32 * (n_whole + d) + tid] = f32_to_bf16(sacc);
+    for (int w2 = 0; w2 < kW; ++w2) sacc += ((const float*)&rr[w2][tid >> 2])[tid & 3];
+    if (!a.overwrite) sacc += bf16_to_f32(old & 0xffffu);
+    if (P.bad) sacc = __uint_as_float(0x7fc00000u);
+    a.out[32 * (n_whole + f) + tid] = f32_to_bf16(sacc);
   }
   GI_STAMP(7);
 }
@@ -899,10 +1008,11 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
 #endif
   GI_STAMP(0);
   int parity = 0;
-  if (a.E <= 2 * kWave) d1_start<2>(a, P, L.it, &parity);
-  else if (a.E <= 4 * kWave) d1_start<4>(a, P, L.it, &parity);
-  else if (a.E <= 8 * kWave) d1_start<8>(a, P, L.it, &parity);
-  else d1_start<kRouteMaxExperts / kWave>(a, P, L.it, &parity);
+  u32x4_t xv;
+  if (a.E <= 2 * kWave) d1_start<2>(a, P, &xv, &parity);
+  else if (a.E <= 4 * kWave) d1_start<4>(a, P, &xv, &parity);
+  else if (a.E <= 8 * kWave) d1_start<8>(a, P, &xv, &parity);
+  else d1_start<kRouteMaxExperts / kWave>(a, P, &xv, &parity);
   GI_STAMP(1);
   const int tid = threadIdx.x;
   const int b = blockIdx.x, G = gridDim.x;
@@ -912,7 +1022,13 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
   const int n_items = U * a.Tk;
   const int n_whole = min(a.units, G - n_items);
   const int n_left = a.units - n_whole;
-  const int Kv8 = min(a.H >> 3, a.Ggu << (a.gsh + 2));
+  const int Kv8 = min(a.H >> 3, a.Ggu << (a.gsh + 2));  // packed rows inside the gate/up scale groups
+  // the workgroups that clear the previous launch's footprint: the idle ones
+  // if there are any, else the units (they wait for the activations), else all
+  const int n_idle = G - n_items - n_whole;
+  const int c0 = n_idle > 0 ? n_items + n_whole : (n_whole > 0 ? n_items : 0);
+  const int nc = n_idle > 0 ? n_idle : (n_whole > 0 ? n_whole : G);
+  const int cslot = (b >= c0 && b < c0 + nc) ? b - c0 : -1;
 #ifdef GI_TIMELINE
   tl_value(29, 2ull);
   tl_value(30, b < n_items ? 1ull : (b - n_items < n_whole ? 2ull : 0ull));
@@ -921,20 +1037,33 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
   if (U == 0) {
     if (a.overwrite && b == 0)
       for (int i = tid; i < a.H; i += kT) a.out[i] = 0;  // a layer call owns out
+    if (cslot >= 0) clear_prev(a, P.epoch, parity, cslot, nc);
   } else if (b < n_items) {
     const int u = b / a.Tk, c = b - u * a.Tk;
     ItemRegs r;
-    item_load(a, uniform(P.uexp[u]), c, Kv8, n_whole, n_left, r);
+    item_load(a, uniform(P.uexp[u]), b, c, Kv8, n_whole, n_left, r);
     GI_STAMP(2);
-    if (a.logits && tid < kWave) d1_weights(a, P);  // read after the item's next barrier
+    // x in LDS in the matrix-core k order, with each chunk's -24 * sum
+    if (tid < kMaxH / 8) {
+      const uint4 v = make_uint4(xv.x, xv.y, xv.z, xv.w);
+      L.it.xs[tid] = tid < Kv8 ? mfma_k_order(v) : make_uint4(0u, 0u, 0u, 0u);
+      P.cb[tid] = tid < Kv8 ? q4_bias(v) : 0.f;
+    }
+    GI_STAMP_BY(14, kWave);
+    if (a.logits && tid < kWave) d1_weights(a, P);
+    lds_barrier();
     item_run<GSH>(a, P, L.it, b, u, c, n_left, act, part, r);
+    if (b < n_left) folded_reduce(a, P, L.it.rr, b, n_items, n_whole, n_left, part, r.old);
+    if (cslot >= 0) clear_prev(a, P.epoch, parity, cslot, nc);
   } else if (b - n_items < n_whole) {
     const int d = b - n_items;
     UnitRegs<NS> r;
     unit_load<NS>(a, P, d, U, n_whole, n_left, r);
     GI_STAMP(2);
     if (a.logits && tid < kWave) d1_weights(a, P);  // read after the unit's next barrier
-    unit_run<NS, GSH>(a, P, L.un, d, U, n_items, n_whole, n_left, act, part, r);
+    unit_run<NS, GSH>(a, P, L.un, d, U, act, r, parity, cslot, nc);
+  } else if (cslot >= 0) {
+    clear_prev(a, P.epoch, parity, cslot, nc);
   }
   // the end: routing report (workgroup 0), the next epoch word with this launch's footprint
   if (b == 0 && a.logits && tid < a.top_k) {

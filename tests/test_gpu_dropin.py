@@ -259,3 +259,42 @@ def test_prefill_without_routing_outputs_keeps_general_path_counters():
     st = ctypes.c_int32(0)
     L.check(lib.gi_workspace_status(p(ws), ws.numel(), ctypes.byref(st), stream), "status")
     assert st.value == 0
+
+
+def _routing_logits(case, e, seed):
+    g = torch.Generator().manual_seed(seed)
+    if case == "ties":
+        # half-integers: many equal values, ties across the top-k boundary
+        return (torch.round(torch.randn(1, e, generator=g) * 2.0) / 2.0)
+    logits = torch.randn(1, e, generator=g)
+    if case == "nan":
+        logits[0, e // 3] = float("nan")
+    return logits.to(torch.bfloat16) if case == "bf16" else logits
+
+
+@pytest.mark.parametrize("e", [36, 128, 200])
+@pytest.mark.parametrize("case", ["fp32", "bf16", "ties", "nan", "scale"])
+def test_one_token_layer_routing(e, case):
+    """The one-token kernel's in-kernel routing (M=1 layer call): ranks of all
+    threads up to 128 experts, the radix select above.  ids bit-exact against
+    the oracle's top-k (value descending, lower index first, NaN highest),
+    weights within one bf16 ulp, the output within the gate; with a NaN logit
+    only the ids and the finite weights are compared."""
+    h, i, gs = 256, 128, 64
+    Wc = synth.moe_weights(e, h, i, gs, seed=700 + e)
+    Wd = _dev(Wc)
+    x = synth.activations(1, h, seed=701)
+    logits = _routing_logits(case, e, seed=702 + e)
+    es = torch.linspace(0.5, 1.5, e) if case == "scale" else None
+    out, idx, w = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                Wd["down_packed"], Wd["down_scales"], TOP_K, gs,
+                                expert_scale=None if es is None else es.to(DEV))
+    ref_out, ref_idx, ref_w, _ = O.moe_layer_from_logits(
+        np64(x), np64(logits), Wc["gate_up_packed"].numpy(), np64(Wc["gate_up_scales"]),
+        Wc["down_packed"].numpy(), np64(Wc["down_scales"]), TOP_K, gs,
+        expert_scale=None if es is None else es.numpy())
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_idx, err_msg=f"{case} E={e}")
+    finite = np.isfinite(ref_w)
+    np.testing.assert_allclose(np64(w)[finite], ref_w[finite], rtol=2.0 ** -7)
+    if case != "nan":
+        assert_bf16_close(out, ref_out, f"routing {case} E={e}")
