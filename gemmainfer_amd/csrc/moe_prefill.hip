@@ -164,17 +164,14 @@ __global__ __launch_bounds__(256) void prefill_xperm_kernel(const uint4* x, uint
 // products.  Each 16-token row tile of the expert's pairs is one A operand
 // (16 bytes of the lane's token row at k 32kb + 8lq .. +7; the rows are
 // stored in the operand's k order).  Every wave needs the same A operands, so
-// wave rt (< kPRT) loads row tile rt and stages it through a 3-slot LDS ring
-// (one barrier per k block) instead of each wave loading all of them.
-// Words and A tiles stream through register rings (straight-line code, PASS
-// k blocks per pass; loads past K read an offset past the resource: zeros,
-// no memory access), so every wait has an exact count.  No cross-wave
-// reduction: every wave covers all of K.
-constexpr int kPRing = 4;    // weight k blocks in flight per wave
-constexpr int kPRingA = 3;   // A tiles in flight per loading wave
-constexpr int kPSlots = 3;   // LDS slots of staged A tiles
-constexpr int kPPass = 96;   // k blocks per straight-line pass, gate/up (H <= 3072 in one pass)
-constexpr int kPPassD = 24;  // the same, down (I <= 768 in one pass)
+// wave rt (< kPRT) loads row tile rt and stages it through LDS, kPChunk k
+// blocks at a time (one barrier per chunk), instead of each wave loading all
+// of them.  Words stream through a register ring kPChunk k blocks ahead (loads
+// past K read an offset past the resource: zeros, no memory access).  No
+// cross-wave reduction: every wave covers all of K.
+constexpr int kPRingGu = 8;  // weight k blocks in flight per wave, gate/up (bounded by registers)
+constexpr int kPRingDn = 8;  // the same, down
+constexpr int kPChunk = 8;   // k blocks of A tiles staged in LDS per barrier (two chunk buffers)
 
 // 16 bytes of a lane's row at k block kb (zeros past the expert's pairs or
 // past K: offset past the resource).
@@ -188,99 +185,114 @@ __device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t 
 // row tile rt, column 4lr + q of the wave's 64) = sum over groups of
 // scale * (D + Db).  Weights: rw/wbase (+ kb * wstep), activations: ra with
 // this wave's own row tile offset (waves < kPRT), scales:
-// sc_lds[g * 64 + 16 w + lr] (4 bf16), aring: [kPSlots][kPRT][64] uint4.
-template <int PASS>
+// sc_lds[g * 64 + 16 w + lr] (4 bf16; groups past G scale by zero), aring:
+// two chunk buffers [2][kPChunk][kPRT][64] uint4.  The group size (32 <<
+// GSH) is a compile-time value, so every group end inside a chunk is known to
+// the compiler (a chunk holds whole groups); a last partial group is finished
+// after the loop.  Every row tile is multiplied (rows past the expert's pairs
+// are zeros): no branch on the tile count.
+template <int kPRing, int GSH>
 __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint32_t wbase, uint32_t wstep,
                                                  uint32_t wsoff, __amdgpu_buffer_rsrc_t ra, uint32_t roff_own,
-                                                 int n_rt, int KB, int G, int gsh, const uint2* sc_lds,
-                                                 uint4* aring, f32x4_t (&y)[kPRT][4]) {
+                                                 int KB, int G, const uint2* sc_lds, uint4* aring,
+                                                 f32x4_t (&y)[kPRT][4]) {
+  constexpr int kKbpg = 1 << GSH;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const bool loader = wave < kPRT;
   const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
-  const int kbpg_m1 = (1 << gsh) - 1;
   auto own = [&](int kb) { return kb < KB ? roff_own : kOob; };
+  // the expert's offset joins the per-lane offset (no scalar offset beside
+  // an out-of-range one, which could wrap into range); wbase == kOob marks a
+  // wave with no columns
+  const bool wlive = wbase != kOob;
+  const uint32_t wb = wbase + wsoff;
   auto wload = [&](int kb) {
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rw, kb < KB ? wbase + (uint32_t)kb * wstep : kOob,
-                                                            wsoff, 2);
+    const u32x4_t v =
+        __builtin_amdgcn_raw_buffer_load_b128(rw, (wlive && kb < KB) ? wb + (uint32_t)kb * wstep : kOob, 0, 2);
     return make_uint4(v.x, v.y, v.z, v.w);
+  };
+  f32x4_t D[kPRT][4], Db[kPRT];
+  auto epilogue = [&](int g) {
+    const uint2 sv = g < G ? sc_lds[g * 64 + 16 * wave + lr] : make_uint2(0u, 0u);
+    const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
+#pragma unroll
+    for (int rt = 0; rt < kPRT; ++rt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
   };
 #pragma unroll
   for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
     for (int q = 0; q < 4; ++q) y[rt][q] = zf;
-  for (int kp = 0; kp < KB; kp += PASS) {
-    uint4 wr[kPRing], ar[kPRingA];
-    const uint4 a0 = row_operand(ra, own(kp), kp, lq);
+  static_assert(kPChunk % kKbpg == 0 && kPRing == kPChunk, "chunks hold whole groups; one ring slot per k block");
+  auto abuf = [&](int c, int j, int rt) -> uint4& { return aring[(((c & 1) * kPChunk + j) * kPRT + rt) * 64 + lane]; };
+  // A tiles stream through LDS a chunk of kPChunk k blocks at a time (one
+  // barrier per chunk): loader wave rt keeps the next chunk of its row tile
+  // in registers and writes it into the free chunk buffer.  The chunk loop is
+  // a real loop (its body fits the instruction cache); inside it every ring
+  // and buffer index is a compile-time value.
+  uint4 wr[kPRing], ar[kPChunk];
+  const int nch = (KB + kPChunk - 1) / kPChunk;
+  __syncthreads();  // the previous call's readers of the chunk buffers are done
+  if (loader) {
+    uint4 a0[kPChunk];
 #pragma unroll
-    for (int s = 0; s < kPRingA; ++s) ar[s] = row_operand(ra, own(kp + 1 + s), kp + 1 + s, lq);
+    for (int j = 0; j < kPChunk; ++j) a0[j] = row_operand(ra, own(j), j, lq);
 #pragma unroll
-    for (int s = 0; s < kPRing; ++s) wr[s] = wload(kp + s);
-    __syncthreads();  // the previous pass's readers of the ring are done
-    if (loader) aring[wave * 64 + lane] = a0;
-    f32x4_t D[kPRT][4], Db[kPRT];
+    for (int j = 0; j < kPChunk; ++j) ar[j] = row_operand(ra, own(kPChunk + j), kPChunk + j, lq);
 #pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt) {
-      Db[rt] = zf;
+    for (int j = 0; j < kPChunk; ++j) abuf(0, j, wave) = a0[j];
+  }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) D[rt][q] = zf;
+  for (int s = 0; s < kPRing; ++s) wr[s] = wload(s);
+#pragma unroll 1
+  for (int c = 0; c < nch; ++c) {
+    lds_barrier();  // chunk c is in its buffer; every reader of chunk c - 1 is done
+    if (loader) {
+      const int kn = (c + 2) * kPChunk;
+#pragma unroll
+      for (int j = 0; j < kPChunk; ++j) {
+        abuf(c + 1, j, wave) = ar[j];
+        ar[j] = row_operand(ra, own(kn + j), kn + j, lq);
+      }
     }
 #pragma unroll
-    for (int j = 0; j < PASS; ++j) {
-      const int kb = kp + j;
-      if (kb >= KB) break;
-      // k block kb + 1 into the next LDS slot; its register slot reloads
-      if (loader) aring[(((j + 1) % kPSlots) * kPRT + wave) * 64 + lane] = ar[j % kPRingA];
-      ar[j % kPRingA] = row_operand(ra, own(kb + 1 + kPRingA), kb + 1 + kPRingA, lq);
-      lds_barrier();  // slot j % kPSlots is complete; nobody reads slot (j + 1) % kPSlots yet
-      const uint4 w = wr[j % kPRing];
+    for (int j = 0; j < kPChunk; ++j) {
+      const int kb = c * kPChunk + j;
+      const uint4 w = wr[j];
       const uint4 q0 = moe::q4_operand(w.x, mq), q1 = moe::q4_operand(w.y, mq);
       const uint4 q2 = moe::q4_operand(w.z, mq), q3 = moe::q4_operand(w.w, mq);
+      const bool gstart = j % kKbpg == 0;  // compile-time: a group's first product starts from zero
 #pragma unroll
       for (int rt = 0; rt < kPRT; ++rt) {
-        if (rt >= n_rt) break;  // row tiles past the expert's pairs
-        const uint4 A = aring[((j % kPSlots) * kPRT + rt) * 64 + lane];
-        D[rt][0] = moe::mfma_bf16(A, q0, D[rt][0]);
-        D[rt][1] = moe::mfma_bf16(A, q1, D[rt][1]);
-        D[rt][2] = moe::mfma_bf16(A, q2, D[rt][2]);
-        D[rt][3] = moe::mfma_bf16(A, q3, D[rt][3]);
-        Db[rt] = moe::mfma_bf16(A, bc, Db[rt]);
+        const uint4 A = abuf(c, j, rt);
+        D[rt][0] = moe::mfma_bf16(A, q0, gstart ? zf : D[rt][0]);
+        D[rt][1] = moe::mfma_bf16(A, q1, gstart ? zf : D[rt][1]);
+        D[rt][2] = moe::mfma_bf16(A, q2, gstart ? zf : D[rt][2]);
+        D[rt][3] = moe::mfma_bf16(A, q3, gstart ? zf : D[rt][3]);
+        Db[rt] = moe::mfma_bf16(A, bc, gstart ? zf : Db[rt]);
       }
-      // a group ends after kb (PASS is a multiple of every group's k blocks),
-      // or K ends
-      if ((kb & kbpg_m1) == kbpg_m1 || kb == KB - 1) {
-        const int g = kb >> gsh;
-        if (g < G) {
-          const uint2 sv = sc_lds[g * 64 + 16 * wave + lr];
-          const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
-#pragma unroll
-          for (int rt = 0; rt < kPRT; ++rt) {
-            if (rt >= n_rt) break;
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-              for (int jj = 0; jj < 4; ++jj) y[rt][q][jj] += sc[q] * (D[rt][q][jj] + Db[rt][jj]);
-          }
-        }
-#pragma unroll
-        for (int rt = 0; rt < kPRT; ++rt) {
-          Db[rt] = zf;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) D[rt][q] = zf;
-        }
-      }
-      wr[j % kPRing] = wload(kb + kPRing);
+      // k blocks past K multiply zeros (their loads read nothing) and add
+      // nothing: a group that K ends inside is finished below
+      if (j % kKbpg == kKbpg - 1 && kb < KB) epilogue(kb >> GSH);
+      wr[j] = wload(kb + kPRing);
     }
   }
+  // K ends inside a group: its partial sums
+  if (KB % kKbpg) epilogue((KB - 1) >> GSH);
 }
 
 // gate/up: workgroup (tile t, expert e) owns gate columns [128t, 128t+128)
 // (waves 0, 1) and the same up columns (waves 2, 3); act = bf16(gelu(g)*u).
+template <int GSH>
 __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
   __shared__ float yb[16][256];   // one row tile's gate | up sums
-  __shared__ uint4 aring[kPSlots * kPRT * 64];
+  __shared__ uint4 aring[2 * kPChunk * kPRT * 64];
   extern __shared__ uint2 gsc[];  // [Ggu][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
@@ -307,9 +319,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(a.order[off_e + jo] / a.top_k) * (uint32_t)a.H * 2u
                                                  : kOob;
     f32x4_t y[kPRT][4];
-    const int n_rt = min(kPRT, (n_e - base + 15) >> 4);
-    grouped_products<kPPass>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, n_rt, a.H >> 5, a.Ggu, a.gsh, gsc, aring,
-                             y);
+    grouped_products<kPRingGu, GSH>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, a.H >> 5, a.Ggu, gsc,
+                                            aring, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       __syncthreads();
@@ -332,8 +343,9 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
 
 // down: workgroup (unit d, expert e) owns output columns [256d, 256d+256);
 // y[pos] fp32 rows of the expert's pairs.
+template <int GSH>
 __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
-  __shared__ uint4 aring[kPSlots * kPRT * 64];
+  __shared__ uint4 aring[2 * kPChunk * kPRT * 64];
   extern __shared__ uint2 dsc[];  // [Gd][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
@@ -356,9 +368,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
     const int jo = base + 16 * wave + lr;
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(off_e + jo) * (uint32_t)a.I * 2u : kOob;
     f32x4_t y[kPRT][4];
-    const int n_rt = min(kPRT, (n_e - base + 15) >> 4);
-    grouped_products<kPPassD>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, n_rt, a.I >> 5, a.Gd, a.gsh,
-                              dsc, aring, y);
+    grouped_products<kPRingDn, GSH>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, a.I >> 5,
+                                             a.Gd, dsc, aring, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
@@ -436,15 +447,12 @@ int log2_exact(int v) {
 bool moe_prefill_supported(const MoeHostArgs& h) {
   if (h.M < kPrefillMinRows) return false;
   if (h.H % 64 || h.I % 32) return false;
-  if (h.gs % 32 || log2_exact(h.gs / 32) < 0 || kPPassD % (h.gs / 32)) return false;
+  if (h.gs % 32 || log2_exact(h.gs / 32) < 0 || kPChunk % (h.gs / 32)) return false;
   if (h.top_k > 64 || h.E > 1024) return false;
   const long long P = (long long)h.M * h.top_k;
-  // 32-bit buffer offsets
-  // (reads past the last packed row of a pass stay below 2^32 too)
-  const long long kbp_gu = ((long long)h.H / 32 + kPPass - 1) / kPPass * kPPass;
-  const long long kbp_dn = ((long long)h.I / 32 + kPPassD - 1) / kPPassD * kPPassD;
-  if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 + kbp_gu * 4 * 2 * h.I * 4 >= (1LL << 32)) return false;
-  if ((long long)h.E * (h.I / 8) * h.H * 4 + kbp_dn * 4 * h.H * 4 >= (1LL << 32)) return false;
+  // 32-bit buffer offsets (loads past K read an offset past the resource)
+  if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 >= (1LL << 32)) return false;
+  if ((long long)h.E * (h.I / 8) * h.H * 4 >= (1LL << 32)) return false;
   if ((long long)h.M * h.H * 2 >= (1LL << 32) || P * h.I * 2 >= (1LL << 32)) return false;
   return P <= (1 << 20);
 }
@@ -516,10 +524,20 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   if (e != hipSuccess) return hip_fail(e, "prefill x reorder launch");
   const size_t gl = (size_t)h.Ggu * 64 * sizeof(uint2), dl = (size_t)h.Gd * 64 * sizeof(uint2);
   const dim3 ggrid((h.I + 127) / 128, h.E), dgrid((h.H + 255) / 256, h.E);
-  hipLaunchKernelGGL(prefill_gu_kernel, ggrid, dim3(kPThreads), gl, h.stream, k);
+  switch (k.gsh) {
+    case 0: hipLaunchKernelGGL(prefill_gu_kernel<0>, ggrid, dim3(kPThreads), gl, h.stream, k); break;
+    case 1: hipLaunchKernelGGL(prefill_gu_kernel<1>, ggrid, dim3(kPThreads), gl, h.stream, k); break;
+    case 2: hipLaunchKernelGGL(prefill_gu_kernel<2>, ggrid, dim3(kPThreads), gl, h.stream, k); break;
+    default: hipLaunchKernelGGL(prefill_gu_kernel<3>, ggrid, dim3(kPThreads), gl, h.stream, k); break;
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill gate/up launch");
-  hipLaunchKernelGGL(prefill_down_kernel, dgrid, dim3(kPThreads), dl, h.stream, k);
+  switch (k.gsh) {
+    case 0: hipLaunchKernelGGL(prefill_down_kernel<0>, dgrid, dim3(kPThreads), dl, h.stream, k); break;
+    case 1: hipLaunchKernelGGL(prefill_down_kernel<1>, dgrid, dim3(kPThreads), dl, h.stream, k); break;
+    case 2: hipLaunchKernelGGL(prefill_down_kernel<2>, dgrid, dim3(kPThreads), dl, h.stream, k); break;
+    default: hipLaunchKernelGGL(prefill_down_kernel<3>, dgrid, dim3(kPThreads), dl, h.stream, k); break;
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill down launch");
   hipLaunchKernelGGL(prefill_combine_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
