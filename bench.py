@@ -291,7 +291,8 @@ TIMELINE_PHASES = {
     # one-token kernel: item and unit workgroups
     (2, "item"): ["start", "routing", "weight loads issued", None, "gate/up products",
                   "activations published", "folded partial sums published",
-                  "folded unit output written (items 0-7)", None, "end", *D1_ROUTING_PHASES],
+                  "folded unit output written (items 0-7)", None, "end", *D1_ROUTING_PHASES,
+                  "first k block's words landed (wave 0)", "last k block's words landed (wave 0)"],
     (2, "unit"): ["start", "routing", "weight loads issued", "words unpacked", "activations staged (wave 0)",
                   "down products", "unit output written", None, None, "end", *D1_ROUTING_PHASES,
                   "activations staged (last expert's wave)", "products issued (wave 0)",
@@ -783,12 +784,13 @@ def bench_dense(steps, warmup, device):
     }
 
 
-def pmc_pass(copies, steps, warmup, device):
+def pmc_pass(copies, steps, warmup, device, m=1):
     """Eager launches for one rocprofv3 --pmc pass (FETCH_SIZE or WRITE_SIZE).
 
     First three float32 negations of a 256 MiB buffer (a plain streaming
     kernel that reads and writes exactly CALIB_BYTES each: the calibration
-    for the counter), then W warmup + K rotated M=1 layers launched one by
+    for the counter), then W warmup + K rotated M-row layers (M=1, or M=7
+    with the verify noise of configs[2]) launched one by
     one.  The profiler serialises dispatches; the rotation keeps >= 1 GB of
     other weights between reuses, as in the timed run.  Per-dispatch HBM
     bytes of the layer kernel = mean counter over the K layers after warmup,
@@ -801,8 +803,8 @@ def pmc_pass(copies, steps, warmup, device):
         torch.neg(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
-    desc = make_steps(1, 0.0, 1, warmup + steps)
-    runner = LayerRunner(1, desc, copies, device)
+    desc = make_steps(m, 0.0 if m == 1 else 0.5, 1 if m == 1 else 2, warmup + steps)
+    runner = LayerRunner(m, desc, copies, device)
     for i in range(warmup + steps):
         runner.launch(i)
     torch.cuda.synchronize()
@@ -811,11 +813,11 @@ def pmc_pass(copies, steps, warmup, device):
     mean_u = statistics.fmean(desc[i]["U"] for i in range(warmup, warmup + steps))
     print(json.dumps({"pmc_pass": {"calibration_kernel": "neg float32", "calibration_bytes_read": CALIB_BYTES,
                                    "calibration_bytes_written": CALIB_BYTES, "calibration_dispatches": 3,
-                                   "layer_dispatches": warmup + steps, "warmup": warmup,
+                                   "layer_dispatches": warmup + steps, "warmup": warmup, "M": m,
                                    "algorithmic_bytes_per_layer": mean_u * expert_bytes()}}))
 
 
-def pmc_reduce(fetch_csv, write_csv, out_path):
+def pmc_reduce(fetch_csv, write_csv, out_path, algorithmic_bytes=None):
     """Per-dispatch HBM bytes of the M=1 layer kernel from the counter CSVs of
     two --pmc-pass runs (FETCH_SIZE, then WRITE_SIZE; values in KiB per
     dispatch).  Each counter is scaled by CALIB_BYTES / its reading on the
@@ -846,7 +848,7 @@ def pmc_reduce(fetch_csv, write_csv, out_path):
                     "calibration_factor": factor, "bytes_per_dispatch": statistics.fmean(lay) * 1024.0 * factor,
                     "dispatches": len(lay)}
     res["hbm_bytes_per_launch"] = res["fetch"]["bytes_per_dispatch"] + res["write"]["bytes_per_dispatch"]
-    res["algorithmic_bytes_per_launch"] = 8 * expert_bytes()
+    res["algorithmic_bytes_per_launch"] = algorithmic_bytes if algorithmic_bytes else 8 * expert_bytes()
     Path(out_path).write_text(json.dumps(res, indent=1) + "\n")
     print(json.dumps(res))
 
@@ -930,11 +932,15 @@ def main():
                          "lm_head = configs[4])")
     ap.add_argument("--pmc-reduce", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "OUT_JSON"),
                     help="reduce two --pmc-pass counter CSVs to per-launch HBM bytes (no GPU needed)")
+    ap.add_argument("--pmc-m", type=int, choices=[1, 7], default=1,
+                    help="rows of the --pmc-pass layers (7: configs[2])")
+    ap.add_argument("--pmc-alg-bytes", type=float, default=None,
+                    help="--pmc-reduce: algorithmic bytes per launch (the pass prints them; default 8 experts)")
     ap.add_argument("--pmc-pass", action="store_true",
                     help="eager calibration copy + rotated M=1 layers for a rocprofv3 --pmc run; no timing")
     args = ap.parse_args()
     if args.pmc_reduce:
-        pmc_reduce(*args.pmc_reduce)
+        pmc_reduce(*args.pmc_reduce, algorithmic_bytes=args.pmc_alg_bytes)
         return
     if args.workload == "cpu_table":
         print(json.dumps(cpu_table(args.cpu_budget_s)))
@@ -987,7 +993,7 @@ def main():
             "cpu_baseline": None, "stream": rows}))
         return
     if args.pmc_pass:
-        pmc_pass(copies, args.steps, args.warmup, device)
+        pmc_pass(copies, args.steps, args.warmup, device, args.pmc_m)
         return
     if args.workload == "timeline":
         tl = bench_timeline(copies, min(args.steps, 100), args.warmup, device, gs)

@@ -623,6 +623,13 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
     const uint4 xa = L.xs[4 * kb + lq];
     const uint4 A = lr == 0 ? xa : z4;  // A row 0 is the token, rows 1-15 zero
     const uint4 w = opaque(r.w[j]);
+#ifdef GI_TIMELINE
+    if (j == 0 || j == kKbw - 1) {
+      asm volatile("" ::"v"(w.x), "v"(w.w));
+      if (j == 0) GI_STAMP(20);
+      else GI_STAMP(21);
+    }
+#endif
     D[0] = mfma_bf16(A, q4_operand_fast(w.x, mq, mc), D[0]);
     D[1] = mfma_bf16(A, q4_operand_fast(w.y, mq, mc), D[1]);
     D[2] = mfma_bf16(A, q4_operand_fast(w.z, mq, mc), D[2]);
