@@ -110,9 +110,19 @@ __device__ __forceinline__ float fdot2(uint32_t a, uint32_t b, float c) {
 // precision: the fp32 sums carry base * sum x, which cancels.)
 //   lo = (w << 3) & 0x78787878 | 0x80808080 holds codes (q0, q2, q4, q6),
 //   hi = (w >> 1) & 0x78787878 | 0x80808080 holds (q1, q3, q5, q7).
+// 0x80808080 held in a vector register, so that (v & 0x78787878) | 0x80808080
+// is one v_and_or_b32 (a VOP3 instruction takes no literal and reads at most
+// one scalar register here); the empty asm has no side effects, so repeated
+// calls fold into one register.
+__device__ __forceinline__ uint32_t q4_high_bits() {
+  uint32_t v = 0x80808080u;
+  asm("" : "+v"(v));
+  return v;
+}
 __device__ __forceinline__ void q4_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
-  lo = ((w << 3) & 0x78787878u) | 0x80808080u;
-  hi = ((w >> 1) & 0x78787878u) | 0x80808080u;
+  const uint32_t mc = q4_high_bits();
+  lo = ((w << 3) & 0x78787878u) | mc;
+  hi = ((w >> 1) & 0x78787878u) | mc;
 }
 __device__ __forceinline__ float dot8_q4(uint32_t w, uint4 xp, float bias, uint32_t mq) {
   uint32_t lo, hi;

@@ -181,13 +181,6 @@ __device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, floa
   return fdot2(A.w, q.p3, c);
 }
 
-// 0x80808080 held in a VGPR, so that (v & 0x78787878) | 0x80808080 is one
-// v_and_or_b32 (one literal operand).
-__device__ __forceinline__ uint32_t q4_high_bits() {
-  uint32_t v = 0x80808080u;
-  asm volatile("" : "+v"(v));
-  return v;
-}
 // q4_operand (moe_shared.h) in 8 VALU operations per word: the byte of code
 // q is 0x80 | q << 3, and v_perm_b32 pairs those bytes with 0x41 bytes into
 // bf16 16 + q, in the matrix-core k order (0,4) (2,6) (1,5) (3,7).
