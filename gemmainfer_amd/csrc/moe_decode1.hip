@@ -145,6 +145,7 @@ struct D1Pro {
 
 struct ItemLds {
   uint4 xs[kMaxH / 8];            // x in the matrix-core k order, per packed row
+  uint4 xz[4 * kKbw];             // zeros: the A operand rows 1-15 (lanes lr > 0) read these
   float4 red[kW][16];             // per-wave sums: lane lr holds 4 gate (lr < 8) or up columns
   uint4 sa[4];                    // the item's 32 activations, matrix-core k order
   float4 fr[4][kMaxLeft * 8];     // folded products per packed row
@@ -589,6 +590,44 @@ __device__ __forceinline__ void item_load(const D1Args& a, int e, int it, int c,
   __builtin_amdgcn_sched_barrier(0);
 }
 
+// The gate/up products of one wave's kKbw k blocks, whose first k block sits
+// at phase PH of its scale group (group size 32 << GSH): y[i] (column quad
+// lr's column i; lanes lr >= 8 hold up columns) = sum over groups of
+// scale * (the group's products + its -24 * sum of x).  A group's first
+// product starts from zero.
+template <int GSH, int PH>
+__device__ __forceinline__ void item_products(const ItemRegs& r, const uint4* arow, float kbv, uint32_t mq,
+                                              uint32_t mc, float (&y)[4]) {
+  constexpr int kPg = 1 << GSH;
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  f32x4_t D[4];
+  float bacc = 0.f;
+#pragma unroll
+  for (int j = 0; j < kKbw; ++j) {
+    const bool gstart = j == 0 || (PH + j) % kPg == 0;
+    const uint4 A = arow[4 * j];
+    const uint4 w = opaque(r.w[j]);
+#ifdef GI_TIMELINE
+    if (j == 0 || j == kKbw - 1) {
+      asm volatile("" ::"v"(w.x), "v"(w.w));
+      if (j == 0) GI_STAMP(20);
+      else GI_STAMP(21);
+    }
+#endif
+    D[0] = mfma_bf16(A, q4_operand_fast(w.x, mq, mc), gstart ? zf : D[0]);
+    D[1] = mfma_bf16(A, q4_operand_fast(w.y, mq, mc), gstart ? zf : D[1]);
+    D[2] = mfma_bf16(A, q4_operand_fast(w.z, mq, mc), gstart ? zf : D[2]);
+    D[3] = mfma_bf16(A, q4_operand_fast(w.w, mq, mc), gstart ? zf : D[3]);
+    bacc = (gstart ? 0.f : bacc) + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kbv), 4 * j));
+    if ((PH + j + 1) % kPg == 0 || j == kKbw - 1) {  // a scale group ends
+      const uint2 s2 = opaque(r.s[(PH + j) / kPg]);  // opaque: the variants' epilogues stay apart
+      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] += sc[i] * (D[i][0] + bacc);
+    }
+  }
+}
+
 template <int GSH>
 __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLds& L, int it, int u, int c,
                                          int n_left, char* act, char* part, const ItemRegs& r) {
@@ -605,42 +644,52 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
   kbv += dpp_f32<0x4E>(kbv);  // quad_perm [2,3,0,1]
   const uint32_t mq = q4_magic();
   const uint32_t mc = q4_high_bits();
-  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
-  const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-  f32x4_t D[4] = {zf, zf, zf, zf};
-  float bacc = 0.f;
+  // A row 0 is the token (lanes lr == 0 read x), rows 1-15 are zero (the
+  // other lanes read the zero block at the same offsets): no select per k block
+  const uint4* arow = lr == 0 ? L.xs + 4 * kb0 + lq : L.xz + lq;
   float y[4] = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (GSH > 0) {
+    // the wave's first k block sits at phase kb0 % (k blocks per group) of
+    // its group: with the phase a compile-time value, every group end, group
+    // start and scale register of the loop is known to the compiler
+    constexpr int kPh = 1 << GSH;
+    const int ph = kb0 & (kPh - 1);
+    if (ph == 0) item_products<GSH, 0>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 1 && ph == 1) item_products<GSH, (kPh > 1 ? 1 : 0)>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 2 && ph == 2) item_products<GSH, (kPh > 2 ? 2 : 0)>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 3 && ph == 3) item_products<GSH, (kPh > 3 ? 3 : 0)>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 4 && ph == 4) item_products<GSH, (kPh > 4 ? 4 : 0)>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 5 && ph == 5) item_products<GSH, (kPh > 5 ? 5 : 0)>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 6 && ph == 6) item_products<GSH, (kPh > 6 ? 6 : 0)>(r, arow, kbv, mq, mc, y);
+    else item_products<GSH, (kPh > 7 ? 7 : 0)>(r, arow, kbv, mq, mc, y);
+  } else {
+    const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t D[4] = {zf, zf, zf, zf};
+    float bacc = 0.f;
 #pragma unroll
-  for (int j = 0; j < kKbw; ++j) {
-    const int kb = kb0 + j;
-    const uint4 xa = L.xs[4 * kb + lq];
-    const uint4 A = lr == 0 ? xa : z4;  // A row 0 is the token, rows 1-15 zero
-    const uint4 w = opaque(r.w[j]);
-#ifdef GI_TIMELINE
-    if (j == 0 || j == kKbw - 1) {
-      asm volatile("" ::"v"(w.x), "v"(w.w));
-      if (j == 0) GI_STAMP(20);
-      else GI_STAMP(21);
-    }
-#endif
-    D[0] = mfma_bf16(A, q4_operand_fast(w.x, mq, mc), D[0]);
-    D[1] = mfma_bf16(A, q4_operand_fast(w.y, mq, mc), D[1]);
-    D[2] = mfma_bf16(A, q4_operand_fast(w.z, mq, mc), D[2]);
-    D[3] = mfma_bf16(A, q4_operand_fast(w.w, mq, mc), D[3]);
-    bacc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kbv), 4 * j));
-    if (((kb + 1) & kbpg_m1) == 0 || j == kKbw - 1) {  // a scale group ends
-      const int gi = (kb >> gsh) - g0;
-      uint2 s2 = opaque(r.s[0]);
+    for (int j = 0; j < kKbw; ++j) {
+      const int kb = kb0 + j;
+      const uint4 A = arow[4 * j];
+      const uint4 w = opaque(r.w[j]);
+      D[0] = mfma_bf16(A, q4_operand_fast(w.x, mq, mc), D[0]);
+      D[1] = mfma_bf16(A, q4_operand_fast(w.y, mq, mc), D[1]);
+      D[2] = mfma_bf16(A, q4_operand_fast(w.z, mq, mc), D[2]);
+      D[3] = mfma_bf16(A, q4_operand_fast(w.w, mq, mc), D[3]);
+      bacc += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kbv), 4 * j));
+      if (((kb + 1) & kbpg_m1) == 0 || j == kKbw - 1) {  // a scale group ends
+        const int gi = (kb >> gsh) - g0;
+        uint2 s2 = opaque(r.s[0]);
 #pragma unroll
-      for (int q = 1; q < kGuSc; ++q)
-        if (gi == q) s2 = opaque(r.s[q]);
-      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+        for (int q = 1; q < kGuSc; ++q)
+          if (gi == q) s2 = opaque(r.s[q]);
+        const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        y[i] += sc[i] * (D[i][0] + bacc);
-        D[i] = zf;
+        for (int i = 0; i < 4; ++i) {
+          y[i] += sc[i] * (D[i][0] + bacc);
+          D[i] = zf;
+        }
+        bacc = 0.f;
       }
-      bacc = 0.f;
     }
   }
   if (lq == 0) L.red[wave][lr] = make_float4(y[0], y[1], y[2], y[3]);
@@ -1048,6 +1097,8 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
       const uint4 v = make_uint4(xv.x, xv.y, xv.z, xv.w);
       L.it.xs[tid] = tid < Kv8 ? mfma_k_order(v) : make_uint4(0u, 0u, 0u, 0u);
       P.cb[tid] = tid < Kv8 ? q4_bias(v) : 0.f;
+    } else if (tid < kMaxH / 8 + 4 * kKbw) {
+      L.it.xz[tid - kMaxH / 8] = make_uint4(0u, 0u, 0u, 0u);
     }
     GI_STAMP_BY(14, kWave);
     if (a.logits && tid < kWave) d1_weights(a, P);
