@@ -381,26 +381,19 @@ __host__ __device__ constexpr size_t gu_lds_bytes() {
   return (size_t)kRows * GuShape<KBW>::KPM * 16 + (size_t)kWaves * kRows * 16 * 16 + (size_t)kRows * kCols * 2;
 }
 
-// One item: gate/up product, cross-wave reduction, activation, exchange.
+// The gate/up products of one wave's KBW k blocks: y[i][jj] (token row
+// 4lq + jj, task column 4lr + i) = sum over scale groups of scale * (the
+// group's products + its -24 * sum of x, from one more product against a
+// constant operand).  Generic form: the group size is a run-time value.
 template <int KBW>
-__device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, int item, const GuBuf<KBW>& b,
-                                        const GuLds& L, uint16_t* act) {
-  constexpr int KPM = GuShape<KBW>::KPM;
-  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
-  const int lq = lane >> 4, lr = lane & 15;
-  const int u = item / a.Tk, c = item - u * a.Tk;
-  const int kb0 = wave * KBW;
+__device__ __forceinline__ void gu_products(const DecArgs& a, const GuBuf<KBW>& b, const uint4* xrow, int kb0,
+                                            float (&y)[4][4]) {
   const int kbpg_m1 = (1 << a.gsh) - 1;  // k blocks per scale group - 1
   const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   f32x4_t D[4] = {zf, zf, zf, zf};
   f32x4_t Db = zf;
-  float y[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) y[i][0] = y[i][1] = y[i][2] = y[i][3] = 0.f;
-  // rows 8-15 of the product repeat rows 0-7 (never used); x rows >= M are zero
-  const uint4* xrow = L.xs + (lr & 7) * KPM + lq;
 #pragma unroll
   for (int j = 0; j < KBW; ++j) {
     const int kb = kb0 + j;
@@ -426,6 +419,72 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
       }
       Db = zf;
     }
+  }
+}
+
+// The same with the group size 32 << GSH and the phase PH of the wave's first
+// k block within its group fixed at compile time: every group start and end
+// and the scale register of each group are known to the compiler, and a
+// group's first products start from zero.  The scales of groups past the
+// scale tensor were loaded as zeros.
+template <int KBW, int GSH, int PH>
+__device__ __forceinline__ void gu_products_ph(const GuBuf<KBW>& b, const uint4* xrow, int kb0, float (&y)[4][4]) {
+  constexpr int kPg = 1 << GSH;
+  const uint32_t mq = q4_magic();
+  const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
+  const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
+  f32x4_t D[4], Db;
+#pragma unroll
+  for (int j = 0; j < KBW; ++j) {
+    const bool gstart = j == 0 || (PH + j) % kPg == 0;
+    const uint4 A = xrow[4 * (kb0 + j)];
+    const uint4 w = opaque(b.w[j]);
+    D[0] = mfma_bf16(A, q4_operand(w.x, mq), gstart ? zf : D[0]);
+    D[1] = mfma_bf16(A, q4_operand(w.y, mq), gstart ? zf : D[1]);
+    D[2] = mfma_bf16(A, q4_operand(w.z, mq), gstart ? zf : D[2]);
+    D[3] = mfma_bf16(A, q4_operand(w.w, mq), gstart ? zf : D[3]);
+    Db = mfma_bf16(A, bc, gstart ? zf : Db);
+    if ((PH + j + 1) % kPg == 0 || j == KBW - 1) {  // a scale group ends
+      const uint2 s2 = opaque(b.s[(PH + j) / kPg]);
+      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (D[i][jj] + Db[jj]);
+    }
+  }
+}
+
+// One item: gate/up product, cross-wave reduction, activation, exchange.
+// PHASED: the group sizes 64 and 128 take the phase-specialized products.
+template <int KBW, bool PHASED = false>
+__device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, int item, const GuBuf<KBW>& b,
+                                        const GuLds& L, uint16_t* act) {
+  constexpr int KPM = GuShape<KBW>::KPM;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
+  const int lq = lane >> 4, lr = lane & 15;
+  const int u = item / a.Tk, c = item - u * a.Tk;
+  const int kb0 = wave * KBW;
+  float y[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) y[i][0] = y[i][1] = y[i][2] = y[i][3] = 0.f;
+  // rows 8-15 of the product repeat rows 0-7 (never used); x rows >= M are zero
+  const uint4* xrow = L.xs + (lr & 7) * KPM + lq;
+  if constexpr (PHASED) {
+    if (a.gsh == 2) {
+      const int ph = kb0 & 3;
+      if (ph == 0) gu_products_ph<KBW, 2, 0>(b, xrow, kb0, y);
+      else if (ph == 1) gu_products_ph<KBW, 2, 1>(b, xrow, kb0, y);
+      else if (ph == 2) gu_products_ph<KBW, 2, 2>(b, xrow, kb0, y);
+      else gu_products_ph<KBW, 2, 3>(b, xrow, kb0, y);
+    } else if (a.gsh == 1) {
+      if ((kb0 & 1) == 0) gu_products_ph<KBW, 1, 0>(b, xrow, kb0, y);
+      else gu_products_ph<KBW, 1, 1>(b, xrow, kb0, y);
+    } else {
+      gu_products<KBW>(a, b, xrow, kb0, y);
+    }
+  } else {
+    gu_products<KBW>(a, b, xrow, kb0, y);
   }
   // per-wave sums of token rows 4lq+jj, task columns 4lr..4lr+3
 #pragma unroll
@@ -1231,10 +1290,10 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
   if constexpr (NI <= 2) dn_load<BPW>(a, uexp_v, U, dp, dw);
   GI_STAMP(3);
   if constexpr (NI == 1) {
-    gu_item<KBW>(a, P, it0, b0, L, act);
+    gu_item<KBW, true>(a, P, it0, b0, L, act);
   } else if constexpr (NI == 2) {
-    gu_item<KBW>(a, P, it0, b0, L, act);
-    gu_item<KBW>(a, P, it0 + G, b1, L, act);
+    gu_item<KBW, true>(a, P, it0, b0, L, act);
+    gu_item<KBW, true>(a, P, it0 + G, b1, L, act);
   } else {
     gu_items<KBW, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
