@@ -285,7 +285,12 @@ D1_ROUTING_PHASES = ["routing inputs landed (wave 0)", "wave 0 routing work done
 TIMELINE_PHASES = {
     # decode kernel (up to 8 rows per launch): roles by whether the workgroup holds gate/up items
     (1, "item"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
-                  "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
+                  "activations staged", "down products", "sums over waves", "output / partial sums", "end",
+                  "first item's first k block's words landed (wave 0)",
+                  "first item's last k block's words landed (wave 0)",
+                  "second item's first k block's words landed (wave 0)",
+                  "second item's last k block's words landed (wave 0)",
+                  "first down batch's words landed (wave 0)"],
     (1, "down"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
                   "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
     # one-token kernel: item and unit workgroups

@@ -470,6 +470,15 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
   for (int i = 0; i < 4; ++i) y[i][0] = y[i][1] = y[i][2] = y[i][3] = 0.f;
   // rows 8-15 of the product repeat rows 0-7 (never used); x rows >= M are zero
   const uint4* xrow = L.xs + (lr & 7) * KPM + lq;
+#ifdef GI_TIMELINE
+  {  // arrival of this item's first and last k block's words (wave 0's view)
+    const int k = item == (int)blockIdx.x ? 0 : 2;
+    asm volatile("" ::"v"(b.w[0].x));
+    GI_STAMP(10 + k);
+    asm volatile("" ::"v"(b.w[KBW - 1].x));
+    GI_STAMP(11 + k);
+  }
+#endif
   if constexpr (PHASED) {
     if (a.gsh == 2) {
       const int ph = kb0 & 3;
@@ -1107,6 +1116,10 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   // the first batch's words unpacked while the activations are on their way,
   // where the registers allow: every block with one token and few blocks,
   // the first kDownPreMfma blocks on the matrix-core path
+#ifdef GI_TIMELINE
+  asm volatile("" ::"v"(dw0[BPW - 1][kDownKpw - 1].x));
+  GI_STAMP(14);  // the first batch's down words landed (wave 0's view)
+#endif
   constexpr int NPRE = PRE ? BPW : (MODE == 0 ? (BPW < kDownPreMfma ? BPW : kDownPreMfma) : 0);
   DnQ dq[NPRE > 0 ? NPRE : 1][kDownKpw];
   if constexpr (NPRE > 0) {
@@ -1274,11 +1287,14 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
 }
 
 // The workgroup's gate/up items (it0, it0 + G, ...) and the issue of its down
-// words: the first items' words go out first, then the down words, so that
-// every wait of the gate/up products has an exact count; NI = 1 and 2 have
-// paths of their own (no load is issued for nothing), NI = 3 is the general
-// path (two items in flight, the next one loaded as each finishes), which
-// issues the down words after its items (registers: a rare case).
+// words: the items' words go out first, then the down words, so that every
+// wait of the gate/up products has an exact count.  NI = 1 issues the down
+// words right behind its item; NI = 2 issues them after its first item's
+// products, so that both items' words are served before the down words (the
+// second item's products wait on them; the down words are needed only after
+// the activation exchange).  NI = 3 is the general path (two items in
+// flight, the next one loaded as each finishes), which issues the down words
+// after its items (registers: a rare case).
 template <int KBW, int NI, int BPW>
 __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P, const GuLds& L, int U,
                                          int uexp_v, uint16_t* act, const DnPlan& dp, int n_items,
@@ -1287,12 +1303,13 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
   GuBuf<KBW> b0, b1;
   gu_load<KBW>(a, uexp_v, it0, n_items, b0);
   if constexpr (NI >= 2) gu_load<KBW>(a, uexp_v, it0 + G, n_items, b1);
-  if constexpr (NI <= 2) dn_load<BPW>(a, uexp_v, U, dp, dw);
+  if constexpr (NI == 1) dn_load<BPW>(a, uexp_v, U, dp, dw);
   GI_STAMP(3);
   if constexpr (NI == 1) {
     gu_item<KBW, true>(a, P, it0, b0, L, act);
   } else if constexpr (NI == 2) {
     gu_item<KBW, true>(a, P, it0, b0, L, act);
+    dn_load<BPW>(a, uexp_v, U, dp, dw);
     gu_item<KBW, true>(a, P, it0 + G, b1, L, act);
   } else {
     gu_items<KBW, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
