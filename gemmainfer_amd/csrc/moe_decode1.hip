@@ -84,6 +84,12 @@ constexpr int kSlots = 64;
 constexpr int kDefaultSpin = 1 << 20;
 constexpr int kCpolNt = 2;             // non-temporal: weights are read once
 constexpr uint32_t kOob = 0xFFFFFFF0u;  // past every buffer resource: the load returns zeros
+// Unit workgroups hold their down words back for the time the items' bytes
+// take at this rate (bytes per 10 ns tick of the constant clock, ~9.4 TB/s:
+// the items' words are then about 60% served at the ~5.5 TB/s the layer
+// streams at).  Measured at M=1 (U = 8, 16.4 MB of item bytes): holds of
+// 1.5-2.0 us give 12.0 us per layer against 12.7 us with no hold; 4 us, 13.5.
+constexpr uint32_t kUnitHoldBytesPerTick = 94208;
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
@@ -1109,6 +1115,16 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
   } else if (b - n_items < n_whole) {
     const int d = b - n_items;
     UnitRegs<NS> r;
+    // The units' words are needed only after the activation exchange: issued
+    // right after the routing they would share the HBM with the items' words,
+    // whose products are on the critical path.  Hold them back for about the
+    // time the items' bytes take (a bounded wait on the constant clock).
+    {
+      const uint32_t item_bytes = 32u * (uint32_t)a.H + 128u * (uint32_t)a.Ggu;
+      const unsigned long long hold = (unsigned long long)n_items * item_bytes / kUnitHoldBytesPerTick;
+      const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+      while (__builtin_amdgcn_s_memrealtime() - t0 < hold) __builtin_amdgcn_s_sleep(4);
+    }
     unit_load<NS>(a, P, d, U, n_whole, n_left, r);
     GI_STAMP(2);
     if (a.logits && tid < kWave) d1_weights(a, P);  // read after the unit's next barrier
