@@ -290,7 +290,10 @@ TIMELINE_PHASES = {
                   "first item's last k block's words landed (wave 0)",
                   "second item's first k block's words landed (wave 0)",
                   "second item's last k block's words landed (wave 0)",
-                  "first down batch's words landed (wave 0)"],
+                  "first down batch's words landed (wave 0)",
+                  "top-k and softmax of token 0 (wave 0)", "all tokens routed (barrier)",
+                  "Token-Union tables built (wave 0)", "work split computed (wave 0)",
+                  "x written to LDS (wave 0)"],
     (1, "down"): ["start", "routing and tables", "x in LDS", "weight loads issued", "gate/up items done",
                   "activations staged", "down products", "sums over waves", "output / partial sums", "end"],
     # one-token kernel: item and unit workgroups

@@ -227,7 +227,9 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, c
                                                   : bf16_to_f32(in.wb);
     P.slot_w[lane] = round_to_bf16(wv);
   }
+  GI_STAMP(15);
   lds_barrier();
+  GI_STAMP(16);
   if (wave == 0) {
     int e = lane < S ? P.slot_e[lane] : -1;
     float w = lane < S ? P.slot_w[lane] : 0.f;
@@ -291,6 +293,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, c
       P.epos[U] = total;
       P.n_unique = U;
     }
+    GI_STAMP(17);
   }
   lds_barrier();
 }
@@ -591,6 +594,7 @@ __device__ __forceinline__ void stage_x(const DecArgs& a, const GuLds& L, const 
     }
   }
   lds_barrier();
+  GI_STAMP(2);
 }
 
 // ---------------------------------------------------------------------------
@@ -1288,11 +1292,10 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
 
 // The workgroup's gate/up items (it0, it0 + G, ...) and the issue of its down
 // words: the items' words go out first, then the down words, so that every
-// wait of the gate/up products has an exact count.  NI = 1 issues the down
-// words right behind its item; NI = 2 issues them after its first item's
-// products, so that both items' words are served before the down words (the
-// second item's products wait on them; the down words are needed only after
-// the activation exchange).  NI = 3 is the general path (two items in
+// wait of the gate/up products has an exact count.  The down words are
+// needed only after the activation exchange: NI = 1 issues them after its
+// item's products, NI = 2 after its first item's products, so that the
+// items' words (whose products are on the critical path) are served first.  NI = 3 is the general path (two items in
 // flight, the next one loaded as each finishes), which issues the down words
 // after its items (registers: a rare case).
 template <int KBW, int NI, int BPW>
@@ -1303,10 +1306,10 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
   GuBuf<KBW> b0, b1;
   gu_load<KBW>(a, uexp_v, it0, n_items, b0);
   if constexpr (NI >= 2) gu_load<KBW>(a, uexp_v, it0 + G, n_items, b1);
-  if constexpr (NI == 1) dn_load<BPW>(a, uexp_v, U, dp, dw);
   GI_STAMP(3);
   if constexpr (NI == 1) {
     gu_item<KBW, true>(a, P, it0, b0, L, act);
+    dn_load<BPW>(a, uexp_v, U, dp, dw);
   } else if constexpr (NI == 2) {
     gu_item<KBW, true>(a, P, it0, b0, L, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
@@ -1393,9 +1396,11 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   L.xs = (uint4*)dyn_lds;
   L.red = (float4*)(dyn_lds + (size_t)kRows * KPM * 16);
   L.sact = (uint16_t*)(L.red + kWaves * kRows * 16);
+  GI_STAMP(18);
   // x into LDS first: its registers are free before the word buffers fill
+  // (staged after the word loads are issued, it waited as long as the first
+  // item's words: M=7 29.7 -> 30.0 us)
   if (n_my > 0) stage_x<KBW>(a, L, xr);
-  GI_STAMP(2);
 #ifdef GI_TIMELINE
   tl_value(29, 1ull);
   tl_value(30, (unsigned long long)n_my);
