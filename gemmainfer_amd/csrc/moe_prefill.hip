@@ -414,6 +414,76 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, co
   }
 }
 
+// The same for top_k <= 8 with every load of the workgroup issued before any
+// use: the token's slot positions and weights are read once, then the three
+// column chunks of each thread (H <= 3072 per pass) over all slots, and the
+// previous output, go out together (one memory round trip instead of one per
+// chunk).  Same arithmetic and order as prefill_combine_kernel.
+constexpr int kCombineSlots = 8;
+constexpr int kCombineChunks = 3;
+__global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, const int* posmap, const float* wts,
+                                                               uint16_t* out, int H, int top_k, int overwrite) {
+  const int t = blockIdx.x;
+  __shared__ int spos[kCombineSlots];
+  __shared__ float swt[kCombineSlots];
+  if (threadIdx.x < kCombineSlots) {
+    const bool ok = (int)threadIdx.x < top_k;
+    spos[threadIdx.x] = ok ? posmap[(size_t)t * top_k + threadIdx.x] : -1;
+    swt[threadIdx.x] = ok ? wts[(size_t)t * top_k + threadIdx.x] : 0.f;
+  }
+  __syncthreads();
+  int pos[kCombineSlots];
+  float wv[kCombineSlots];
+#pragma unroll
+  for (int k = 0; k < kCombineSlots; ++k) {
+    pos[k] = __builtin_amdgcn_readfirstlane(spos[k]);
+    wv[k] = swt[k];
+  }
+  const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out + (size_t)t * H, overwrite ? 0u : (uint32_t)H * 2u);
+  for (int c0 = threadIdx.x * 4; c0 < H; c0 += 256 * 4 * kCombineChunks) {
+    u32x4_t v[kCombineChunks][kCombineSlots];
+    u32x2_t o[kCombineChunks];
+#pragma unroll
+    for (int k = 0; k < kCombineSlots; ++k) {
+      // a row's resource (its offsets stay below 2^32 whatever the row count)
+      const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(y + (size_t)max(pos[k], 0) * H, pos[k] >= 0 ? (uint32_t)H * 4u : 0u);
+#pragma unroll
+      for (int i = 0; i < kCombineChunks; ++i) {
+        const int c = c0 + i * 1024;
+        v[i][k] = __builtin_amdgcn_raw_buffer_load_b128(ry, c < H ? (uint32_t)c * 4u : kOob, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kCombineChunks; ++i) {
+      const int c = c0 + i * 1024;
+      o[i] = __builtin_amdgcn_raw_buffer_load_b64(ro, c < H ? (uint32_t)c * 2u : kOob, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < kCombineChunks; ++i) {
+      const int c = c0 + i * 1024;
+      if (c >= H) continue;
+      float4 s = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f)
+                           : make_float4(bf16lo(o[i].x), bf16hi(o[i].x), bf16lo(o[i].y), bf16hi(o[i].y));
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k) {
+        if (pos[k] < 0) continue;
+        acc.x += wv[k] * __uint_as_float(v[i][k].x);
+        acc.y += wv[k] * __uint_as_float(v[i][k].y);
+        acc.z += wv[k] * __uint_as_float(v[i][k].z);
+        acc.w += wv[k] * __uint_as_float(v[i][k].w);
+      }
+      s.x += acc.x;
+      s.y += acc.y;
+      s.z += acc.z;
+      s.w += acc.w;
+      const uint32_t lo = (uint32_t)f32_to_bf16(s.x) | ((uint32_t)f32_to_bf16(s.y) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16(s.z) | ((uint32_t)f32_to_bf16(s.w) << 16);
+      *(uint2*)(out + (size_t)t * H + c) = make_uint2(lo, hi);
+    }
+  }
+}
+
 constexpr size_t kPAlign = 256;
 inline size_t pround(size_t v) { return (v + kPAlign - 1) / kPAlign * kPAlign; }
 
@@ -540,8 +610,12 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   }
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill down launch");
-  hipLaunchKernelGGL(prefill_combine_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
-                     (uint16_t*)h.out, h.H, h.top_k, h.overwrite);
+  if (h.top_k <= kCombineSlots)
+    hipLaunchKernelGGL(prefill_combine8_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
+                       (uint16_t*)h.out, h.H, h.top_k, h.overwrite);
+  else
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
+                       (uint16_t*)h.out, h.H, h.top_k, h.overwrite);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill combine launch");
   return GI_OK;
