@@ -141,6 +141,7 @@ struct D1Pro {
   uint32_t id_key[kSlots];    // the same in id order (radix select)
   float id_es[kSlots];
   int rpart[kW][kRankKeys];   // rank select: wave w's count of its keys above each key
+  __attribute__((aligned(16))) unsigned long long rkeys[kW][16];  // rank select: the 16 keys wave w reads
   int uexp[kMaxU];
   float uw[kMaxU];
   float cb[kMaxH / 8];        // -24 * the sum of each 8-value chunk of x (zero past the scale groups)
@@ -267,18 +268,25 @@ __device__ __forceinline__ void d1_rank_count(const D1Args& a, D1Pro& P, const R
     k.c[v] = ((unsigned long long)key << 10) | (unsigned long long)(1023 - e);
     k.es[v] = a.expert_scale ? __uint_as_float(r.es[v]) : 1.f;
   }
-  // keys j = 16w + jj: lane (16w + jj) % 64 of c[w / 4]
+  // keys j = 16w + jj: lane (16w + jj) % 64 of c[w / 4]; those 16 lanes put
+  // them in the wave's own LDS row, and every lane reads the row back (same
+  // wave: ordered without a barrier; broadcast reads, all issued at once)
   const unsigned long long src = wave < 4 ? k.c[0] : k.c[1];
-  const uint32_t src_lo = (uint32_t)src, src_hi = (uint32_t)(src >> 32);
   const int l0 = (wave & 3) * 16;
+  if (lane >= l0 && lane < l0 + 16) P.rkeys[wave][lane - l0] = src;
+  lds_fence();
+  unsigned long long cj[16];
+#pragma unroll
+  for (int jj = 0; jj < 16; jj += 2) {
+    const uint4 v = *(const uint4*)&P.rkeys[wave][jj];
+    cj[jj] = ((unsigned long long)v.y << 32) | v.x;
+    cj[jj + 1] = ((unsigned long long)v.w << 32) | v.z;
+  }
   int n0 = 0, n1 = 0;
 #pragma unroll
   for (int jj = 0; jj < 16; ++jj) {
-    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)src_lo, l0 + jj);
-    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)src_hi, l0 + jj);
-    const unsigned long long cj = ((unsigned long long)hi << 32) | lo;
-    n0 += cj > k.c[0] ? 1 : 0;
-    n1 += cj > k.c[1] ? 1 : 0;
+    n0 += cj[jj] > k.c[0] ? 1 : 0;
+    n1 += cj[jj] > k.c[1] ? 1 : 0;
   }
   P.rpart[wave][lane] = n0;
   P.rpart[wave][kWave + lane] = n1;
