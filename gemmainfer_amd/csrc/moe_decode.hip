@@ -1295,9 +1295,10 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
 // wait of the gate/up products has an exact count.  The down words are
 // needed only after the activation exchange: NI = 1 issues them after its
 // item's products, NI = 2 after its first item's products, so that the
-// items' words (whose products are on the critical path) are served first.  NI = 3 is the general path (two items in
-// flight, the next one loaded as each finishes), which issues the down words
-// after its items (registers: a rare case).
+// items' words (whose products are on the critical path) are served first.
+// NI = 3 is the general path (two items in flight, the next one loaded as
+// each finishes), which issues the down words after its items (registers: a
+// rare case).
 template <int KBW, int NI, int BPW>
 __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P, const GuLds& L, int U,
                                          int uexp_v, uint16_t* act, const DnPlan& dp, int n_items,

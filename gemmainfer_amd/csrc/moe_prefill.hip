@@ -446,7 +446,8 @@ __global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, c
 #pragma unroll
     for (int k = 0; k < kCombineSlots; ++k) {
       // a row's resource (its offsets stay below 2^32 whatever the row count)
-      const __amdgpu_buffer_rsrc_t ry = buffer_rsrc(y + (size_t)max(pos[k], 0) * H, pos[k] >= 0 ? (uint32_t)H * 4u : 0u);
+      const __amdgpu_buffer_rsrc_t ry =
+          buffer_rsrc(y + (size_t)max(pos[k], 0) * H, pos[k] >= 0 ? (uint32_t)H * 4u : 0u);
 #pragma unroll
       for (int i = 0; i < kCombineChunks; ++i) {
         const int c = c0 + i * 1024;
