@@ -520,6 +520,12 @@ bool moe_prefill_supported(const MoeHostArgs& h) {
   if (h.H % 64 || h.I % 32) return false;
   if (h.gs % 32 || log2_exact(h.gs / 32) < 0 || kPChunk % (h.gs / 32)) return false;
   if (h.top_k > 64 || h.E > 1024) return false;
+  // a workgroup's scales sit in LDS beside its static arrays (the gate/up sums
+  // of a row tile, the staged A tiles): a launch past the CU's 160 KB fails
+  constexpr size_t kLds = 160 * 1024, kDnStatic = 2 * kPChunk * kPRT * 64 * sizeof(uint4),
+                   kGuStatic = 16 * 256 * sizeof(float) + kDnStatic;
+  if ((size_t)h.Ggu * 64 * sizeof(uint2) + kGuStatic > kLds || (size_t)h.Gd * 64 * sizeof(uint2) + kDnStatic > kLds)
+    return false;
   const long long P = (long long)h.M * h.top_k;
   // 32-bit buffer offsets (loads past K read an offset past the resource)
   if ((long long)h.E * (h.H / 8) * 2 * h.I * 4 >= (1LL << 32)) return false;

@@ -216,6 +216,26 @@ def test_prefill_duplicates_invalid_skewed(small):
     assert_bf16_close(out, ref, "prefill duplicates/invalid")
 
 
+@pytest.mark.parametrize("I", [7168, 7200])
+def test_prefill_scale_table_at_lds_limit(I):
+    """Group size 32 puts I / 32 scale groups of a down workgroup's 64 column
+    quads in LDS beside the staged tiles: at I = 7168 that workgroup uses the
+    whole 160 KB of a CU, at I = 7200 it would not fit and the call takes the
+    general path instead of failing its launch."""
+    m, top_k, gs, H = 64, 2, 32, 256
+    W = synth.moe_weights(E=4, H=H, I=I, group_size=gs, seed=31)
+    Wd = _dev(W)
+    g = torch.Generator().manual_seed(32)
+    idx = torch.randint(0, 4, (m, top_k), generator=g, dtype=torch.int32)
+    w = torch.rand(m, top_k, generator=g).to(torch.bfloat16)
+    x = synth.activations(m, H, seed=33)
+    out = torch.zeros(m, H, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    ref, _ = _oracle_moe(x, W, idx, w, torch.zeros(m, H), gs)
+    assert_bf16_close(out, ref, f"prefill I={I} gs32")
+
+
 def test_prefill_layer_matches_oracle_and_is_deterministic(gemma128):
     """Layer mode through the prefill path: routing bit-exact, output within
     tolerance, and bitwise-identical across calls."""
