@@ -15,17 +15,22 @@ Measurement:
     Each step's N(0,1) logits are relabelled (a permutation of expert ids,
     values unchanged) so that every copy's experts are visited in rotation:
     >= 1 GB of other weights is read between two reads of the same expert
-    bytes, so the 256 MB MALL cannot serve them.  The realised minimum reuse
-    distance is reported.
-  * W warmup steps, then K steps captured in one HIP graph and replayed
-    between HIP events on the launch stream (synchronised on both sides);
-    us_per_layer = elapsed / K.  Hot-cache (same weights every step) and
+    bytes inside the timed replay, so the 256 MB MALL cannot serve them.
+  * W warmup steps, then K steps captured in one HIP graph, replayed once
+    untimed (the graph's upload), then 1 GiB of other memory is read (a
+    cache flush), then the graph is replayed between HIP events on the
+    launch stream (synchronised on both sides); us_per_layer = elapsed / K.
+    The realised minimum reuse distance, counting the untimed replay and the
+    flush, is reported.  Hot-cache (same weights every step) and
     stream-launched (no graph, Python ctypes per call) figures are reported
     separately; neither is ``value``.
   * Algorithmic bytes per layer = unique experts x 3,069,440 B (packed
     gate_up + down words and their bf16 scales), activations excluded.
   * cpu_baseline: the reference's PyTorch CPU dequant+matmul path
     (oracle/cpu_baseline.py), timed on this host's cores on a bounded sample.
+  * The default line also carries every other BASELINE config under the
+    same clock (``configs``): the W4A16 linear, the prefill
+    layer at M=512 and the lm_head at M=6.
 """
 from __future__ import annotations
 
@@ -96,21 +101,47 @@ def make_steps(m, noise, seed, n_desc):
     return steps
 
 
-def min_reuse_distance_bytes(steps, order, gs=None):
-    """Smallest number of weight bytes read between two reads of one expert."""
+def min_reuse_distance_bytes(steps, order, gs=None, prior=(), gap_bytes=0):
+    """Smallest number of bytes read between a read of one expert's weights in
+    the timed ``order`` and the previous read of the same bytes: earlier reads
+    in ``order`` or in ``prior`` (the steps run before the timed region: the
+    launch before capture and the graph's upload replay), with ``gap_bytes``
+    of other reads (the cache flush) between ``prior`` and ``order``."""
     eb = expert_bytes(gs=gs)
     last, touched, best = {}, 0, None
-    for s in order:
+
+    def visit(s, timed):
+        nonlocal touched, best
         st = steps[s]
         for e in st["unique"]:
             key = (st["copy"], e)
-            if key in last:
+            if timed and key in last:
                 d = touched - last[key]
                 best = d if best is None else min(best, d)
         for e in st["unique"]:
             last[(st["copy"], e)] = touched
         touched += st["U"] * eb
+
+    for s in prior:
+        visit(s, False)
+    touched += gap_bytes
+    for s in order:
+        visit(s, True)
     return best
+
+
+# Bytes read between a graph's untimed upload replay and its timed replay:
+# more than the 256 MB MALL and the 32 MB of L2, so the timed replay cannot
+# find the upload replay's weights in a cache.
+FLUSH_BYTES = 1 << 30
+_FLUSH = {}
+
+
+def flush_caches(device):
+    buf = _FLUSH.get(device)
+    if buf is None:
+        buf = _FLUSH[device] = torch.zeros(FLUSH_BYTES // 8, dtype=torch.int64, device=device)
+    buf.max()  # reads every byte once
 
 
 class LayerRunner:
@@ -166,6 +197,7 @@ def time_graph(runner, order, device):
             runner.launch(i)
     torch.cuda.synchronize()
     g.replay()  # untimed replay: first replay uploads the graph
+    flush_caches(device)
     torch.cuda.synchronize()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -215,7 +247,8 @@ def bench_config(m, noise, seed, copies, steps, warmup, device, gs=None):
         "unique_experts_mean": mean_u,
         "unique_experts_range": [min(desc[i]["U"] for i in order), max(desc[i]["U"] for i in order)],
         "algorithmic_bytes_per_layer": nbytes,
-        "min_reuse_distance_bytes": min_reuse_distance_bytes(desc, order, gs),
+        "min_reuse_distance_bytes": min_reuse_distance_bytes(desc, order, gs, prior=[order[0]] + order,
+                                                             gap_bytes=FLUSH_BYTES),
         "hot_cache_us_per_layer": hot_us,
         "stream_launched_us_per_layer": stream_us,
     }
@@ -1055,6 +1088,34 @@ def main():
             other[key] = bench_config(m, noise, seed, copies, args.steps, args.warmup, device, 64)
             print(f"[bench] group size 64 M={m} {other[key]['us_per_layer']:.2f} us "
                   f"{other[key]['gbps']:.0f} GB/s", file=sys.stderr, flush=True)
+    # the other BASELINE configs on the same clock: configs[0] (W4A16 linear,
+    # M=1), configs[3] (prefill, M=512) and configs[4] (lm_head, M=6)
+    del copies
+    torch.cuda.empty_cache()
+    pf = bench_prefill(min(args.steps, 50), min(args.warmup, 5), device)
+    print(f"[bench] prefill M=512 {pf['value']:.1f} us {pf['gbps']:.0f} GB/s "
+          f"(8-row chunks {pf['chunked_8row_us_per_layer']:.0f} us)", file=sys.stderr, flush=True)
+    torch.cuda.empty_cache()
+    lin = bench_linear("linear", args.steps, args.warmup, device)
+    print(f"[bench] linear M=1 {lin['us_per_launch']:.2f} us {lin['value']:.0f} GB/s", file=sys.stderr, flush=True)
+    lmh = bench_linear("lm_head", args.steps, args.warmup, device)
+    print(f"[bench] lm_head M=6 {lmh['us_per_launch']:.2f} us {lmh['value']:.0f} GB/s", file=sys.stderr, flush=True)
+    torch.cuda.empty_cache()
+
+    def cfg_row(us, nbytes, **extra):
+        gbps = nbytes / (us * 1e-6) / 1e9
+        return {"us": us, "gbps": gbps, "frac": gbps / PEAK_GBPS, "algorithmic_bytes": nbytes, **extra}
+
+    configs = {
+        "cfg0_linear_M1": cfg_row(lin["us_per_launch"], lin["algorithmic_bytes_per_launch"]),
+        "cfg1_moe_M1": cfg_row(m1["us_per_layer"], m1["algorithmic_bytes_per_layer"],
+                               unique_experts_mean=m1["unique_experts_mean"]),
+        "cfg2_moe_M7": cfg_row(m7["us_per_layer"], m7["algorithmic_bytes_per_layer"],
+                               unique_experts_mean=m7["unique_experts_mean"]),
+        "cfg3_prefill_M512": cfg_row(pf["value"], pf["algorithmic_bytes_per_layer"], mfma_util=pf["mfma_util"],
+                                     chunked_8row_us=pf["chunked_8row_us_per_layer"]),
+        "cfg4_lm_head_M6": cfg_row(lmh["us_per_launch"], lmh["algorithmic_bytes_per_launch"]),
+    }
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(args.cpu_budget_s, 100000)
@@ -1096,6 +1157,8 @@ def main():
         "stream_ceiling": ceiling,
         "group_size_64": other or None,
         "router_front_end": fe,
+        "configs": configs,
+        "cache_flush_bytes_before_timed_replay": FLUSH_BYTES,
     }
     print(json.dumps(res))
 

@@ -46,6 +46,7 @@ SIGNATURES = {
                                             c_void_p, c_int, c_void_p, c_int, c_void_p, c_int,
                                             c_void_p, c_int, c_int, c_int, c_int, c_int, c_int,
                                             c_int, c_void_p]),
+    "gi_fused_batched_moe_static_status": (c_int, [POINTER(c_int32), c_int, c_void_p]),
     "gi_moe_layer_from_logits": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p,
                                          c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_int,
                                          c_void_p, c_void_p, c_void_p,

@@ -38,16 +38,18 @@ int device_cu_count() {
 
 // Error flags of up to 64 devices, one 128-byte line each, in host memory
 // mapped into every device (coherent: a kernel's store is visible to the
-// host without a synchronisation).  Allocated on first use.
+// host without a synchronisation).  One pinned page per process, allocated
+// by gi_device_error_flags or by the first MoE launch whose stream is not
+// capturing a graph (an allocation there could invalidate the capture); a
+// failed allocation is tried again on the next such call.
 namespace {
 constexpr int kFlagStride = 32;  // ints
 std::mutex g_flag_mu;
 int* g_flags = nullptr;
-bool g_flags_failed = false;
 
 int* flags_host(bool allocate) {
   std::lock_guard<std::mutex> lk(g_flag_mu);
-  if (allocate && !g_flags && !g_flags_failed) {
+  if (allocate && !g_flags) {
     void* p = nullptr;
     if (hipHostMalloc(&p, 64 * kFlagStride * sizeof(int),
                       hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) == hipSuccess && p) {
@@ -55,17 +57,25 @@ int* flags_host(bool allocate) {
       g_flags = (int*)p;
     } else {
       (void)hipGetLastError();
-      g_flags_failed = true;
     }
   }
   return g_flags;
 }
+
+bool capturing(hipStream_t stream) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return true;  // unknown: do not allocate
+  }
+  return cs != hipStreamCaptureStatusNone;
+}
 }  // namespace
 
-int* device_error_flag(bool allocate) {
+int* device_error_flag(bool allocate, hipStream_t stream) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-  int* h = flags_host(allocate);
+  int* h = flags_host(allocate && !capturing(stream));
   if (!h) return nullptr;
   void* d = nullptr;
   if (hipHostGetDevicePointer(&d, h + dev * kFlagStride, 0) != hipSuccess) {
@@ -77,7 +87,7 @@ int* device_error_flag(bool allocate) {
 
 int read_device_error_flags(int device, int clear) {
   if (device < 0 || device >= 64) return fail(GI_ERR_INVALID_ARG, "device_error_flags: device index out of range");
-  int* h = flags_host(false);
+  int* h = flags_host(true);
   if (!h) return 0;
   volatile int* f = h + device * kFlagStride;
   const int v = *f;

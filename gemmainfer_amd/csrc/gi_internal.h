@@ -21,9 +21,10 @@ int device_cu_count();
 // mapped into the device, which kernels set when a bounded wait gives up
 // (null if the mapping is unavailable).  Read and cleared by
 // gi_device_error_flags without any device synchronisation.  The flags are
-// allocated (pinned host memory) on the first call with allocate = true;
+// allocated (pinned host memory) by gi_device_error_flags or by the first
+// call with allocate = true whose stream is not capturing a graph;
 // allocate = false only returns them once they exist.
-int* device_error_flag(bool allocate = true);
+int* device_error_flag(bool allocate, hipStream_t stream);
 int read_device_error_flags(int device, int clear);
 
 // ---- fused MoE --------------------------------------------------------------

@@ -1628,7 +1628,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
   k.overwrite = h.overwrite;
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
   k.status = status;
-  k.host_flag = device_error_flag(!h.no_alloc);
+  k.host_flag = device_error_flag(!h.no_alloc, h.stream);
   k.epochs = (unsigned long long*)state;
   k.act = (uint16_t*)((char*)state + moe_state::act_offset());
   k.part = (float*)((char*)state + moe_state::part_offset());

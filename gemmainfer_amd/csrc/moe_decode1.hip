@@ -56,6 +56,7 @@
 #include <mutex>
 
 #include "../../include/gemmainfer_amd.h"
+#include "decode1_split.h"
 #include "gi_common.h"
 #include "gi_internal.h"
 #include "moe_shared.h"
@@ -1082,9 +1083,8 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
   const int U = uniform(P.U);
   char* act = a.act + (size_t)parity * kActParity;
   char* part = a.part + (size_t)parity * kPartParity;
-  const int n_items = U * a.Tk;
-  const int n_whole = min(a.units, G - n_items);
-  const int n_left = a.units - n_whole;
+  const d1::Split sp = d1::split(G, U, a.Tk, a.units);
+  const int n_items = sp.n_items, n_whole = sp.n_whole, n_left = sp.n_left;
   const int Kv8 = min(a.H >> 3, a.Ggu << (a.gsh + 2));  // packed rows inside the gate/up scale groups
   // the workgroups that clear the previous launch's footprint: the idle ones
   // if there are any, else the units (they wait for the activations), else all
@@ -1239,14 +1239,11 @@ bool moe_decode1_supported(const MoeHostArgs& h) {
   const int Tk = h.I / 32, units = h.H / 32;
   const int umax = h.top_k < h.E ? h.top_k : h.E;
   const int v = variant_for(Tk, log2_exact(h.gs / 32));
-  if (v < 0 || umax > kMaxU || umax * Tk > G) return false;
+  if (v < 0 || umax > kMaxU || !d1::split_ok(G, umax, Tk, units, kMaxLeft)) return false;
   if (umax * h.Gd * 4 > kT) return false;  // down-scale staging: one chunk per thread
   // the split at the most unique experts (fewer experts only shrink the folded part)
-  const int items = umax * Tk;
-  const int n_whole = units < G - items ? units : G - items;
-  const int n_left = units - n_whole;
-  if (n_left > kMaxLeft || n_left > n_whole) return false;
-  if ((size_t)items * n_left * 32 * 4 > kPartParity) return false;
+  const d1::Split sp = d1::split(G, umax, Tk, units);
+  if ((size_t)sp.n_items * sp.n_left * 32 * 4 > kPartParity) return false;
   if ((size_t)umax * h.I * 2 > kActParity) return false;
   return resident_everywhere(v);
 }
@@ -1269,7 +1266,7 @@ int launch_moe_decode1(const MoeHostArgs& h, void* state, int* status) {
   k.act = (char*)state + moe_state::act_offset();
   k.part = (char*)state + moe_state::part_offset();
   k.status = status;
-  k.host_flag = device_error_flag(!h.no_alloc);
+  k.host_flag = device_error_flag(!h.no_alloc, h.stream);
   k.timeline = decode_timeline_slot();
   k.gu_bytes = (uint32_t)((h.H / 8) * 2 * h.I * 4);
   k.gus_bytes = (uint32_t)(h.Ggu * 2 * h.I * 2);

@@ -1204,7 +1204,7 @@ int launch_fused_moe(const MoeHostArgs& h) {
   k.Gd = h.Gd;
   k.overwrite = h.overwrite;
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
-  k.host_flag = device_error_flag();
+  k.host_flag = device_error_flag(true, h.stream);
 
   const size_t idx_es = h.idx_is64 ? 8 : 4;
   const size_t w_es = h.w_dtype == GI_DTYPE_FP32 ? 4 : 2;

@@ -189,7 +189,7 @@ __device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t 
 // two chunk buffers [2][kPChunk][kPRT][64] uint4.  The group size (32 <<
 // GSH) is a compile-time value, so every group end inside a chunk is known to
 // the compiler (a chunk holds whole groups); a last partial group is finished
-// after the loop.  Every row tile is multiplied (rows past the expert's pairs
+// at K.  Every row tile is multiplied (rows past the expert's pairs
 // are zeros): no branch on the tile count.
 template <int kPRing, int GSH>
 __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint32_t wbase, uint32_t wstep,
@@ -277,14 +277,13 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
         D[rt][3] = moe::mfma_bf16(A, q3, gstart ? zf : D[rt][3]);
         Db[rt] = moe::mfma_bf16(A, bc, gstart ? zf : Db[rt]);
       }
-      // k blocks past K multiply zeros (their loads read nothing) and add
-      // nothing: a group that K ends inside is finished below
-      if (j % kKbpg == kKbpg - 1 && kb < KB) epilogue(kb >> GSH);
+      // a group ends at its last k block or at K (a group that K ends inside
+      // is finished there: the next group start, past K, resets D); k blocks
+      // past K multiply zeros (their loads read nothing) and add nothing
+      if (kb < KB && (j % kKbpg == kKbpg - 1 || kb == KB - 1)) epilogue(kb >> GSH);
       wr[j] = wload(kb + kPRing);
     }
   }
-  // K ends inside a group: its partial sums
-  if (KB % kKbpg) epilogue((KB - 1) >> GSH);
 }
 
 // gate/up: workgroup (tile t, expert e) owns gate columns [128t, 128t+128)

@@ -72,6 +72,35 @@ int static_scratch(hipStream_t stream, unsigned char** out) {
 
 }  // namespace
 
+int read_static_status(int32_t* host_status, int clear, hipStream_t stream) {
+  if (!host_status) return fail(GI_ERR_INVALID_ARG, "fused MoE static status: null pointer");
+  *host_status = 0;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(GI_ERR_UNSUPPORTED, "fused MoE (static): device index >= 64");
+  unsigned char* base = nullptr;
+  {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_zeroed[dev]) return GI_OK;  // no static call has run on this device
+    base = g_scratch[dev];
+  }
+  int32_t v = 0;
+  e = hipMemcpyAsync(&v, base, sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+  if (e != hipSuccess) return hip_fail(e, "fused MoE static status copy");
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_fail(e, "fused MoE static status sync");
+  *host_status = v;
+  if (clear && v) {
+    // after a failed wait the whole scratch goes back to its first-use state
+    // (status, epochs and exchange buffers zero), as a fresh workspace would
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(256), dim3(256), 0, stream, (uint4*)base, kStaticScratchBytes / 16);
+    e = hipGetLastError();
+    if (e != hipSuccess) return hip_fail(e, "fused MoE static status clear");
+  }
+  return GI_OK;
+}
+
 int launch_fused_moe_static(MoeHostArgs h) {
   int st = check_moe_args(h);
   if (st != GI_OK) return st;
@@ -131,4 +160,8 @@ extern "C" int gi_fused_batched_moe_static(const void* x, int x_dtype, const int
   a.spin_limit = spin_limit;
   a.stream = reinterpret_cast<hipStream_t>(stream);
   return gi::launch_fused_moe_static(a);
+}
+
+extern "C" int gi_fused_batched_moe_static_status(int32_t* host_status, int clear, void* stream) {
+  return gi::read_static_status(host_status, clear, reinterpret_cast<hipStream_t>(stream));
 }

@@ -4,8 +4,14 @@
  * Plain C: pointers, sizes and int status codes; no torch or HIP types in the
  * signatures (a stream is passed as ``void*`` holding a hipStream_t, NULL =
  * the default stream).  Every entry point is asynchronous on that stream,
- * allocates no memory and performs no host<->device synchronisation, so it
- * can be recorded into a HIP graph.  Scratch memory is caller-owned
+ * allocates no device memory and performs no host<->device synchronisation,
+ * so it can be recorded into a HIP graph.  One exception, once per process:
+ * the page of device error flags (64 ints per device, pinned host memory,
+ * see gi_device_error_flags) is allocated by gi_device_error_flags or by the
+ * first fused-MoE call whose stream is not capturing a graph; a launch under
+ * capture before that has no host flag (its device status word still
+ * records a failed wait).  Call gi_device_error_flags once at start-up to
+ * allocate it at a time of your choosing.  Scratch memory is caller-owned
  * ("workspace"); it must be zero-filled once when first allocated and is
  * left zeroed by every successful call (the kernels reset their own
  * counters).  Calls that share one workspace must be ordered (same stream).
@@ -143,7 +149,12 @@ int gi_fused_batched_moe(const void* x, int x_dtype,
  * streams, other host threads) race.  Serves the decode kernel's shapes
  * (H, I multiples of 32, H <= 2816, I <= 768, group_size 64 * 2^k,
  * top_k <= 64; any M as launches of up to 8 rows); other shapes return
- * GI_ERR_WORKSPACE.  Results are bitwise those of gi_fused_batched_moe.   */
+ * GI_ERR_WORKSPACE.  Results are bitwise those of gi_fused_batched_moe.
+ * Errors: a bounded wait that gives up writes NaN into the outputs it could
+ * not complete and sets the status word of this device's static scratch
+ * (read it with gi_fused_batched_moe_static_status); it also sets the host
+ * flag of gi_device_error_flags if that page already exists (this entry
+ * never allocates it).                                                     */
 int gi_fused_batched_moe_static(const void* x, int x_dtype,
                                 const int32_t* gu_packed, const void* gu_scales, int gu_groups,
                                 const int32_t* d_packed, const void* d_scales, int d_groups,
@@ -152,6 +163,16 @@ int gi_fused_batched_moe_static(const void* x, int x_dtype,
                                 void* out,
                                 int M, int H, int I, int E, int top_k, int group_size,
                                 int spin_limit, void* stream);
+
+/* Status word of the current device's static scratch (the device-side error
+ * bits, GI_DEVICE_*, of gi_fused_batched_moe_static calls since the last
+ * clearing read): copied to *host_status after the work queued on `stream`
+ * (synchronises the stream); if it is non-zero and clear != 0, the whole
+ * static scratch is then zero-filled by a kernel on `stream` (its first-use
+ * state: status, launch epochs and exchange buffers).  No counterpart in the reference (its launches report
+ * no errors, csrc/marlin.cu:699-701); for callers of the static entry.
+ * 0 if no static call has run on this device.  Not for use under capture. */
+int gi_fused_batched_moe_static_status(int32_t* host_status, int clear, void* stream);
 
 /* Router + fused MoE: logits [M, E] (bf16/fp32) are routed as
  * gi_moe_route_topk_softmax does (weights rounded to bf16), out[M, H] is
@@ -206,7 +227,9 @@ int gi_moe_layer_from_hidden(const void* x, int x_dtype, const void* router_scal
  * complete, so no wrong finite value is ever returned.  No counterpart in
  * the reference, whose launches report no errors (csrc/marlin.cu:699-701):
  * for callers that want such errors without a synchronisation of their own
- * (gemmainfer_csrc checks it before each MoE call).                       */
+ * (gemmainfer_csrc checks it before each MoE call).  The first call in a
+ * process allocates the flag page (pinned host memory, 8 KiB) if no MoE
+ * launch has yet; do that call outside graph capture.                     */
 int gi_device_error_flags(int device, int clear);
 
 /* Copies the workspace's device status word to *host_status (synchronises

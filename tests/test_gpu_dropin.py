@@ -298,3 +298,90 @@ def test_one_token_layer_routing(e, case):
     np.testing.assert_allclose(np64(w)[finite], ref_w[finite], rtol=2.0 ** -7)
     if case != "nan":
         assert_bf16_close(out, ref_out, f"routing {case} E={e}")
+
+
+def _one_token_case(case, idx, w, g):
+    """ids/weights of one token for the edge cases of the reference's
+    launch_fused_batched_moe at M=1 (csrc/marlin.cu:286-296: the MAX_MATCH=1
+    path skips ids outside [0, E); :631-636: ids cast to int32, weights to the
+    activation dtype)."""
+    if case == "invalid_mix":
+        idx[0, 1], idx[0, 4], idx[0, 6] = -1, E, 4096
+    elif case == "all_invalid":
+        idx[0] = torch.tensor([-1, E, -7, 4096, E + 1, -1, 99999, -100], dtype=idx.dtype)
+    elif case == "int64":
+        idx = idx.to(torch.int64)
+    elif case == "w_fp32":
+        w = torch.rand(1, TOP_K, generator=g) + 0.05        # not bf16-representable: cast in the kernel
+    elif case == "w_fp16":
+        w = (torch.rand(1, TOP_K, generator=g) + 0.05).to(torch.float16)
+    elif case == "dups":
+        idx[0, 3] = idx[0, 0]
+        idx[0, 5] = idx[0, 0]
+        idx[0, 7] = idx[0, 2]
+        w = (torch.rand(1, TOP_K, generator=g) + 0.05).to(torch.bfloat16)
+    elif case == "dups_invalid":
+        idx[0] = torch.tensor([9, -1, 9, 9, E, 9, 9, -3], dtype=idx.dtype)   # U = 1
+    return idx, w
+
+
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("case", ["invalid_mix", "all_invalid", "int64", "w_fp32", "w_fp16", "dups",
+                                  "dups_invalid"])
+def test_one_token_kernel_reference_edge_cases(signed64, signed128, gs, case):
+    """The one-token kernel (every M=1 call at the Gemma shapes) on the
+    reference's edge cases, through the drop-in module, accumulating into a
+    non-zero out: ids outside [0, E) mixed in or all of them (U = 0: out is
+    left as it was), int64 ids, fp32 and fp16 routing weights, one expert in
+    several slots with different weights."""
+    W, Wd = signed64 if gs == 64 else signed128
+    g = torch.Generator().manual_seed(900)
+    x = synth.activations(1, H, seed=900)
+    idx, w = _routing(1, seed=900)
+    idx, w = _one_token_case(case, idx, w, g)
+    out_in = (torch.randn(1, H, generator=g) * 0.5).to(torch.bfloat16)
+    out = out_in.to(DEV).clone()
+    print(f"one-token edge case {case} gs={gs} ids={idx.tolist()}", flush=True)
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    ref, al = _oracle(W, x, idx, w, out_in, gs)
+    if case == "all_invalid":
+        assert al.num_unique == 0
+        assert torch.equal(out.cpu(), out_in)
+    assert_bf16_close(out, ref, f"one-token {case} gs={gs}")
+    assert ops.workspace_status() == 0
+
+
+@pytest.mark.parametrize("i,gs", [(704, 256), (768, 128), (768, 64)])
+def test_one_token_kernel_other_variants(i, gs):
+    """The one-token kernel's variants with the group size read at run time
+    (group 256 at I = 704) and with 12 unit steps (I = 768), at H = 2816,
+    E = 32, top-8, against the oracle, from ids and from logits."""
+    e = 32
+    Wc = _signed_weights_shape(e, H, i, gs, seed=910 + i + gs)
+    Wd = _dev(Wc)
+    x = synth.activations(1, H, seed=911)
+    logits = synth.router_logits(1, e, seed=912)
+    top, idx = torch.topk(logits, TOP_K, dim=-1)
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(torch.bfloat16)
+    idx = idx.to(torch.int32)
+    out_in = (torch.randn(1, H) * 0.1).to(torch.bfloat16)
+    out = out_in.to(DEV).clone()
+    print(f"one-token variant I={i} gs={gs}", flush=True)
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    ref, _ = _oracle(Wc, x, idx, w, out_in, gs)
+    assert_bf16_close(out, ref, f"one-token I={i} gs={gs}")
+    lo, lidx, lw = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                 Wd["down_packed"], Wd["down_scales"], TOP_K, gs)
+    np.testing.assert_array_equal(lidx.cpu().numpy(), idx.numpy())
+    ref0, _ = _oracle(Wc, x, idx, lw.cpu(), torch.zeros(1, H), gs)
+    assert_bf16_close(lo, ref0, f"one-token layer I={i} gs={gs}")
+
+
+def _signed_weights_shape(e, h, i, gs, seed):
+    W = synth.moe_weights(e, h, i, gs, seed=seed)
+    g = torch.Generator().manual_seed(seed + 7)
+    for k in ("gate_up_scales", "down_scales"):
+        W[k] = (torch.randn(W[k].shape, generator=g) * 0.02).to(torch.bfloat16)
+    return W

@@ -216,6 +216,27 @@ def test_prefill_duplicates_invalid_skewed(small):
     assert_bf16_close(out, ref, "prefill duplicates/invalid")
 
 
+@pytest.mark.parametrize("H,I,gs", [(320, 96, 64), (320, 96, 128), (256, 96, 128), (320, 128, 128),
+                                     (2816, 704, 256)])
+def test_prefill_partial_last_scale_group(H, I, gs):
+    """K ends inside a scale group that is not the last of its 8-k-block chunk
+    (I = 96: 3 k blocks; H = 320: 10): the partial group's sums must reach the
+    output, as in the oracle, which counts ceil(K / gs) groups."""
+    m, e, top_k = 64, 8, 4
+    W = synth.moe_weights(E=e, H=H, I=I, group_size=gs, seed=40 + I + gs)
+    Wd = _dev(W)
+    g = torch.Generator().manual_seed(41)
+    idx = torch.stack([torch.randperm(e, generator=g)[:top_k] for _ in range(m)]).to(torch.int32)
+    w = torch.softmax(torch.randn(m, top_k, generator=g), dim=-1).to(torch.bfloat16)   # sums to 1, gemma.py:78
+    x = synth.activations(m, H, seed=42)
+    print(f"prefill partial group H={H} I={I} gs={gs}", flush=True)
+    out = torch.zeros(m, H, dtype=torch.bfloat16, device=DEV)
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    ref, _ = _oracle_moe(x, W, idx, w, torch.zeros(m, H), gs)
+    assert_bf16_close(out, ref, f"prefill partial group H={H} I={I} gs={gs}")
+
+
 @pytest.mark.parametrize("I", [7168, 7200])
 def test_prefill_scale_table_at_lds_limit(I):
     """Group size 32 puts I / 32 scale groups of a down workgroup's 64 column

@@ -65,3 +65,46 @@ def test_static_scratch_rejects_shapes_it_cannot_serve():
                                          p, 1, 256, 128, 8, 2, 24, 0, stream)
     assert st == L.GI_ERR_WORKSPACE
     assert "caller workspace" in lib.gi_last_error().decode()
+
+
+@pytest.mark.parametrize("m", [1, 7])
+def test_static_entry_wait_timeout_is_reported(m):
+    """spin_limit=1 makes the static entry's bounded waits give up from the
+    host (every kernel still ends): outputs are then bitwise those of the
+    workspace entry point or NaN, never a wrong finite value;
+    gi_fused_batched_moe_static_status reports the timeout exactly when an
+    output is NaN, and its clearing read resets the static scratch, after
+    which a call is right again and the status reads 0."""
+    lib = L.load()
+    gs = 128
+    dev = torch.cuda.current_device()
+    W = synth.device_moe_weights(E, H, I, gs, DEV, seed=830)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    ws = torch.zeros(lib.gi_fused_moe_workspace_bytes(8, TOP_K, H, I, E), dtype=torch.uint8, device=DEV)
+    x = synth.activations(m, H, seed=840 + m).to(DEV)
+    logits = synth.router_logits(m, E, seed=840 + m, verify_noise=0.5)
+    top, idx = torch.topk(logits, TOP_K, dim=-1)
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(torch.bfloat16).to(DEV)
+    idx = idx.to(torch.int32).to(DEV)
+    out_in = (torch.randn(m, H) * 0.1).to(torch.bfloat16).to(DEV)
+    ref = out_in.clone()
+    L.check(lib.gi_fused_batched_moe(*_args(W, x, idx, w, ref, m, gs), _p(ws), ws.numel(), 0, stream),
+            "gi_fused_batched_moe")
+    print(f"static timeout m={m}", flush=True)
+    got = out_in.clone()
+    L.check(lib.gi_fused_batched_moe_static(*_args(W, x, idx, w, got, m, gs), 1, stream), "static spin 1")
+    torch.cuda.synchronize()
+    finite = torch.isfinite(got.float())
+    print(f"  {int((~finite).sum())} NaN outputs of {got.numel()}", flush=True)
+    assert torch.equal(got[finite], ref[finite]), "a finite output is wrong after a timeout"
+    st = ctypes.c_int32(-1)
+    L.check(lib.gi_fused_batched_moe_static_status(ctypes.byref(st), 1, stream), "static status")
+    assert st.value == (0 if bool(finite.all()) else L.DEVICE_SPIN_TIMEOUT)
+    lib.gi_device_error_flags(dev, 1)  # the host flag this timeout may have set
+    again = out_in.clone()
+    L.check(lib.gi_fused_batched_moe_static(*_args(W, x, idx, w, again, m, gs), 0, stream), "static after")
+    torch.cuda.synchronize()
+    assert torch.equal(again, ref)
+    L.check(lib.gi_fused_batched_moe_static_status(ctypes.byref(st), 1, stream), "static status")
+    assert st.value == 0
+    assert lib.gi_device_error_flags(dev, 1) == 0
