@@ -254,6 +254,67 @@ def bench_config(m, noise, seed, copies, steps, warmup, device, gs=None):
     }
 
 
+class DtypeRunner:
+    """gi_fused_batched_moe with fp16 or fp32 activations and scales (the
+    reference's other dtypes, marlin.cu:694-700): ids and weights routed on
+    the host from each step's logits (gemma.py:77-80), out accumulated into."""
+
+    def __init__(self, m, steps, copies, device, dt, gs=None):
+        self.lib = L.load()
+        self.m, self.dev, self.copies, self.dt = m, device, copies, dt
+        self.gs = GS if gs is None else gs
+        self.code = L.DTYPE_FP16 if dt == torch.float16 else L.DTYPE_FP32
+        self.x = synth.activations(m, H, seed=7).to(dt).to(device)
+        self.idx, self.w = [], []
+        for st in steps:
+            top, ix = torch.topk(st["logits"], TOP_K, dim=-1)
+            self.idx.append(ix.to(torch.int32).contiguous().to(device))
+            self.w.append(torch.softmax(top, dim=-1, dtype=torch.float32).to(dt).contiguous().to(device))
+        self.copy_of = [st["copy"] for st in steps]
+        self.out = torch.zeros(m, H, dtype=dt, device=device)
+        nbytes = self.lib.gi_fused_moe_workspace_bytes(m, TOP_K, H, I, E)
+        self.ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        torch.cuda.synchronize()
+
+    def launch(self, s):
+        W = self.copies[self.copy_of[s]]
+        stream = ctypes.c_void_p(torch.cuda.current_stream(self.dev).cuda_stream)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        st = self.lib.gi_fused_batched_moe(
+            p(self.x), self.code, p(W["gate_up_packed"]), p(W["gate_up_scales"]), W["gate_up_scales"].shape[1],
+            p(W["down_packed"]), p(W["down_scales"]), W["down_scales"].shape[1], p(self.idx[s]), L.DTYPE_INT32,
+            p(self.w[s]), self.code, p(self.out), self.m, H, I, E, TOP_K, self.gs, p(self.ws), self.ws.numel(), 0,
+            stream)
+        L.check(st, "gi_fused_batched_moe (fp16/fp32)")
+
+
+def bench_dtype(dt, steps, warmup, device):
+    """The MoE layer at M=1 and M=7 (configs[1], [2] routing) with fp16 or fp32
+    activations and scales: the same rotated weight words, scales in the dtype."""
+    copies = []
+    for c in range(COPIES):
+        Wc = synth.device_moe_weights(E, H, I, GS, device, seed=100 + c)
+        Wc["gate_up_scales"] = Wc["gate_up_scales"].to(dt)
+        Wc["down_scales"] = Wc["down_scales"].to(dt)
+        copies.append(Wc)
+    torch.cuda.synchronize()
+    rows = {}
+    for m, noise, seed in ((1, 0.0, 1), (7, 0.5, 2)):
+        desc = make_steps(m, noise, seed, warmup + steps)
+        runner = DtypeRunner(m, desc, copies, device, dt)
+        for i in range(warmup):
+            runner.launch(i)
+        torch.cuda.synchronize()
+        order = [warmup + i for i in range(steps)]
+        us = time_graph(runner, order, device)
+        mean_u = statistics.fmean(desc[i]["U"] for i in order)
+        sb = 2 if dt == torch.float16 else 4
+        nbytes = mean_u * (expert_bytes() + (sb - 2) * (math.ceil(H / GS) * 2 * I + math.ceil(I / GS) * H))
+        rows[f"M{m}"] = {"us_per_layer": us, "gbps": nbytes / (us * 1e-6) / 1e9, "unique_experts_mean": mean_u,
+                         "algorithmic_bytes_per_layer": nbytes}
+    return rows
+
+
 class StreamRunner:
     """gi_probe_stream_read over the bytes one layer launch of each step reads
     (the packed gate_up and down words and the scales of the step's unique
@@ -966,7 +1027,7 @@ def main():
                     help="scale group size of the MoE weights of the headline line (configs[1]/[2] use 128; "
                          "the engine's checkpoints use 64, reported beside it in the default run)")
     ap.add_argument("--workload", choices=["moe", "prefill", "dense", "router", "stream", "timeline",
-                                           "cpu_table", *LINEAR_WORKLOADS],
+                                           "cpu_table", "fp16", "fp32", *LINEAR_WORKLOADS],
                     default="moe",
                     help="moe (default: the BASELINE metric, M=1 value with M=7 beside it), prefill "
                          "(configs[3], M=512) or a dense W4A16 shape (linear = configs[0], "
@@ -1001,6 +1062,11 @@ def main():
         return
     if args.workload == "dense":
         print(json.dumps(bench_dense(args.steps, args.warmup, device)))
+        return
+    if args.workload in ("fp16", "fp32"):
+        dt = torch.float16 if args.workload == "fp16" else torch.float32
+        print(json.dumps({"workload": f"MoE layer with {args.workload} activations and scales",
+                          "rows": bench_dtype(dt, min(args.steps, 100), args.warmup, device)}))
         return
     if args.workload not in ("moe", "router", "stream", "timeline"):
         print(json.dumps(bench_linear(args.workload, args.steps, args.warmup, device,
@@ -1101,6 +1167,10 @@ def main():
     lmh = bench_linear("lm_head", args.steps, args.warmup, device)
     print(f"[bench] lm_head M=6 {lmh['us_per_launch']:.2f} us {lmh['value']:.0f} GB/s", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
+    fp16 = bench_dtype(torch.float16, min(args.steps, 100), args.warmup, device)
+    print(f"[bench] fp16 M=1 {fp16['M1']['us_per_layer']:.2f} us, M=7 {fp16['M7']['us_per_layer']:.2f} us",
+          file=sys.stderr, flush=True)
+    torch.cuda.empty_cache()
 
     def cfg_row(us, nbytes, **extra):
         gbps = nbytes / (us * 1e-6) / 1e9
@@ -1158,6 +1228,7 @@ def main():
         "group_size_64": other or None,
         "router_front_end": fe,
         "configs": configs,
+        "fp16_activations": fp16,
         "cache_flush_bytes_before_timed_replay": FLUSH_BYTES,
     }
     print(json.dumps(res))

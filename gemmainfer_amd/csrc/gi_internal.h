@@ -93,9 +93,10 @@ int launch_moe_router(const void* x, const void* router_scale, const void* gate,
                       int H, int E, float eps, hipStream_t stream);
 
 // fp16 / fp32 activations (generic_dtype.hip): VALU kernels, fp32 arithmetic,
-// the reference's rounding points in the activation dtype; the activations
-// of the MoE go through an fp32 buffer [M*top_k][I] in the workspace
-size_t moe_generic_workspace_bytes(int M, int top_k, int I);
+// the reference's rounding points in the activation dtype; the MoE runs in
+// launches of up to 64 slots whose activations [S][I], slot outputs [S][H]
+// (fp32) and Token-Union tables sit in the workspace
+size_t moe_generic_workspace_bytes(int M, int top_k, int H, int I);
 int launch_moe_generic(const MoeHostArgs& h, int x_dtype, void* act_ws, size_t act_bytes);
 int launch_w4a16_generic(const void* A, int a_dtype, const int32_t* B, const void* scales, int n_groups, void* C,
                          int M, int K, int N, int gs, float softcap, hipStream_t stream);

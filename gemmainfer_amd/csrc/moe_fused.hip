@@ -916,15 +916,15 @@ __global__ __launch_bounds__(256) void moe_align_kernel(Args a, int32_t* uniq, i
   if (tid < U) uniq[tid] = P.uexp[tid];
   if (tid == 0) *nuniq = U;
   if (tid < a.S) s2u[tid] = P.slot_u[tid];
-  if (tid == 0) {
+  // offsets[u + 1] = slots of unique experts 0..u (every thread one u, in parallel)
+  if (tid == 0) offsets[0] = 0;
+  for (int u = tid; u < U; u += 256) {
     int run = 0;
-    offsets[0] = 0;
-    for (int u = 0; u < U; ++u) {
-      int cnt = 0;
-      for (int s = 0; s < a.S; ++s) cnt += P.slot_u[s] == u;
-      run += cnt;
-      offsets[u + 1] = run;
+    for (int s = 0; s < a.S; ++s) {
+      const int su = P.slot_u[s];
+      run += (su >= 0 && su <= u);
     }
+    offsets[u + 1] = run;
   }
   if (tid < a.S && P.slot_u[tid] >= 0) {
     const int u = P.slot_u[tid];
@@ -1145,7 +1145,7 @@ size_t moe_workspace_bytes(int rows, int top_k, int H, int I, int E) {
 // their activations after the decode state and the barrier counters.
 size_t moe_workspace_bytes_any(int rows, int top_k, int H, int I, int E) {
   const size_t b = moe_workspace_bytes(rows, top_k, H, I, E);
-  const size_t g = prefill_base(H, I) + moe_generic_workspace_bytes(rows, top_k, I);
+  const size_t g = prefill_base(H, I) + moe_generic_workspace_bytes(rows, top_k, H, I);
   return g > b ? g : b;
 }
 

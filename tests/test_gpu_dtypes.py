@@ -84,6 +84,33 @@ def test_moe_duplicates_invalid_ids_and_many_rows(tag):
 
 
 @pytest.mark.parametrize("tag", ["fp16", "fp32"])
+@pytest.mark.parametrize("m,k,e", [(20, 2, 4), (3, 64, 80)])
+def test_moe_skewed_and_wide_top_k(tag, m, k, e):
+    """One expert taking most slots of a launch (several passes of 8 slots
+    over its words; a 20-row call is one launch of 40 slots at top_k 2), and
+    top_k = 64 (one row, 64 slots, per launch)."""
+    dt = DT[tag]
+    h, i, gs = 256, 128, 64
+    W = _moe_weights(e, h, i, gs, seed=840 + k, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    g = torch.Generator().manual_seed(841 + k)
+    if k == 2:
+        idx = torch.ones((m, k), dtype=torch.int32)
+        idx[::5, 1] = 3
+        idx[2, 0] = -1
+    else:
+        idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(m)]).to(torch.int32)
+    w = torch.softmax(torch.randn((m, k), generator=g), dim=-1).to(dt)
+    x = synth.activations(m, h, seed=842 + k).to(dt)
+    out_in = (torch.randn(m, h, generator=g) * 0.1).to(dt)
+    out = out_in.to(DEV).clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, tag), tag, f"skewed {tag} m={m} top_k={k}")
+
+
+@pytest.mark.parametrize("tag", ["fp16", "fp32"])
 def test_moe_reference_golden(tag):
     g = np.load(GOLDEN / f"moe_m3_dups_gs64_{tag}.npz")
     dt = DT[tag]
