@@ -320,23 +320,28 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// One or two token rows and K <= 8192: 16 columns per workgroup over ALL of
-// K, so N / 16 workgroups fill the chip without a K split and a launch has no
-// inter-workgroup exchange at all.  Lane (rrow = lane >> 2, colq = lane & 3)
-// loads the 16 bytes of columns 4colq..4colq+3 at packed row
-// 64j + 16wave + rrow: one wave instruction reads 16 rows x 64 B.  As in the
-// path above every load goes out first (weights, scales, then the token rows
-// into LDS), masked loads read zeros and zero scales cancel them.  The sums
-// over the 16 lanes of a column group: two DPP rotations inside each row of
-// 16 lanes, then the 16 (row, wave) partials of a column in LDS, added in a
-// fixed order.
-constexpr int kNarrowCols = 16;
+// One or two token rows and K <= 8192: NC (8 or 16) columns per workgroup
+// over ALL of K, so N / NC workgroups fill the chip without a K split and a
+// launch has no inter-workgroup exchange at all.  A lane loads the 16 bytes
+// of 4 columns: LPR = NC / 4 lanes cover a packed row, a wave instruction
+// reads RW = 64 / LPR rows x 4NC bytes (NC 16: 16 rows x 64 B; NC 8: 32 rows
+// x 32 B), a step of the 4 waves 4RW rows.  As in the path above every load
+// goes out first (weights, scales, then the token rows into LDS), masked
+// loads read zeros and zero scales cancel them.  The sums over the lanes of
+// a column group: DPP rotations inside each row of 16 lanes, then the 16
+// (row, wave) partials of a column in LDS, added in a fixed order.
+// Workgroup b runs on XCD b % 8: with a grid of whole rounds of 8 the tiles
+// are handed out so that each XCD holds a contiguous run of them, and tiles
+// that share a 128-byte line of the words meet in one L2.
+constexpr int kNarrowColsMax = 16;
 constexpr int kMaxSegs = 4;
+constexpr int kNarrowColsM1 = 16;  // tile width of the one- and two-row calls
+constexpr bool kNarrowXcdOrder = true;
 
 // Several projections of the same token rows in one launch: segment s owns
-// column tiles [tile0, tile0 + ceil(N / 16)).  GATED: segments 0 and 1 are
+// column tiles [tile0, tile0 + ceil(N / NC)).  GATED: segments 0 and 1 are
 // the gate and up projections of a gated MLP with the same N; every
-// workgroup computes both for its 16 columns and writes
+// workgroup computes both for its NC columns and writes
 // bf16(bf16(gelu_tanh(bf16(gate))) * bf16(up)) to segment 0's output.
 struct NarrowSeg {
   const int32_t* B;  // [K/8, N]
@@ -357,16 +362,24 @@ struct NarrowW {
   uint2 sc[S];
 };
 
-template <int S>
+template <int NC>
+struct NarrowShape {
+  static constexpr int LPR = NC / 4;      // lanes per packed row
+  static constexpr int RW = kWave / LPR;  // rows per wave instruction
+  static constexpr int RS = kWaves * RW;  // rows per step
+};
+
+template <int NC, int S>
 __device__ __forceinline__ void narrow_issue(const NarrowSeg& sg, int Kp, int rpg, int col, int wave, int rrow,
                                              NarrowW<S>& o) {
+  using Sh = NarrowShape<NC>;
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(sg.B, (uint32_t)((size_t)Kp * sg.N * 4));
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sg.S, (uint32_t)((size_t)sg.G * sg.N * 2));
   constexpr uint32_t kOob = 0xFFFFFFF0u;
   const bool col_ok = col < sg.N;
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const int r = 64 * j + 16 * wave + rrow;
+    const int r = Sh::RS * j + Sh::RW * wave + rrow;
     const bool ok = col_ok && r < Kp;
     const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * sg.N + col) * 4) : kOob,
                                                             0, kGemvNt);
@@ -378,17 +391,18 @@ __device__ __forceinline__ void narrow_issue(const NarrowSeg& sg, int Kp, int rp
   }
 }
 
-template <int NT, int S, int kRows>
+template <int NC, int NT, int S, int kRows>
 __device__ __forceinline__ void narrow_products(const NarrowW<S>& in, const uint4 (&xs)[NT][kRows],
                                                 const float (&xb)[NT][kRows], int wave, int rrow, uint32_t mq,
                                                 float (&acc)[4][NT]) {
+  using Sh = NarrowShape<NC>;
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[q][n] = 0.f;
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const int r = 64 * j + 16 * wave + rrow;
+    const int r = Sh::RS * j + Sh::RW * wave + rrow;
     const float sv[4] = {bf16lo(in.sc[j].x), bf16hi(in.sc[j].x), bf16lo(in.sc[j].y), bf16hi(in.sc[j].y)};
     const Q4Pairs u[4] = {unpack_q4(in.w[j].x, mq), unpack_q4(in.w[j].y, mq), unpack_q4(in.w[j].z, mq),
                           unpack_q4(in.w[j].w, mq)};
@@ -400,40 +414,44 @@ __device__ __forceinline__ void narrow_products(const NarrowW<S>& in, const uint
       for (int q = 0; q < 4; ++q) acc[q][n] = fmaf(sv[q], dot_unpacked(u[q], xp, bias), acc[q][n]);
     }
   }
-  // lanes c, c+4, c+8, c+12 of each 16-lane row share a column group
+  // lanes c, c + LPR, c + 2LPR, ... of each 16-lane row share a column group
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       float v = acc[q][n];
-      v += dpp_f32<0x124>(v);  // row_ror:4
-      v += dpp_f32<0x128>(v);  // row_ror:8
+      if constexpr (NC == 8) v += dpp_f32<0x122>(v);  // row_ror:2
+      v += dpp_f32<0x124>(v);                         // row_ror:4
+      v += dpp_f32<0x128>(v);                         // row_ror:8
       acc[q][n] = v;
     }
 }
 
-template <int NT, int S, bool GATED>
+template <int NC, int NT, int S, bool GATED>
 __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
-  constexpr int kRows = S * 64;  // packed rows covered (>= K / 8)
+  using Sh = NarrowShape<NC>;
+  constexpr int kRows = S * Sh::RS;  // packed rows covered (>= K / 8)
   constexpr int kOut = GATED ? 2 : 1;
   __shared__ uint4 xs[NT][kRows];
   __shared__ float xb[NT][kRows];
-  __shared__ float red[kOut][kWaves * 4][NT][kNarrowCols];
+  __shared__ float red[kOut][kWaves * 4][NT][NC];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
-  const int rrow = lane >> 2, colq = lane & 3;
+  const int rrow = lane / Sh::LPR, colq = lane % Sh::LPR;
   const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  const int nb = (int)gridDim.x, b0 = (int)blockIdx.x;
+  const int b = (kNarrowXcdOrder && nb % 8 == 0) ? (b0 % 8) * (nb / 8) + b0 / 8 : b0;
   // the workgroup's segment, by uniform selects (no dynamic kernarg index)
   NarrowSeg sg = a.seg[0];
 #pragma unroll
   for (int i = 1; i < kMaxSegs; ++i)
-    if (!GATED && (int)blockIdx.x >= a.seg[i].tile0) sg = a.seg[i];
-  const int c0 = ((int)blockIdx.x - sg.tile0) * kNarrowCols;
+    if (!GATED && b >= a.seg[i].tile0) sg = a.seg[i];
+  const int c0 = (b - sg.tile0) * NC;
   const int col = c0 + colq * 4;
 
   NarrowW<S> w0;
-  narrow_issue<S>(sg, Kp, rpg, col, wave, rrow, w0);
+  narrow_issue<NC, S>(sg, Kp, rpg, col, wave, rrow, w0);
   NarrowW<S> w1;
-  if constexpr (GATED) narrow_issue<S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
+  if constexpr (GATED) narrow_issue<NC, S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
   constexpr uint32_t kOob = 0xFFFFFFF0u;
   constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;
@@ -463,8 +481,8 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   const int slot = wave * 4 + (lane >> 4);
   {
     float acc[4][NT];
-    narrow_products<NT, S, kRows>(w0, xs, xb, wave, rrow, mq, acc);
-    if ((lane & 15) < 4) {
+    narrow_products<NC, NT, S, kRows>(w0, xs, xb, wave, rrow, mq, acc);
+    if ((lane & 15) < Sh::LPR) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -473,8 +491,8 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   }
   if constexpr (GATED) {
     float acc[4][NT];
-    narrow_products<NT, S, kRows>(w1, xs, xb, wave, rrow, mq, acc);
-    if ((lane & 15) < 4) {
+    narrow_products<NC, NT, S, kRows>(w1, xs, xb, wave, rrow, mq, acc);
+    if ((lane & 15) < Sh::LPR) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -482,8 +500,8 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
     }
   }
   __syncthreads();
-  if (tid < NT * kNarrowCols) {
-    const int n = tid / kNarrowCols, cc = tid - n * kNarrowCols;
+  if (tid < NT * NC) {
+    const int n = tid / NC, cc = tid - n * NC;
     const int oc = c0 + cc;
     if (n < a.M && oc < sg.N) {
       float y = 0.f;
@@ -504,15 +522,36 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   }
 }
 
-constexpr int kNarrowSteps[] = {2, 4, 6, 8, 12, 16};
+constexpr int kNarrowSteps[] = {2, 3, 4, 6, 8, 12, 16};
 
 bool narrow_path(int M, int K, int N) {
   const int Kp = K / 8;
   return M <= 2 && Kp <= 64 * 16 && N >= 1024 && (size_t)Kp * N * 4 < (1ull << 32);
 }
 
+template <int NC, int NT, bool G>
+int launch_narrow_t(const NarrowArgs& k, int tiles, int steps, hipStream_t stream) {
+  const dim3 grid((unsigned)tiles);
+  switch (steps) {
+#define GI_NARROW_CASE(S)                                                                         \
+  case S:                                                                                         \
+    hipLaunchKernelGGL((w4a16_narrow_kernel<NC, NT, S, G>), grid, dim3(kThreads), 0, stream, k); \
+    break;
+    GI_NARROW_CASE(2) GI_NARROW_CASE(3) GI_NARROW_CASE(4) GI_NARROW_CASE(6) GI_NARROW_CASE(8)
+    GI_NARROW_CASE(12) GI_NARROW_CASE(16)
+#undef GI_NARROW_CASE
+    default:
+      return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
+  }
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 narrow launch");
+}
+
 int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSeg* segs, int nseg, bool gated,
                   hipStream_t stream) {
+  // one plain projection uses the M=1 tile width; several projections and the
+  // gated form keep 16 columns (their grids are already large)
+  const int nc = (!gated && nseg == 1) ? kNarrowColsM1 : kNarrowColsMax;
   NarrowArgs k{};
   k.A = (const uint16_t*)A;
   k.M = M;
@@ -524,36 +563,29 @@ int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSe
   for (int i = 0; i < nseg; ++i) {
     k.seg[i] = segs[i];
     k.seg[i].tile0 = gated ? 0 : tiles;
-    if (!gated) tiles += (segs[i].N + kNarrowCols - 1) / kNarrowCols;
+    if (!gated) tiles += (segs[i].N + nc - 1) / nc;
   }
-  if (gated) tiles = (segs[0].N + kNarrowCols - 1) / kNarrowCols;
+  if (gated) tiles = (segs[0].N + nc - 1) / nc;
   for (int i = nseg; i < kMaxSegs; ++i) k.seg[i].tile0 = 0x7fffffff;
-  const int need = (K / 8 + 63) / 64;
-  int steps = 16;
+  const int rows_per_step = kWaves * (kWave / (nc / 4));
+  const int need = (K / 8 + rows_per_step - 1) / rows_per_step;
+  int steps = 0;
   for (int st : kNarrowSteps)
     if (st >= need) {
       steps = st;
       break;
     }
-  const dim3 grid((unsigned)tiles);
-  switch ((gated ? 1000 : 0) + (M <= 1 ? 100 : 200) + steps) {
-#define GI_NARROW_CASE(G, NT, S)                                                                          \
-  case (G ? 1000 : 0) + NT * 100 + S:                                                                     \
-    hipLaunchKernelGGL((w4a16_narrow_kernel<NT, S, G>), grid, dim3(kThreads), 0, stream, k); \
-    break;
-#define GI_NARROW_NT(G, NT) GI_NARROW_CASE(G, NT, 2) GI_NARROW_CASE(G, NT, 4) GI_NARROW_CASE(G, NT, 6) \
-  GI_NARROW_CASE(G, NT, 8) GI_NARROW_CASE(G, NT, 12) GI_NARROW_CASE(G, NT, 16)
-    GI_NARROW_NT(false, 1)
-    GI_NARROW_NT(false, 2)
-    GI_NARROW_NT(true, 1)
-    GI_NARROW_NT(true, 2)
-#undef GI_NARROW_NT
-#undef GI_NARROW_CASE
-    default:
-      return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
+  if (steps == 0) return fail(GI_ERR_UNSUPPORTED, "w4a16: no narrow-tile variant for this shape");
+  if (nc == 8) {
+    if (M <= 1) return launch_narrow_t<8, 1, false>(k, tiles, steps, stream);
+    return launch_narrow_t<8, 2, false>(k, tiles, steps, stream);
   }
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? GI_OK : hip_fail(e, "w4a16 narrow launch");
+  if (gated) {
+    if (M <= 1) return launch_narrow_t<16, 1, true>(k, tiles, steps, stream);
+    return launch_narrow_t<16, 2, true>(k, tiles, steps, stream);
+  }
+  if (M <= 1) return launch_narrow_t<16, 1, false>(k, tiles, steps, stream);
+  return launch_narrow_t<16, 2, false>(k, tiles, steps, stream);
 }
 
 // ---------------------------------------------------------------------------
