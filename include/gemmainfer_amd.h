@@ -114,9 +114,10 @@ int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
  *   idx        int32|int64 [M*top_k]  w  bf16|fp16|fp32 [M*top_k]
  *   out        T [M, H]               accumulated into (caller zeroes it)
  * T = x_dtype: bf16, fp16 or fp32 (marlin.cu:694-700).  bf16 runs the paths
- * below; fp16 and fp32 run VALU kernels (fp32 arithmetic, the weights cast
- * to T, the activation stored in T, one rounding of the output in T; two
- * launches).
+ * below; fp16 and fp32 run VALU kernels (fp32 arithmetic, the routing
+ * weights cast to T, the activation stored in T, one rounding of the output
+ * in T; the dequantised weights are never rounded; Token-Union in launches
+ * of up to 64 slots, top_k <= 64: alignment, gate/up, down, combine).
  * One kernel launch per 256/top_k rows (8 rows on the decode kernel); from
  * 64 rows with top_k <= 64, a power-of-two multiple of 32 as group size,
  * H % 64 == 0 and I % 32 == 0, the grouped-GEMM prefill path (align,
