@@ -187,8 +187,9 @@ __global__ __launch_bounds__(kThreads) void w4a16_kernel(GemvArgs a) {
 // ---------------------------------------------------------------------------
 // Decode-shape path (M <= 8): the same tiling (64 columns x one K slice per
 // workgroup, 4 packed rows x 256 B per wave instruction) with every global
-// load of the workgroup issued before any is used -- S steps of weight words
-// and their scales, then the slice's token rows -- so a launch is one memory
+// load of the workgroup issued before any is used -- the slice's token rows
+// (staged as soon as they land), then S steps of weight words and their
+// scales, which the products take as they land -- so a launch is one memory
 // round trip, the products and the split-K reduction.  Masked loads (rows
 // past the slice or past the last scale group, columns past N, tokens past
 // M) read zeros through the buffer range check; a zero scale then zeroes the
@@ -217,6 +218,18 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(a.S, (uint32_t)((size_t)a.G * a.N * 2));
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
   constexpr uint32_t kOob = 0xFFFFFFF0u;
+  constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;  // 16-byte x vectors per thread
+  uint4 xv[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const int idx = tid + kThreads * i;
+    const int n = idx / kRows, rr = idx - n * kRows;
+    const bool ok = n < NT && n < a.M && rr < nrows;
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(
+        ra, ok ? (uint32_t)(((size_t)n * a.K + 8 * (r_begin + rr)) * 2) : kOob, 0, 0);
+    xv[i] = make_uint4(d.x, d.y, d.z, d.w);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint4 w[S];
   uint2 sc[S];
 #pragma unroll
@@ -231,17 +244,6 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
     const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < a.G) ? (uint32_t)((g * a.N + col) * 2) : kOob,
                                                            0, 0);
     sc[j] = make_uint2(e.x, e.y);
-  }
-  constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;  // 16-byte x vectors per thread
-  uint4 xv[kXPer];
-#pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
-    const int idx = tid + kThreads * i;
-    const int n = idx / kRows, rr = idx - n * kRows;
-    const bool ok = n < NT && n < a.M && rr < nrows;
-    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(
-        ra, ok ? (uint32_t)(((size_t)n * a.K + 8 * (r_begin + rr)) * 2) : kOob, 0, 0);
-    xv[i] = make_uint4(d.x, d.y, d.z, d.w);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -325,9 +327,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
 // launch has no inter-workgroup exchange at all.  A lane loads the 16 bytes
 // of 4 columns: LPR = NC / 4 lanes cover a packed row, a wave instruction
 // reads RW = 64 / LPR rows x 4NC bytes (NC 16: 16 rows x 64 B; NC 8: 32 rows
-// x 32 B), a step of the 4 waves 4RW rows.  As in the path above every load
-// goes out first (weights, scales, then the token rows into LDS), masked
-// loads read zeros and zero scales cancel them.  The sums over the lanes of
+// x 32 B), a step of the 4 waves 4RW rows.  Every load goes out first: the
+// token rows (staged into LDS as soon as they land: the waits count in issue
+// order, so rows issued after the weights would wait for every weight word),
+// then the weights and scales, whose steps the products then take as they
+// land; masked loads read zeros and zero scales cancel them.  The sums over the lanes of
 // a column group: DPP rotations inside each row of 16 lanes, then the 16
 // (row, wave) partials of a column in LDS, added in a fixed order.
 // Workgroup b runs on XCD b % 8: with a grid of whole rounds of 8 the tiles
@@ -448,10 +452,6 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   const int c0 = (b - sg.tile0) * NC;
   const int col = c0 + colq * 4;
 
-  NarrowW<S> w0;
-  narrow_issue<NC, S>(sg, Kp, rpg, col, wave, rrow, w0);
-  NarrowW<S> w1;
-  if constexpr (GATED) narrow_issue<NC, S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
   const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
   constexpr uint32_t kOob = 0xFFFFFFF0u;
   constexpr int kXPer = (NT * kRows + kThreads - 1) / kThreads;
@@ -465,6 +465,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
                                                             0, 0);
     xv[i] = make_uint4(d.x, d.y, d.z, d.w);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  NarrowW<S> w0;
+  narrow_issue<NC, S>(sg, Kp, rpg, col, wave, rrow, w0);
+  NarrowW<S> w1;
+  if constexpr (GATED) narrow_issue<NC, S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < kXPer; ++i) {
@@ -832,24 +837,46 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MnArgs a)
   const int col = c0 + 4 * lr;
   const int slice = blockIdx.y;
   const int kb0 = (slice * kMnWaves + wave) * KBW;
+  // this K slice of the token rows (row M, rows past it and packed rows past
+  // K read as zero), loaded first and staged in the matrix-core k order as
+  // soon as they land: the waits count in issue order, so rows issued after
+  // the weights would wait for every weight word
+  constexpr uint32_t kOob = 0xFFFFFFF0u;
+  constexpr int kSp = kMnWaves * KBW * 4;  // packed rows of a slice
+  constexpr int kXn = ((kMfMaxM + 1) * kSp + kMnThreads - 1) / kMnThreads;  // M <= 16 rows
+  // the long slices (large K) keep the rows' loads behind the weights: their
+  // registers would not fit beside the weight words
+  constexpr bool kXFirst = kXn <= 8;
+  const int r0 = slice * kSp;
+  uint4* xs = mf_lds;  // [M + 1][kSp]
+  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
+  auto x_load = [&](int i) {
+    const int n = i / kSp, r = r0 + (i - n * kSp);
+    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
+        ra, (n < a.M && r < Kp) ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+  };
+  uint4 xv[kXFirst ? kXn : 1];
+  if constexpr (kXFirst) {
+#pragma unroll
+    for (int j = 0; j < kXn; ++j) xv[j] = x_load(tid + j * kMnThreads);
+    __builtin_amdgcn_sched_barrier(0);
+  }
   uint4 w0[KBW];
   uint2 s0[KBW / KPG];
   mn_issue<KBW, KPG>(sg, Kp, KB, col, kb0, lq, w0, s0);
   uint4 w1[GATED ? KBW : 1];
   uint2 s1[GATED ? KBW / KPG : 1];
   if constexpr (GATED) mn_issue<KBW, KPG>(a.seg[1], Kp, KB, col, kb0, lq, w1, s1);
-  // this K slice of the token rows in the matrix-core k order; row M (and
-  // rows past it, and packed rows past K) zero
-  constexpr uint32_t kOob = 0xFFFFFFF0u;
-  constexpr int kSp = kMnWaves * KBW * 4;  // packed rows of a slice
-  const int r0 = slice * kSp;
-  uint4* xs = mf_lds;  // [M + 1][kSp]
-  const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(a.A, (uint32_t)((size_t)a.M * a.K * 2));
-  for (int i = tid; i < (a.M + 1) * kSp; i += kMnThreads) {
-    const int n = i / kSp, r = r0 + (i - n * kSp);
-    const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(
-        ra, (n < a.M && r < Kp) ? (uint32_t)(((size_t)n * a.K + 8 * r) * 2) : kOob, 0, 0);
-    xs[i] = moe::mfma_k_order(make_uint4(v.x, v.y, v.z, v.w));
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (kXFirst) {
+#pragma unroll
+    for (int j = 0; j < kXn; ++j) {
+      const int i = tid + j * kMnThreads;
+      if (i < (a.M + 1) * kSp) xs[i] = moe::mfma_k_order(xv[j]);
+    }
+  } else {
+    for (int i = tid; i < (a.M + 1) * kSp; i += kMnThreads) xs[i] = moe::mfma_k_order(x_load(i));
   }
   __syncthreads();
 
