@@ -356,6 +356,7 @@ struct NarrowSeg {
 struct NarrowArgs {
   const uint16_t* A;  // [M, K]
   int M, K, gs, nseg;
+  uint32_t gmul;      // ceil(2^20 / (gs / 8)): scale group of a packed row by a multiply
   float cap;
   NarrowSeg seg[kMaxSegs];
 };
@@ -373,25 +374,34 @@ struct NarrowShape {
   static constexpr int RS = kWaves * RW;  // rows per step
 };
 
+// The loads of one projection's S steps.  Rows past K read zeros through the
+// buffer's range check (their x rows are zero too); a column past N (the last
+// tile of an N that is not a multiple of NC) reads other columns' words and
+// scales, into sums that are never stored.  The word offsets advance by a
+// constant per step; the scale group of packed row r is (r * gmul) >> 20 with
+// gmul = ceil(2^20 / rpg), which equals r / rpg for every r and rpg below 1024
+// (the error r * (gmul * rpg - 2^20) stays below 2^20).
 template <int NC, int S>
-__device__ __forceinline__ void narrow_issue(const NarrowSeg& sg, int Kp, int rpg, int col, int wave, int rrow,
+__device__ __forceinline__ void narrow_issue(const NarrowSeg& sg, int Kp, uint32_t gmul, int col, int wave, int rrow,
                                              NarrowW<S>& o) {
   using Sh = NarrowShape<NC>;
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(sg.B, (uint32_t)((size_t)Kp * sg.N * 4));
   const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(sg.S, (uint32_t)((size_t)sg.G * sg.N * 2));
-  constexpr uint32_t kOob = 0xFFFFFFF0u;
-  const bool col_ok = col < sg.N;
+  const uint32_t n = (uint32_t)sg.N, r0 = (uint32_t)(Sh::RW * wave + rrow);
+  const uint32_t wo = (r0 * n + (uint32_t)col) * 4u;
+  // the scales first: the waits count in issue order, and step j's products
+  // need its scales, not the later steps' words
 #pragma unroll
   for (int j = 0; j < S; ++j) {
-    const int r = Sh::RS * j + Sh::RW * wave + rrow;
-    const bool ok = col_ok && r < Kp;
-    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, ok ? (uint32_t)(((size_t)r * sg.N + col) * 4) : kOob,
-                                                            0, kGemvNt);
-    o.w[j] = make_uint4(d.x, d.y, d.z, d.w);
-    const int g = r / rpg;
-    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (ok && g < sg.G) ? (uint32_t)((g * sg.N + col) * 2) : kOob,
-                                                           0, 0);
+    const uint32_t g = ((r0 + (uint32_t)(Sh::RS * j)) * gmul) >> 20;
+    const u32x2_t e = __builtin_amdgcn_raw_buffer_load_b64(rs, (g * n + (uint32_t)col) * 2u, 0, 0);
     o.sc[j] = make_uint2(e.x, e.y);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < S; ++j) {
+    const u32x4_t d = __builtin_amdgcn_raw_buffer_load_b128(rb, wo + (uint32_t)j * (Sh::RS * 4u) * n, 0, kGemvNt);
+    o.w[j] = make_uint4(d.x, d.y, d.z, d.w);
   }
 }
 
@@ -443,12 +453,29 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   const int rrow = lane / Sh::LPR, colq = lane % Sh::LPR;
   const int Kp = a.K >> 3, rpg = a.gs >> 3;
   const int nb = (int)gridDim.x, b0 = (int)blockIdx.x;
-  const int b = (kNarrowXcdOrder && nb % 8 == 0) ? (b0 % 8) * (nb / 8) + b0 / 8 : b0;
-  // the workgroup's segment, by uniform selects (no dynamic kernarg index)
+  // XCD-aware order for grids of whole rounds of 8 (arithmetic, not a branch:
+  // the argument loads below then go out in one batch)
+  const int xo = (kNarrowXcdOrder && (nb & 7) == 0) ? 1 : 0;
+  const int b = b0 + xo * ((b0 & 7) * (nb >> 3) + (b0 >> 3) - b0);
+  // the workgroup's segment: every segment's fields are loaded in one batch
+  // and selected (a branch per segment would wait for each argument load in
+  // turn before the first vector load)
+  int si = 0;
+  if constexpr (!GATED) {
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; ++i) si += b >= a.seg[i].tile0 ? 1 : 0;
+  }
   NarrowSeg sg = a.seg[0];
 #pragma unroll
-  for (int i = 1; i < kMaxSegs; ++i)
-    if (!GATED && b >= a.seg[i].tile0) sg = a.seg[i];
+  for (int i = 1; i < kMaxSegs; ++i) {
+    const bool t = si >= i;
+    sg.B = t ? a.seg[i].B : sg.B;
+    sg.S = t ? a.seg[i].S : sg.S;
+    sg.C = t ? a.seg[i].C : sg.C;
+    sg.N = t ? a.seg[i].N : sg.N;
+    sg.G = t ? a.seg[i].G : sg.G;
+    sg.tile0 = t ? a.seg[i].tile0 : sg.tile0;
+  }
   const int c0 = (b - sg.tile0) * NC;
   const int col = c0 + colq * 4;
 
@@ -467,9 +494,9 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   }
   __builtin_amdgcn_sched_barrier(0);
   NarrowW<S> w0;
-  narrow_issue<NC, S>(sg, Kp, rpg, col, wave, rrow, w0);
+  narrow_issue<NC, S>(sg, Kp, a.gmul, col, wave, rrow, w0);
   NarrowW<S> w1;
-  if constexpr (GATED) narrow_issue<NC, S>(a.seg[1], Kp, rpg, col, wave, rrow, w1);
+  if constexpr (GATED) narrow_issue<NC, S>(a.seg[1], Kp, a.gmul, col, wave, rrow, w1);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int i = 0; i < kXPer; ++i) {
@@ -529,9 +556,23 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
 
 constexpr int kNarrowSteps[] = {2, 3, 4, 6, 8, 12, 16};
 
+// Packed rows a narrow launch addresses (whole steps of 64 or 128 rows, rows
+// past K included): every word offset stays below 2^32 when this many rows of
+// N columns do.
+size_t narrow_rows(int Kp) {
+  size_t rows = 0;
+  for (int rs : {64, 128})
+    for (int st : kNarrowSteps)
+      if (st * rs >= Kp) {
+        rows = std::max(rows, (size_t)st * rs);
+        break;
+      }
+  return rows;
+}
+
 bool narrow_path(int M, int K, int N) {
   const int Kp = K / 8;
-  return M <= 2 && Kp <= 64 * 16 && N >= 1024 && (size_t)Kp * N * 4 < (1ull << 32);
+  return M <= 2 && Kp <= 64 * 16 && N >= 1024 && narrow_rows(Kp) * N * 4 < (1ull << 32);
 }
 
 template <int NC, int NT, bool G>
@@ -562,6 +603,7 @@ int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSe
   k.M = M;
   k.K = K;
   k.gs = gs;
+  k.gmul = (uint32_t)(((1u << 20) + (uint32_t)(gs / 8) - 1) / (uint32_t)(gs / 8));
   k.cap = cap;
   k.nseg = nseg;
   int tiles = 0;
@@ -1262,7 +1304,7 @@ bool narrow_multi(int M, int K, const int* N, int n) {
   if (M > 2 || K / 8 > 64 * 16) return false;
   long total = 0;
   for (int i = 0; i < n; ++i) {
-    if ((size_t)(K / 8) * N[i] * 4 >= (1ull << 32)) return false;
+    if (narrow_rows(K / 8) * N[i] * 4 >= (1ull << 32)) return false;
     total += N[i];
   }
   return total >= 1024;
@@ -1286,7 +1328,7 @@ bool mfma_multi(int M, int K, const int* N, int n, int gs) {
 }
 
 bool gated_narrow(int M, int K, int N) {
-  return M <= 2 && K / 8 <= 64 * 16 && (size_t)(K / 8) * N * 4 < (1ull << 32);
+  return M <= 2 && K / 8 <= 64 * 16 && narrow_rows(K / 8) * N * 4 < (1ull << 32);
 }
 bool gated_mfma(int M, int K, int N, int gs) {
   return mfma_narrow_ok(M, K, gs, true) && (size_t)(K / 8) * N * 4 < (1ull << 32);

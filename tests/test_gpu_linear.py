@@ -31,6 +31,23 @@ def test_w4a16_linear(m, k, n, gs):
         record_parity("cfg0_linear", stats)
 
 
+@pytest.mark.parametrize("m,k,n,gs", [
+    (1, 2816, 1028, 96),   # N not a multiple of the 16-column tile; 12 packed rows per group
+    (2, 8000, 1024, 8000), # one group over all of K (1000 packed rows, the largest step count)
+    (1, 520, 2048, 40),    # 65 packed rows: most of the second step past K; 5 rows per group
+    (2, 256, 1036, 8),     # one packed row per group
+])
+def test_w4a16_narrow_path_odd_shapes(m, k, n, gs):
+    """One and two rows at N >= 1024 take the 16-column narrow kernel: rows past
+    K, columns past N and group sizes that are not a power of two."""
+    B, S = synth.linear_weights(k, n, gs, seed=m + 3 * n)
+    A = synth.activations(m, k, seed=k + 1)
+    C = torch.empty(m, n, dtype=torch.bfloat16, device=DEV)
+    gemmainfer_csrc.marlin_w4a16(A.to(DEV), B.to(DEV), S.to(DEV), C, gs)
+    ref = O.w4a16_linear(np64(A), B.numpy(), np64(S), gs)
+    assert_bf16_close(C, ref, f"narrow m={m} k={k} n={n} gs={gs}")
+
+
 def test_w4a16_reference_floor_groups_drop_tail():
     """A scales tensor with K//gs groups drops rows past the last group, like
     the reference kernel (marlin.cu:128)."""
