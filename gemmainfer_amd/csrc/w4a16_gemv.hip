@@ -361,6 +361,30 @@ struct NarrowArgs {
   NarrowSeg seg[kMaxSegs];
 };
 
+// The segment that owns column tile b.  Every segment's fields are loaded in
+// one batch and selected: a branch per segment would wait for each argument
+// load in turn before the kernel's first vector load.
+template <bool SINGLE>
+__device__ __forceinline__ NarrowSeg select_seg(const NarrowSeg (&seg)[kMaxSegs], int b) {
+  int si = 0;
+  if constexpr (!SINGLE) {
+#pragma unroll
+    for (int i = 1; i < kMaxSegs; ++i) si += b >= seg[i].tile0 ? 1 : 0;
+  }
+  NarrowSeg sg = seg[0];
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i) {
+    const bool t = si >= i;
+    sg.B = t ? seg[i].B : sg.B;
+    sg.S = t ? seg[i].S : sg.S;
+    sg.C = t ? seg[i].C : sg.C;
+    sg.N = t ? seg[i].N : sg.N;
+    sg.G = t ? seg[i].G : sg.G;
+    sg.tile0 = t ? seg[i].tile0 : sg.tile0;
+  }
+  return sg;
+}
+
 template <int S>
 struct NarrowW {
   uint4 w[S];
@@ -457,25 +481,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   // the argument loads below then go out in one batch)
   const int xo = (kNarrowXcdOrder && (nb & 7) == 0) ? 1 : 0;
   const int b = b0 + xo * ((b0 & 7) * (nb >> 3) + (b0 >> 3) - b0);
-  // the workgroup's segment: every segment's fields are loaded in one batch
-  // and selected (a branch per segment would wait for each argument load in
-  // turn before the first vector load)
-  int si = 0;
-  if constexpr (!GATED) {
-#pragma unroll
-    for (int i = 1; i < kMaxSegs; ++i) si += b >= a.seg[i].tile0 ? 1 : 0;
-  }
-  NarrowSeg sg = a.seg[0];
-#pragma unroll
-  for (int i = 1; i < kMaxSegs; ++i) {
-    const bool t = si >= i;
-    sg.B = t ? a.seg[i].B : sg.B;
-    sg.S = t ? a.seg[i].S : sg.S;
-    sg.C = t ? a.seg[i].C : sg.C;
-    sg.N = t ? a.seg[i].N : sg.N;
-    sg.G = t ? a.seg[i].G : sg.G;
-    sg.tile0 = t ? a.seg[i].tile0 : sg.tile0;
-  }
+  const NarrowSeg sg = select_seg<GATED>(a.seg, b);
   const int c0 = (b - sg.tile0) * NC;
   const int col = c0 + colq * 4;
 
@@ -870,11 +876,7 @@ __global__ __launch_bounds__(kMnThreads) void w4a16_mfma_narrow_kernel(MnArgs a)
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const int Kp = a.K >> 3, KB = a.K >> 5;
-  // the workgroup's segment, by uniform selects (no dynamic kernarg index)
-  NarrowSeg sg = a.seg[0];
-#pragma unroll
-  for (int i = 1; i < kMaxSegs; ++i)
-    if (!GATED && (int)blockIdx.x >= a.seg[i].tile0) sg = a.seg[i];
+  const NarrowSeg sg = select_seg<GATED>(a.seg, (int)blockIdx.x);
   const int c0 = ((int)blockIdx.x - sg.tile0) * kMnCols;
   const int col = c0 + 4 * lr;
   const int slice = blockIdx.y;
