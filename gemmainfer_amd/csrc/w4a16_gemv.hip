@@ -330,10 +330,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(GemvArgs a) {
 // x 32 B), a step of the 4 waves 4RW rows.  Every load goes out first: the
 // token rows (staged into LDS as soon as they land: the waits count in issue
 // order, so rows issued after the weights would wait for every weight word),
-// then the weights and scales, whose steps the products then take as they
-// land; masked loads read zeros and zero scales cancel them.  The sums over the lanes of
-// a column group: DPP rotations inside each row of 16 lanes, then the 16
-// (row, wave) partials of a column in LDS, added in a fixed order.
+// then the scales, then the weights, whose steps the products take as they
+// land; rows past K read zeros through the buffer range check.  The sums over
+// the lanes of a column group: DPP rotations inside each row of 16 lanes, permlane swaps
+// across the four rows, then the 4 wave partials of a column in LDS, added in
+// a fixed order.
 // Workgroup b runs on XCD b % 8: with a grid of whole rounds of 8 the tiles
 // are handed out so that each XCD holds a contiguous run of them, and tiles
 // that share a 128-byte line of the words meet in one L2.
@@ -461,7 +462,11 @@ __device__ __forceinline__ void narrow_products(const NarrowW<S>& in, const uint
       if constexpr (NC == 8) v += dpp_f32<0x122>(v);  // row_ror:2
       v += dpp_f32<0x124>(v);                         // row_ror:4
       v += dpp_f32<0x128>(v);                         // row_ror:8
-      acc[q][n] = v;
+      // then the four 16-lane rows: (r0 + r2) + (r1 + r3), in every lane
+      const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+      const float x = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+      const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+      acc[q][n] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
     }
 }
 
@@ -472,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   constexpr int kOut = GATED ? 2 : 1;
   __shared__ uint4 xs[NT][kRows];
   __shared__ float xb[NT][kRows];
-  __shared__ float red[kOut][kWaves * 4][NT][NC];
+  __shared__ float red[kOut][kWaves][NT][NC];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int rrow = lane / Sh::LPR, colq = lane % Sh::LPR;
   const int Kp = a.K >> 3, rpg = a.gs >> 3;
@@ -516,11 +521,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   __syncthreads();
 
   const uint32_t mq = q4_magic();
-  const int slot = wave * 4 + (lane >> 4);
+  const int slot = wave;  // one partial per wave and column
   {
     float acc[4][NT];
     narrow_products<NC, NT, S, kRows>(w0, xs, xb, wave, rrow, mq, acc);
-    if ((lane & 15) < Sh::LPR) {
+    if (lane < Sh::LPR) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -530,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   if constexpr (GATED) {
     float acc[4][NT];
     narrow_products<NC, NT, S, kRows>(w1, xs, xb, wave, rrow, mq, acc);
-    if ((lane & 15) < Sh::LPR) {
+    if (lane < Sh::LPR) {
 #pragma unroll
       for (int n = 0; n < NT; ++n)
 #pragma unroll
@@ -544,11 +549,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
     if (n < a.M && oc < sg.N) {
       float y = 0.f;
 #pragma unroll
-      for (int i = 0; i < kWaves * 4; ++i) y += red[0][i][n][cc];
+      for (int i = 0; i < kWaves; ++i) y += red[0][i][n][cc];
       if constexpr (GATED) {
         float u = 0.f;
 #pragma unroll
-        for (int i = 0; i < kWaves * 4; ++i) u += red[kOut - 1][i][n][cc];
+        for (int i = 0; i < kWaves; ++i) u += red[kOut - 1][i][n][cc];
         // activations.py:26-28 on bf16 tensors: each linear's output, the
         // gelu and the product are rounded to bf16
         const float g = round_to_bf16(gelu_tanh(round_to_bf16(y)));
