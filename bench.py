@@ -1178,7 +1178,11 @@ def main():
     print(f"[bench] prefill M=512 {pf['value']:.1f} us {pf['gbps']:.0f} GB/s "
           f"(8-row chunks {pf['chunked_8row_us_per_layer']:.0f} us)", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
-    lin = bench_linear("linear", args.steps, args.warmup, device)
+    # configs[0] moves 4.09 MB per step: 200 steps over its 300 rotated copies
+    # put 813 MB between two reads of a copy, more than every cache, with no
+    # flush read (which would also cool the address translation of every one
+    # of a short replay's ~4 us launches)
+    lin = bench_linear("linear", max(args.steps, 200), args.warmup, device)
     print(f"[bench] linear M=1 {lin['us_per_launch']:.2f} us {lin['value']:.0f} GB/s", file=sys.stderr, flush=True)
     lmh = bench_linear("lm_head", args.steps, args.warmup, device)
     print(f"[bench] lm_head M=6 {lmh['us_per_launch']:.2f} us {lmh['value']:.0f} GB/s", file=sys.stderr, flush=True)
