@@ -480,7 +480,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_narrow_kernel(NarrowArgs a) {
   __shared__ float red[kOut][kWaves][NT][NC];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int rrow = lane / Sh::LPR, colq = lane % Sh::LPR;
-  const int Kp = a.K >> 3, rpg = a.gs >> 3;
+  const int Kp = a.K >> 3;
   const int nb = (int)gridDim.x, b0 = (int)blockIdx.x;
   // XCD-aware order for grids of whole rounds of 8 (arithmetic, not a branch:
   // the argument loads below then go out in one batch)
