@@ -151,24 +151,31 @@ struct D1Pro {
   unsigned long long epoch;
 };
 
+template <bool F16>
 struct ItemLds {
-  uint4 xs[kMaxH / 8];            // x in the matrix-core k order, per packed row
+  uint4 xs[kMaxH / 8];            // x in the matrix-core k order, per packed row (fp16: the bf16 hi part)
+  uint4 xs_lo[F16 ? kMaxH / 8 : 1];  // fp16: the bf16 lo part (A row 1)
   uint4 xz[4 * kKbw];             // zeros: the A operand rows 1-15 (lanes lr > 0) read these
   float4 red[kW][16];             // per-wave sums: lane lr holds 4 gate (lr < 8) or up columns
   uint4 sa[4];                    // the item's 32 activations, matrix-core k order
   float4 fr[4][kMaxLeft * 8];     // folded products per packed row
   float4 rr[kW][8];               // folded unit reduction: each wave's sums (8 column quads)
 };
+template <bool F16>
 struct UnitLds {
-  uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 in matrix-core k order
+  uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 in matrix-core k order (fp16: hi)
+  uint4 sact_lo[F16 ? kMaxU * kMaxTk * 4 : 1];  // fp16: the bf16 lo parts
   float cbias[kMaxU * kMaxTk * 4];  // -24 * each chunk's sum
   uint4 dsc[kMaxU * kMaxGd * 4];    // down scales of the unit's columns [u][g][32]
   float4 red[kW][16];
 };
+template <bool F16>
 union D1Lds {
-  ItemLds it;
-  UnitLds un;
+  ItemLds<F16> it;
+  UnitLds<F16> un;
 };
+
+
 
 // Every 16-bit half non-zero.
 __device__ __forceinline__ bool chunk_ready(const u32x4_t v) {
@@ -418,7 +425,7 @@ __device__ __forceinline__ void d1_weights(const D1Args& a, D1Pro& P) {
 // marlin.cu:634-636).  The unique experts are in the order of their first
 // slot: for ids from a sorted top-k (gemma.py:77-80) that is the rank order
 // of the router-logits form, so both forms split the work alike.
-template <int VPL>
+template <int VPL, bool F16>
 __device__ __forceinline__ void d1_route_ids(const D1Args& a, D1Pro& P, const D1In<VPL>& in) {
   const int lane = threadIdx.x & (kWave - 1);
   const int S = a.top_k;
@@ -432,7 +439,7 @@ __device__ __forceinline__ void d1_route_ids(const D1Args& a, D1Pro& P, const D1
     const float wv = a.w_dtype == GI_DTYPE_FP32   ? __uint_as_float(in.wb)
                      : a.w_dtype == GI_DTYPE_FP16 ? fp16_to_f32((uint16_t)in.wb)
                                                   : bf16_to_f32(in.wb);
-    P.slot_w[lane] = round_to_bf16(wv);
+    P.slot_w[lane] = round_to_act<F16>(wv);
   }
   lds_fence();
   const int e = lane < S ? P.slot_e[lane] : -1;
@@ -489,7 +496,7 @@ __device__ __forceinline__ void clear_prev(const D1Args& a, unsigned long long e
 // registers, thread c holding 16-byte chunk c, until the workgroup knows its
 // role).  Ends with the routing in LDS (P.U, P.uexp; from router logits also
 // the selection in rank order) after the last barrier.
-template <int VPL>
+template <int VPL, bool F16>
 __device__ __forceinline__ void d1_start(const D1Args& a, D1Pro& P, u32x4_t* xv_out, int* parity_out) {
   const int tid = threadIdx.x, wave = uniform(tid >> 6);
   constexpr bool kRank = VPL * kWave <= kRankKeys;
@@ -525,7 +532,7 @@ __device__ __forceinline__ void d1_start(const D1Args& a, D1Pro& P, u32x4_t* xv_
         P.U = a.top_k;
       }
     } else {
-      d1_route_ids<VPL>(a, P, in);
+      d1_route_ids<VPL, F16>(a, P, in);
     }
     GI_STAMP(11);
     if (tid == 0) {
@@ -610,7 +617,7 @@ __device__ __forceinline__ void item_load(const D1Args& a, int e, int it, int c,
 // lr's column i; lanes lr >= 8 hold up columns) = sum over groups of
 // scale * (the group's products + its -24 * sum of x).  A group's first
 // product starts from zero.
-template <int GSH, int PH>
+template <int GSH, int PH, bool F16>
 __device__ __forceinline__ void item_products(const ItemRegs& r, const uint4* arow, float kbv, uint32_t mq,
                                               uint32_t mc, float (&y)[4]) {
   constexpr int kPg = 1 << GSH;
@@ -636,15 +643,15 @@ __device__ __forceinline__ void item_products(const ItemRegs& r, const uint4* ar
     bacc = (gstart ? 0.f : bacc) + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kbv), 4 * j));
     if ((PH + j + 1) % kPg == 0 || j == kKbw - 1) {  // a scale group ends
       const uint2 s2 = opaque(r.s[(PH + j) / kPg]);  // opaque: the variants' epilogues stay apart
-      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] += sc[i] * (D[i][0] + bacc);
+      for (int i = 0; i < 4; ++i) y[i] += sc[i] * ((F16 ? D[i][0] + D[i][1] : D[i][0]) + bacc);
     }
   }
 }
 
-template <int GSH>
-__device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLds& L, int it, int u, int c,
+template <int GSH, bool F16>
+__device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLds<F16>& L, int it, int u, int c,
                                          int n_left, char* act, char* part, const ItemRegs& r) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int lq = lane >> 4, lr = lane & 15;
@@ -661,7 +668,8 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
   const uint32_t mc = q4_high_bits();
   // A row 0 is the token (lanes lr == 0 read x), rows 1-15 are zero (the
   // other lanes read the zero block at the same offsets): no select per k block
-  const uint4* arow = lr == 0 ? L.xs + 4 * kb0 + lq : L.xz + lq;
+  // (fp16: row 1 is x's lo part)
+  const uint4* arow = lr == 0 ? L.xs + 4 * kb0 + lq : (F16 && lr == 1) ? L.xs_lo + 4 * kb0 + lq : L.xz + lq;
   float y[4] = {0.f, 0.f, 0.f, 0.f};
   if constexpr (GSH > 0) {
     // the wave's first k block sits at phase kb0 % (k blocks per group) of
@@ -669,14 +677,14 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
     // start and scale register of the loop is known to the compiler
     constexpr int kPh = 1 << GSH;
     const int ph = kb0 & (kPh - 1);
-    if (ph == 0) item_products<GSH, 0>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 1 && ph == 1) item_products<GSH, (kPh > 1 ? 1 : 0)>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 2 && ph == 2) item_products<GSH, (kPh > 2 ? 2 : 0)>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 3 && ph == 3) item_products<GSH, (kPh > 3 ? 3 : 0)>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 4 && ph == 4) item_products<GSH, (kPh > 4 ? 4 : 0)>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 5 && ph == 5) item_products<GSH, (kPh > 5 ? 5 : 0)>(r, arow, kbv, mq, mc, y);
-    else if (kPh > 6 && ph == 6) item_products<GSH, (kPh > 6 ? 6 : 0)>(r, arow, kbv, mq, mc, y);
-    else item_products<GSH, (kPh > 7 ? 7 : 0)>(r, arow, kbv, mq, mc, y);
+    if (ph == 0) item_products<GSH, 0, F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 1 && ph == 1) item_products<GSH, (kPh > 1 ? 1 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 2 && ph == 2) item_products<GSH, (kPh > 2 ? 2 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 3 && ph == 3) item_products<GSH, (kPh > 3 ? 3 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 4 && ph == 4) item_products<GSH, (kPh > 4 ? 4 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 5 && ph == 5) item_products<GSH, (kPh > 5 ? 5 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else if (kPh > 6 && ph == 6) item_products<GSH, (kPh > 6 ? 6 : 0), F16>(r, arow, kbv, mq, mc, y);
+    else item_products<GSH, (kPh > 7 ? 7 : 0), F16>(r, arow, kbv, mq, mc, y);
   } else {
     const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
     f32x4_t D[4] = {zf, zf, zf, zf};
@@ -697,10 +705,10 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
 #pragma unroll
         for (int q = 1; q < kGuSc; ++q)
           if (gi == q) s2 = opaque(r.s[q]);
-        const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+        const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          y[i] += sc[i] * (D[i][0] + bacc);
+          y[i] += sc[i] * ((F16 ? D[i][0] + D[i][1] : D[i][0]) + bacc);
           D[i] = zf;
         }
         bacc = 0.f;
@@ -720,9 +728,8 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
       g += rg[tid & 3];
       up += ru[tid & 3];
     }
-    const float av = (32 * c + tid < Iv) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
-    uint16_t bits = f32_to_bf16(av);
-    if ((bits & 0x7fffu) > 0x7f80u) bits = 0x7fc0u;  // canonical NaN: never stored as zero
+    const float av = (32 * c + tid < Iv) ? gelu_tanh(g) * up : 0.f;
+    const uint16_t bits = act_signal_bits<F16>(av);  // rounded to the activation dtype, canonical NaN
     ((uint16_t*)L.sa)[(tid & ~7) + mfma_k_pos(tid & 7)] = bits;
   }
   lds_barrier();
@@ -744,11 +751,22 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
   const int pr = tid / n_fq, fq = tid - pr * n_fq;
   if (pr < 4) {
     const uint4 A = L.sa[pr];
-    const float bias = q4_bias(A);
     float s[4];
     const uint32_t wv[4] = {r.fw.x, r.fw.y, r.fw.z, r.fw.w};
+    if constexpr (F16) {
+      uint4 Ah, Al;
+      f16_split(A, Ah, Al);
+      const float bias = q4_bias(Ah) + q4_bias(Al);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s[i] = dot_chunk(A, unpack_q4(wv[i], mq), bias);
+      for (int i = 0; i < 4; ++i) {
+        const Q4Pairs q = unpack_q4(wv[i], mq);
+        s[i] = dot_chunk(Al, q, dot_chunk(Ah, q, bias));
+      }
+    } else {
+      const float bias = q4_bias(A);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s[i] = dot_chunk(A, unpack_q4(wv[i], mq), bias);
+    }
     L.fr[pr][fq] = make_float4(s[0], s[1], s[2], s[3]);
   }
   lds_barrier();
@@ -758,10 +776,10 @@ __device__ __forceinline__ void item_run(const D1Args& a, const D1Pro& P, ItemLd
     const float v0 = ((f0.x + f1.x) + f2.x) + f3.x, v1 = ((f0.y + f1.y) + f2.y) + f3.y;
     const float v2 = ((f0.z + f1.z) + f2.z) + f3.z, v3 = ((f0.w + f1.w) + f2.w) + f3.w;
     u32x4_t o;
-    o.x = f32_signal_bits((wu * bf16lo(r.fs.x)) * v0);
-    o.y = f32_signal_bits((wu * bf16hi(r.fs.x)) * v1);
-    o.z = f32_signal_bits((wu * bf16lo(r.fs.y)) * v2);
-    o.w = f32_signal_bits((wu * bf16hi(r.fs.y)) * v3);
+    o.x = f32_signal_bits((wu * sc_lo<F16>(r.fs.x)) * v0);
+    o.y = f32_signal_bits((wu * sc_hi<F16>(r.fs.x)) * v1);
+    o.z = f32_signal_bits((wu * sc_lo<F16>(r.fs.y)) * v2);
+    o.w = f32_signal_bits((wu * sc_hi<F16>(r.fs.y)) * v3);
     __builtin_amdgcn_raw_buffer_store_b128(o, buffer_rsrc(part, kPartParity),
                                            (uint32_t)((it * n_fq * 4 + 4 * tid) * 4), 0, kCpolAgent);
   }
@@ -820,9 +838,9 @@ __device__ __forceinline__ void unit_load(const D1Args& a, const D1Pro& P, int d
 // (all of them present: no 16-bit half zero), inverted back, with each
 // chunk's -24 * sum of its 8 values into bias.  Bounded: on timeout the status
 // word and host flag are set, *bad is set and the wave goes on.
-template <int CPT>
+template <int CPT, bool F16>
 __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buffer_rsrc_t src, uint4* dst,
-                                            float* bias, int n, int* bad) {
+                                            uint4* dst_lo, float* bias, int n, int* bad) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t pending = 0u;
 #pragma unroll
@@ -839,8 +857,16 @@ __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buff
     for (int j = 0; j < CPT; ++j) {
       if (((pending >> j) & 1u) && chunk_ready(v[j])) {
         const uint4 x = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
-        dst[lane + j * kWave] = x;
-        bias[lane + j * kWave] = q4_bias(x);
+        if constexpr (F16) {
+          uint4 xh, xl;
+          f16_split(x, xh, xl);
+          dst[lane + j * kWave] = xh;
+          dst_lo[lane + j * kWave] = xl;
+          bias[lane + j * kWave] = q4_bias(xh) + q4_bias(xl);
+        } else {
+          dst[lane + j * kWave] = x;
+          bias[lane + j * kWave] = q4_bias(x);
+        }
         pending &= ~(1u << j);
       }
     }
@@ -870,14 +896,20 @@ __device__ __forceinline__ void folded_poll(const __amdgpu_buffer_rsrc_t rp, int
 // The products of one scale group, finished: y += scale * (the group's sum +
 // its -24 * sum of activations); lanes lr < 8 take A row 0 (k block 2s),
 // lanes lr >= 8 row 1 (k block 2s + 1).
+// (fp16: rows 0 and 1 are k block 2s's hi and lo parts, rows 2 and 3 k block
+// 2s + 1's)
+template <bool F16>
 __device__ __forceinline__ void group_epilogue(float (&y)[4], const f32x4_t (&D)[4], uint2 s2, float bacc, int h) {
-  const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+  const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) y[i] += sc[i] * ((h ? D[i][1] : D[i][0]) + bacc);
+  for (int i = 0; i < 4; ++i) {
+    const float d = F16 ? (h ? D[i][2] + D[i][3] : D[i][0] + D[i][1]) : (h ? D[i][1] : D[i][0]);
+    y[i] += sc[i] * (d + bacc);
+  }
 }
 
-template <int NS, int GSH>
-__device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, int d, int U, const char* act,
+template <int NS, int GSH, bool F16>
+__device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>& L, int d, int U, const char* act,
                                          const UnitRegs<NS>& r, int parity, int cslot, int nslots) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int lq = lane >> 4, lr = lane & 15, h = lr >> 3;
@@ -917,8 +949,8 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
   if (u < U) {
     // wave u waits for expert u's activations only (its products start as
     // soon as they are there), with each chunk's -24 * sum
-    poll_chunks<2>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps,
-                   L.cbias + u * cps, cps, bad);
+    poll_chunks<2, F16>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps,
+                        F16 ? L.sact_lo + u * cps : nullptr, L.cbias + u * cps, cps, bad);
     GI_STAMP(4);
     GI_STAMP_BY(20, (U - 1) * kWave);
     // lane l holds k block l's -24 * sum of the expert's activations (this
@@ -926,11 +958,15 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
     const float* cb = L.cbias + u * cps + 4 * min(lane, Tk - 1);
     const float kv = ((cb[0] + cb[1]) + cb[2]) + cb[3];
     // A rows 0, 1: k blocks 2s, 2s+1 (lanes lr < 2), read three steps ahead
+    // (fp16: rows 0-3 = k block 2s hi, lo, k block 2s+1 hi, lo; lanes lr < 4)
     const int rowoff = uc * cps + lq;
+    const int kbo = F16 ? ((lr >> 1) & 1) : (lr & 1);
+    const uint4* srow = (F16 && (lr & 1)) ? L.sact_lo : L.sact;
+    constexpr int kArows = F16 ? 4 : 2;
     constexpr int kAhead = 3;
     uint4 an[kAhead];
 #pragma unroll
-    for (int s = 0; s < kAhead; ++s) an[s] = L.sact[rowoff + min(4 * (2 * s + (lr & 1)), cps - 4)];
+    for (int s = 0; s < kAhead; ++s) an[s] = srow[rowoff + min(4 * (2 * s + kbo), cps - 4)];
     // two accumulator sets, alternating by scale group: a group's scale is
     // applied after the next group's products are issued, so that the
     // epilogue does not wait for the matrix cores (the sets are named, not
@@ -950,13 +986,13 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
       const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
       const float b1 = 2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
       bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
-      if (epi) group_epilogue(y, Dp, s2p, bp, h);
+      if (epi) group_epilogue<F16>(y, Dp, s2p, bp, h);
     };
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const int kba = 2 * s + (lr & 1);
-      const uint4 A = (lr < 2 && kba < Tk) ? an[s % kAhead] : z4;
-      if (s + kAhead < NS) an[s % kAhead] = L.sact[rowoff + min(4 * (kba + 2 * kAhead), cps - 4)];
+      const int kba = 2 * s + kbo;
+      const uint4 A = (lr < kArows && kba < Tk) ? an[s % kAhead] : z4;
+      if (s + kAhead < NS) an[s % kAhead] = srow[rowoff + min(4 * (kba + 2 * kAhead), cps - 4)];
       const int g = (2 * s) >> gsh;
       const bool gstart = ((2 * s) & gpb_m1) == 0;
       const bool epi = gstart && g > 0;
@@ -964,8 +1000,8 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
       else step(s, A, gstart, epi, g, D1, s21, bacc1, D0, s20, bacc0);
     }
     GI_STAMP(21);
-    if ((((2 * (NS - 1)) >> gsh) & 1) == 0) group_epilogue(y, D0, s20, bacc0, h);
-    else group_epilogue(y, D1, s21, bacc1, h);
+    if ((((2 * (NS - 1)) >> gsh) & 1) == 0) group_epilogue<F16>(y, D0, s20, bacc0, h);
+    else group_epilogue<F16>(y, D1, s21, bacc1, h);
 #ifdef GI_TIMELINE
     asm volatile("" ::"v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]));
 #endif
@@ -982,9 +1018,9 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
       sacc += ((const float*)&L.red[w2][tid >> 2])[tid & 3];
       sacc += ((const float*)&L.red[w2][8 + (tid >> 2)])[tid & 3];
     }
-    if (!a.overwrite) sacc += bf16_to_f32(r.old & 0xffffu);
+    if (!a.overwrite) sacc += act_to_f32<F16>(r.old & 0xffffu);
     if (P.bad) sacc = __uint_as_float(0x7fc00000u);  // never a wrong finite value
-    a.out[32 * d + tid] = f32_to_bf16(sacc);
+    a.out[32 * d + tid] = f32_to_act<F16>(sacc);
   }
   GI_STAMP(6);
 }
@@ -994,6 +1030,7 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds& L, 
 // 8 column quads, polled with a bounded wait and added in a fixed order: each
 // thread's items in order, then the wave's 8 streams (xor 8, 16, 32), then
 // the 8 waves in order; one bf16 rounding (plus the previous output).
+template <bool F16>
 __device__ __forceinline__ void folded_reduce(const D1Args& a, D1Pro& P, float4 (&rr)[kW][8], int f, int n_items,
                                               int n_whole, int n_left, const char* part, uint32_t old) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
@@ -1053,9 +1090,9 @@ __device__ __forceinline__ void folded_reduce(const D1Args& a, D1Pro& P, float4 
     float sacc = 0.f;
 #pragma unroll
     for (int w2 = 0; w2 < kW; ++w2) sacc += ((const float*)&rr[w2][tid >> 2])[tid & 3];
-    if (!a.overwrite) sacc += bf16_to_f32(old & 0xffffu);
+    if (!a.overwrite) sacc += act_to_f32<F16>(old & 0xffffu);
     if (P.bad) sacc = __uint_as_float(0x7fc00000u);
-    a.out[32 * (n_whole + f) + tid] = f32_to_bf16(sacc);
+    a.out[32 * (n_whole + f) + tid] = f32_to_act<F16>(sacc);
   }
   GI_STAMP(7);
 }
@@ -1063,20 +1100,20 @@ __device__ __forceinline__ void folded_reduce(const D1Args& a, D1Pro& P, float4 
 // ---------------------------------------------------------------------------
 // kernel
 // ---------------------------------------------------------------------------
-template <int NS, int GSH>
+template <int NS, int GSH, bool F16>
 __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
   __shared__ D1Pro P;
-  __shared__ D1Lds L;
+  __shared__ D1Lds<F16> L;
 #ifdef GI_TIMELINE
   tl_init();
 #endif
   GI_STAMP(0);
   int parity = 0;
   u32x4_t xv;
-  if (a.E <= 2 * kWave) d1_start<2>(a, P, &xv, &parity);
-  else if (a.E <= 4 * kWave) d1_start<4>(a, P, &xv, &parity);
-  else if (a.E <= 8 * kWave) d1_start<8>(a, P, &xv, &parity);
-  else d1_start<kRouteMaxExperts / kWave>(a, P, &xv, &parity);
+  if (a.E <= 2 * kWave) d1_start<2, F16>(a, P, &xv, &parity);
+  else if (a.E <= 4 * kWave) d1_start<4, F16>(a, P, &xv, &parity);
+  else if (a.E <= 8 * kWave) d1_start<8, F16>(a, P, &xv, &parity);
+  else d1_start<kRouteMaxExperts / kWave, F16>(a, P, &xv, &parity);
   GI_STAMP(1);
   const int tid = threadIdx.x;
   const int b = blockIdx.x, G = gridDim.x;
@@ -1109,16 +1146,25 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
     // x in LDS in the matrix-core k order, with each chunk's -24 * sum
     if (tid < kMaxH / 8) {
       const uint4 v = make_uint4(xv.x, xv.y, xv.z, xv.w);
-      L.it.xs[tid] = tid < Kv8 ? mfma_k_order(v) : make_uint4(0u, 0u, 0u, 0u);
-      P.cb[tid] = tid < Kv8 ? q4_bias(v) : 0.f;
+      const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+      if constexpr (F16) {
+        uint4 vh, vl;
+        f16_split(v, vh, vl);
+        L.it.xs[tid] = tid < Kv8 ? mfma_k_order(vh) : z;
+        L.it.xs_lo[tid] = tid < Kv8 ? mfma_k_order(vl) : z;
+        P.cb[tid] = tid < Kv8 ? q4_bias(vh) + q4_bias(vl) : 0.f;
+      } else {
+        L.it.xs[tid] = tid < Kv8 ? mfma_k_order(v) : z;
+        P.cb[tid] = tid < Kv8 ? q4_bias(v) : 0.f;
+      }
     } else if (tid < kMaxH / 8 + 4 * kKbw) {
       L.it.xz[tid - kMaxH / 8] = make_uint4(0u, 0u, 0u, 0u);
     }
     GI_STAMP_BY(14, kWave);
     if (a.logits && tid < kWave) d1_weights(a, P);
     lds_barrier();
-    item_run<GSH>(a, P, L.it, b, u, c, n_left, act, part, r);
-    if (b < n_left) folded_reduce(a, P, L.it.rr, b, n_items, n_whole, n_left, part, r.old);
+    item_run<GSH, F16>(a, P, L.it, b, u, c, n_left, act, part, r);
+    if (b < n_left) folded_reduce<F16>(a, P, L.it.rr, b, n_items, n_whole, n_left, part, r.old);
     if (cslot >= 0) clear_prev(a, P.epoch, parity, cslot, nc);
   } else if (b - n_items < n_whole) {
     const int d = b - n_items;
@@ -1136,7 +1182,7 @@ __global__ __launch_bounds__(kT) void moe_decode1_kernel(D1Args a) {
     unit_load<NS>(a, P, d, U, n_whole, n_left, r);
     GI_STAMP(2);
     if (a.logits && tid < kWave) d1_weights(a, P);  // read after the unit's next barrier
-    unit_run<NS, GSH>(a, P, L.un, d, U, act, r, parity, cslot, nc);
+    unit_run<NS, GSH, F16>(a, P, L.un, d, U, act, r, parity, cslot, nc);
   } else if (cslot >= 0) {
     clear_prev(a, P.epoch, parity, cslot, nc);
   }
@@ -1184,23 +1230,28 @@ int variant_for(int Tk, int gsh) {
     }
   return -1;
 }
-const void* kernel_for(int v) {
+template <bool F16>
+const void* kernel_for_t(int v) {
   switch (v) {
-    case 0: return (const void*)moe_decode1_kernel<2, 0>;
-    case 1: return (const void*)moe_decode1_kernel<4, 0>;
-    case 2: return (const void*)moe_decode1_kernel<6, 0>;
-    case 3: return (const void*)moe_decode1_kernel<8, 0>;
-    case 4: return (const void*)moe_decode1_kernel<11, 0>;
-    case 5: return (const void*)moe_decode1_kernel<12, 0>;
-    case 6: return (const void*)moe_decode1_kernel<11, 1>;
-    default: return (const void*)moe_decode1_kernel<11, 2>;
+    case 0: return (const void*)moe_decode1_kernel<2, 0, F16>;
+    case 1: return (const void*)moe_decode1_kernel<4, 0, F16>;
+    case 2: return (const void*)moe_decode1_kernel<6, 0, F16>;
+    case 3: return (const void*)moe_decode1_kernel<8, 0, F16>;
+    case 4: return (const void*)moe_decode1_kernel<11, 0, F16>;
+    case 5: return (const void*)moe_decode1_kernel<12, 0, F16>;
+    case 6: return (const void*)moe_decode1_kernel<11, 1, F16>;
+    default: return (const void*)moe_decode1_kernel<11, 2, F16>;
   }
+}
+// variants [0, kNumVariants): bf16 activations; [kNumVariants, 2 kNumVariants): fp16
+const void* kernel_for(int v) {
+  return v < kNumVariants ? kernel_for_t<false>(v) : kernel_for_t<true>(v - kNumVariants);
 }
 
 // Every workgroup of a launch (one per CU) must be resident at once: the
 // occupancy calculator must put one on every CU (cached per device and variant).
 std::mutex g_occ_mu;
-int g_occ[64][kNumVariants];  // 0 unknown, 1 resident, -1 not
+int g_occ[64][2 * kNumVariants];  // 0 unknown, 1 resident, -1 not
 
 bool resident_everywhere(int v) {
   int dev = 0;
@@ -1238,8 +1289,11 @@ bool moe_decode1_supported(const MoeHostArgs& h) {
   const int G = grid_for();
   const int Tk = h.I / 32, units = h.H / 32;
   const int umax = h.top_k < h.E ? h.top_k : h.E;
-  const int v = variant_for(Tk, log2_exact(h.gs / 32));
-  if (v < 0 || umax > kMaxU || !d1::split_ok(G, umax, Tk, units, kMaxLeft)) return false;
+  const int v0 = variant_for(Tk, log2_exact(h.gs / 32));
+  if (v0 < 0 || umax > kMaxU || !d1::split_ok(G, umax, Tk, units, kMaxLeft)) return false;
+  // bf16, or fp16 from caller ids (the layer-from-logits entry is bf16 only)
+  if (h.x_dtype != GI_DTYPE_BF16 && !(h.x_dtype == GI_DTYPE_FP16 && !h.logits)) return false;
+  const int v = v0 + (h.x_dtype == GI_DTYPE_FP16 ? kNumVariants : 0);
   if (umax * h.Gd * 4 > kT) return false;  // down-scale staging: one chunk per thread
   // the split at the most unique experts (fewer experts only shrink the folded part)
   const d1::Split sp = d1::split(G, umax, Tk, units);
@@ -1290,7 +1344,8 @@ int launch_moe_decode1(const MoeHostArgs& h, void* state, int* status) {
   k.spin_limit = h.spin_limit > 0 ? h.spin_limit : kDefaultSpin;
   void* args[] = {(void*)&k};
   const hipError_t e =
-      hipLaunchKernel(kernel_for(variant_for(k.Tk, k.gsh)), dim3(grid_for()), dim3(kT), args, 0, h.stream);
+      hipLaunchKernel(kernel_for(variant_for(k.Tk, k.gsh) + (h.x_dtype == GI_DTYPE_FP16 ? kNumVariants : 0)),
+                      dim3(grid_for()), dim3(kT), args, 0, h.stream);
   if (e != hipSuccess) return hip_fail(e, "fused MoE one-token decode launch");
   return GI_OK;
 }

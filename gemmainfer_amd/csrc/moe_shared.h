@@ -230,5 +230,65 @@ __device__ __forceinline__ uint4 q4_operand(uint32_t w, uint32_t mq) {
 // position of element p (0..7) of a packed row in that order
 __device__ __forceinline__ int mfma_k_pos(int p) { return (p & 1) * 4 + (p & 2) + (p >> 2); }
 
+// ---------------------------------------------------------------------------
+// fp16 activations
+// ---------------------------------------------------------------------------
+// fp16 activations (the reference's fp16 dispatch, marlin.cu:694-700) run on
+// the same bf16 matrix-core products: an fp16 value splits exactly into bf16
+// hi (its leading 8 significand bits, truncated) and bf16 lo = value - hi
+// (at most 3 significant bits), which take two A operand rows; the sum of the
+// two rows' products is the fp16 value's product, in fp32.  Scales and out
+// are fp16, the activation and the routing weights are rounded to fp16 where
+// the bf16 path rounds to bf16.
+__device__ __forceinline__ void f16_split2(uint32_t v, uint32_t& hi, uint32_t& lo) {
+  const float a = fp16_to_f32((uint16_t)(v & 0xffffu)), b = fp16_to_f32((uint16_t)(v >> 16));
+  const uint32_t ha = __float_as_uint(a) & 0xffff0000u, hb = __float_as_uint(b) & 0xffff0000u;
+  const float la = a - __uint_as_float(ha), lb = b - __uint_as_float(hb);
+  hi = (ha >> 16) | hb;
+  lo = (__float_as_uint(la) >> 16) | (__float_as_uint(lb) & 0xffff0000u);
+}
+__device__ __forceinline__ void f16_split(const uint4 v, uint4& hi, uint4& lo) {
+  f16_split2(v.x, hi.x, lo.x);
+  f16_split2(v.y, hi.y, lo.y);
+  f16_split2(v.z, hi.z, lo.z);
+  f16_split2(v.w, hi.w, lo.w);
+}
+template <bool F16>
+__device__ __forceinline__ float sc_lo(uint32_t v) {
+  if constexpr (F16) return fp16_to_f32((uint16_t)(v & 0xffffu));
+  else return bf16lo(v);
+}
+template <bool F16>
+__device__ __forceinline__ float sc_hi(uint32_t v) {
+  if constexpr (F16) return fp16_to_f32((uint16_t)(v >> 16));
+  else return bf16hi(v);
+}
+template <bool F16>
+__device__ __forceinline__ float act_to_f32(uint32_t bits16) {
+  if constexpr (F16) return fp16_to_f32((uint16_t)bits16);
+  else return bf16_to_f32(bits16);
+}
+template <bool F16>
+__device__ __forceinline__ uint16_t f32_to_act(float f) {
+  if constexpr (F16) return __builtin_bit_cast(uint16_t, (_Float16)f);  // round to nearest even
+  else return f32_to_bf16(f);
+}
+template <bool F16>
+__device__ __forceinline__ float round_to_act(float f) {
+  return act_to_f32<F16>(f32_to_act<F16>(f));
+}
+// the bit pattern of an activation with NaN made canonical (an all-ones half
+// would be stored as zero, "not written", once inverted)
+template <bool F16>
+__device__ __forceinline__ uint16_t act_signal_bits(float f) {
+  uint16_t bits = f32_to_act<F16>(f);
+  if constexpr (F16) {
+    if ((bits & 0x7fffu) > 0x7c00u) bits = 0x7e00u;
+  } else {
+    if ((bits & 0x7fffu) > 0x7f80u) bits = 0x7fc0u;
+  }
+  return bits;
+}
+
 }  // namespace moe
 }  // namespace gi

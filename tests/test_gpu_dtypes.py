@@ -65,6 +65,46 @@ def test_moe_gemma_shape(gemma, m, noise):
     assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, tag), tag, f"moe {tag} gs={gs} m={m}")
 
 
+@pytest.mark.parametrize("gs", [64, 128])
+def test_moe_fp16_one_token_edge_cases(gs):
+    """fp16 at one token runs the one-token kernel's fp16 variant (each fp16
+    value split exactly into bf16 hi + lo operand rows): ids outside [0, E)
+    skipped (marlin.cu:304, :473), one expert in several slots with different
+    weights, int64 ids and fp32 weights cast to fp16 (marlin.cu:631-636),
+    activations spread over fp16's whole range (every significand bit and
+    subnormals in use), accumulation into a non-zero out, and all ids
+    invalid (out unchanged)."""
+    dt = torch.float16
+    W = _moe_weights(E, H, I, gs, seed=900 + gs, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    g = torch.Generator().manual_seed(901)
+    mag = torch.exp(torch.randn(1, H, generator=g)).clamp(max=20.0)
+    x = (synth.activations(1, H, seed=902) * mag).to(dt)
+    x[0, :8] = torch.tensor([6e-8, -6e-8, 1e-6, -3e-5, 0.0, 17.0078125, -1.0009765625, 0.33325195]).to(dt)
+    cases = [
+        (torch.tensor([[5, -1, 5, 127, 128, 99, 0, 3]], dtype=torch.int64), torch.rand(1, 8, generator=g)),
+        (torch.tensor([[3, 3, 3, 3, 3, 3, 3, 3]], dtype=torch.int32), torch.rand(1, 8, generator=g).to(dt)),
+        (torch.tensor([[17, 42, 9, 120, 77, 1, 64, 33]], dtype=torch.int32),
+         torch.softmax(torch.randn(1, 8, generator=g), dim=-1).to(torch.bfloat16)),
+    ]
+    for n, (idx, w) in enumerate(cases):
+        out_in = (torch.randn(1, H, generator=g) * 0.1).to(dt)
+        out = out_in.to(DEV).clone()
+        gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                          Wd["down_packed"], Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+        torch.cuda.synchronize()
+        ref = _oracle(W, x, idx, w.to(dt), out_in, gs, "fp16")
+        assert_dtype_close(out, ref, "fp16", f"fp16 one token gs={gs} case {n}")
+    # no valid id: out unchanged
+    idx = torch.tensor([[-1, 128, 200, -5, 1000, -1, 128, 129]], dtype=torch.int32)
+    out_in = (torch.randn(1, H, generator=g) * 0.1).to(dt).to(DEV)
+    out = out_in.clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), torch.ones(1, 8, dtype=dt).to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_in)
+
+
 @pytest.mark.parametrize("tag", ["fp16", "fp32"])
 def test_moe_duplicates_invalid_ids_and_many_rows(tag):
     dt = DT[tag]
