@@ -204,7 +204,7 @@ __device__ __forceinline__ void dec_issue(const DecArgs& a, DecIn<VPL>& in) {
   }
 }
 
-template <int VPL>
+template <int VPL, bool F16>
 __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, const DecIn<VPL>& in) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = uniform(tid >> 6);
   const int S = a.S;
@@ -225,7 +225,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, c
     const float wv = a.w_dtype == GI_DTYPE_FP32   ? __uint_as_float(in.wb)
                      : a.w_dtype == GI_DTYPE_FP16 ? fp16_to_f32((uint16_t)in.wb)
                                                   : bf16_to_f32(in.wb);
-    P.slot_w[lane] = round_to_bf16(wv);
+    P.slot_w[lane] = round_to_act<F16>(wv);
   }
   GI_STAMP(15);
   lds_barrier();
@@ -235,7 +235,7 @@ __device__ __forceinline__ void dec_prologue(const DecArgs& a, DecPrologue& P, c
     float w = lane < S ? P.slot_w[lane] : 0.f;
     const int t = lane / a.top_k;
     if (a.logits) {
-      w = round_to_bf16(w);
+      w = round_to_act<F16>(w);
       if (lane < S) P.slot_w[lane] = w;  // reported by workgroup 0 at the end
     } else {
       // a token's slots with one expert: the first keeps the sum of their
@@ -388,11 +388,11 @@ __host__ __device__ constexpr size_t gu_lds_bytes() {
 // 4lq + jj, task column 4lr + i) = sum over scale groups of scale * (the
 // group's products + its -24 * sum of x, from one more product against a
 // constant operand).  Generic form: the group size is a run-time value.
-template <int KBW>
+template <int KBW, bool F16>
 __device__ __forceinline__ void gu_products(const DecArgs& a, const GuBuf<KBW>& b, const uint4* xrow, int kb0,
                                             float (&y)[4][4]) {
   const int kbpg_m1 = (1 << a.gsh) - 1;  // k blocks per scale group - 1
-  const uint32_t mq = q4_magic();
+  const uint32_t mq = q4_magic_t<F16>();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   f32x4_t D[4] = {zf, zf, zf, zf};
@@ -402,22 +402,22 @@ __device__ __forceinline__ void gu_products(const DecArgs& a, const GuBuf<KBW>& 
     const int kb = kb0 + j;
     const uint4 A = xrow[4 * kb];
     const uint4 w = opaque(b.w[j]);
-    D[0] = mfma_bf16(A, q4_operand(w.x, mq), D[0]);
-    D[1] = mfma_bf16(A, q4_operand(w.y, mq), D[1]);
-    D[2] = mfma_bf16(A, q4_operand(w.z, mq), D[2]);
-    D[3] = mfma_bf16(A, q4_operand(w.w, mq), D[3]);
-    Db = mfma_bf16(A, bc, Db);  // -24 * sum of each row's x over the k block
+    D[0] = mfma_act<F16>(A, q4_operand_t<F16>(w.x, mq), D[0]);
+    D[1] = mfma_act<F16>(A, q4_operand_t<F16>(w.y, mq), D[1]);
+    D[2] = mfma_act<F16>(A, q4_operand_t<F16>(w.z, mq), D[2]);
+    D[3] = mfma_act<F16>(A, q4_operand_t<F16>(w.w, mq), D[3]);
+    if constexpr (!F16) Db = mfma_bf16(A, bc, Db);  // -24 * sum of each row's x over the k block
     if (((kb + 1) & kbpg_m1) == 0 || j == KBW - 1) {  // a scale group ends here
       const int gi = min(kb >> a.gsh, a.Ggu - 1) - min(kb0 >> a.gsh, a.Ggu - 1);
       uint2 s2 = opaque(b.s[0]);
 #pragma unroll
       for (int q = 1; q < kGuScales; ++q)
         if (gi == q) s2 = opaque(b.s[q]);
-      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (D[i][jj] + Db[jj]);
+        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (F16 ? D[i][jj] : D[i][jj] + Db[jj]);
         D[i] = zf;
       }
       Db = zf;
@@ -430,10 +430,10 @@ __device__ __forceinline__ void gu_products(const DecArgs& a, const GuBuf<KBW>& 
 // and the scale register of each group are known to the compiler, and a
 // group's first products start from zero.  The scales of groups past the
 // scale tensor were loaded as zeros.
-template <int KBW, int GSH, int PH>
+template <int KBW, bool F16, int GSH, int PH>
 __device__ __forceinline__ void gu_products_ph(const GuBuf<KBW>& b, const uint4* xrow, int kb0, float (&y)[4][4]) {
   constexpr int kPg = 1 << GSH;
-  const uint32_t mq = q4_magic();
+  const uint32_t mq = q4_magic_t<F16>();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   f32x4_t D[4], Db;
@@ -442,25 +442,25 @@ __device__ __forceinline__ void gu_products_ph(const GuBuf<KBW>& b, const uint4*
     const bool gstart = j == 0 || (PH + j) % kPg == 0;
     const uint4 A = xrow[4 * (kb0 + j)];
     const uint4 w = opaque(b.w[j]);
-    D[0] = mfma_bf16(A, q4_operand(w.x, mq), gstart ? zf : D[0]);
-    D[1] = mfma_bf16(A, q4_operand(w.y, mq), gstart ? zf : D[1]);
-    D[2] = mfma_bf16(A, q4_operand(w.z, mq), gstart ? zf : D[2]);
-    D[3] = mfma_bf16(A, q4_operand(w.w, mq), gstart ? zf : D[3]);
-    Db = mfma_bf16(A, bc, gstart ? zf : Db);
+    D[0] = mfma_act<F16>(A, q4_operand_t<F16>(w.x, mq), gstart ? zf : D[0]);
+    D[1] = mfma_act<F16>(A, q4_operand_t<F16>(w.y, mq), gstart ? zf : D[1]);
+    D[2] = mfma_act<F16>(A, q4_operand_t<F16>(w.z, mq), gstart ? zf : D[2]);
+    D[3] = mfma_act<F16>(A, q4_operand_t<F16>(w.w, mq), gstart ? zf : D[3]);
+    if constexpr (!F16) Db = mfma_bf16(A, bc, gstart ? zf : Db);
     if ((PH + j + 1) % kPg == 0 || j == KBW - 1) {  // a scale group ends
       const uint2 s2 = opaque(b.s[(PH + j) / kPg]);
-      const float sc[4] = {bf16lo(s2.x), bf16hi(s2.x), bf16lo(s2.y), bf16hi(s2.y)};
+      const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (D[i][jj] + Db[jj]);
+        for (int jj = 0; jj < 4; ++jj) y[i][jj] += sc[i] * (F16 ? D[i][jj] : D[i][jj] + Db[jj]);
     }
   }
 }
 
 // One item: gate/up product, cross-wave reduction, activation, exchange.
 // PHASED: the group sizes 64 and 128 take the phase-specialized products.
-template <int KBW, bool PHASED = false>
+template <int KBW, bool F16, bool PHASED = false>
 __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, int item, const GuBuf<KBW>& b,
                                         const GuLds& L, uint16_t* act) {
   constexpr int KPM = GuShape<KBW>::KPM;
@@ -485,18 +485,18 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
   if constexpr (PHASED) {
     if (a.gsh == 2) {
       const int ph = kb0 & 3;
-      if (ph == 0) gu_products_ph<KBW, 2, 0>(b, xrow, kb0, y);
-      else if (ph == 1) gu_products_ph<KBW, 2, 1>(b, xrow, kb0, y);
-      else if (ph == 2) gu_products_ph<KBW, 2, 2>(b, xrow, kb0, y);
-      else gu_products_ph<KBW, 2, 3>(b, xrow, kb0, y);
+      if (ph == 0) gu_products_ph<KBW, F16, 2, 0>(b, xrow, kb0, y);
+      else if (ph == 1) gu_products_ph<KBW, F16, 2, 1>(b, xrow, kb0, y);
+      else if (ph == 2) gu_products_ph<KBW, F16, 2, 2>(b, xrow, kb0, y);
+      else gu_products_ph<KBW, F16, 2, 3>(b, xrow, kb0, y);
     } else if (a.gsh == 1) {
-      if ((kb0 & 1) == 0) gu_products_ph<KBW, 1, 0>(b, xrow, kb0, y);
-      else gu_products_ph<KBW, 1, 1>(b, xrow, kb0, y);
+      if ((kb0 & 1) == 0) gu_products_ph<KBW, F16, 1, 0>(b, xrow, kb0, y);
+      else gu_products_ph<KBW, F16, 1, 1>(b, xrow, kb0, y);
     } else {
-      gu_products<KBW>(a, b, xrow, kb0, y);
+      gu_products<KBW, F16>(a, b, xrow, kb0, y);
     }
   } else {
-    gu_products<KBW>(a, b, xrow, kb0, y);
+    gu_products<KBW, F16>(a, b, xrow, kb0, y);
   }
   // per-wave sums of token rows 4lq+jj, task columns 4lr..4lr+3
 #pragma unroll
@@ -515,9 +515,8 @@ __device__ __forceinline__ void gu_item(const DecArgs& a, const DecPrologue& P, 
       g += r[ci];
       up += r[32 + ci];
     }
-    const float av = (kCols * c + ci < Iv) ? round_to_bf16(gelu_tanh(g) * up) : 0.f;
-    uint16_t bits = f32_to_bf16(av);
-    if ((bits & 0x7fffu) > 0x7f80u) bits = 0x7fc0u;  // canonical NaN: no stored zero (see header)
+    const float av = (kCols * c + ci < Iv) ? round_to_act<F16>(gelu_tanh(g) * up) : 0.f;
+    const uint16_t bits = act_signal_bits<F16>(av);  // canonical NaN: no stored zero (see header)
     L.sact[t * kCols + (ci & ~7) + mfma_k_pos(ci & 7)] = bits;
   }
   lds_barrier();
@@ -562,16 +561,16 @@ __device__ __forceinline__ void load_x(const DecArgs& a, XRegs<KBW>& x) {
 // is then reloaded with item K+2 while item K+1 runs from `nxt`.  Template
 // recursion instead of a loop: a register array carried around a loop is
 // copied at the loop header, which waits for every load in flight.
-template <int KBW, int K>
+template <int KBW, bool F16, int K>
 __device__ __forceinline__ void gu_items(const DecArgs& a, const DecPrologue& P, const GuLds& L, int uexp_v,
                                          int it0, int stride, int n_items, GuBuf<KBW>& cur, GuBuf<KBW>& nxt,
                                          uint16_t* act) {
   if constexpr (K < kMaxItems) {
     const int item = it0 + K * stride;
     if (item >= n_items) return;
-    gu_item<KBW>(a, P, item, cur, L, act);
+    gu_item<KBW, F16>(a, P, item, cur, L, act);
     gu_load<KBW>(a, uexp_v, item + 2 * stride, n_items, cur);
-    gu_items<KBW, K + 1>(a, P, L, uexp_v, it0, stride, n_items, nxt, cur, act);
+    gu_items<KBW, F16, K + 1>(a, P, L, uexp_v, it0, stride, n_items, nxt, cur, act);
   }
 }
 
@@ -649,11 +648,12 @@ __device__ __forceinline__ bool chunk_ready(const uint4 v) {
 // sum of the 8 values of a staged chunk (in matrix-core k order) times 16+q,
 // for one unpacked word: A.x holds (x0, x4), A.y (x2, x6), A.z (x1, x5), A.w
 // (x3, x7), the order of unpack_q4's pairs.
+template <bool F16>
 __device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, float c) {
-  c = fdot2(A.x, q.p0, c);
-  c = fdot2(A.y, q.p1, c);
-  c = fdot2(A.z, q.p2, c);
-  return fdot2(A.w, q.p3, c);
+  c = fdot2_act<F16>(A.x, q.p0, c);
+  c = fdot2_act<F16>(A.y, q.p1, c);
+  c = fdot2_act<F16>(A.z, q.p2, c);
+  return fdot2_act<F16>(A.w, q.p3, c);
 }
 
 // The workgroup's down blocks and the wave's k blocks: wave w takes blocks
@@ -742,7 +742,7 @@ struct DnBlockF {
   float wt[NT];
   float s[4];  // first group (columns 2lr, 2lr+1), second group
 };
-template <int BPW, int NT>
+template <int BPW, int NT, bool F16>
 __device__ __forceinline__ void dn_blocks_valu(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                                int tm_v, int U, const DnPlan& dp, DnBlockF<NT> (&xb)[BPW]) {
   const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + kDownKpw - 1) >> a.gsh, a.Gd - 1);
@@ -757,10 +757,10 @@ __device__ __forceinline__ void dn_blocks_valu(const DecArgs& a, const DecProlog
       xb[e].ci[t] = x.ci[t];
       xb[e].wt[t] = x.wt[t];
     }
-    xb[e].s[0] = bf16lo(x.s1);
-    xb[e].s[1] = bf16hi(x.s1);
-    xb[e].s[2] = bf16lo(x.s2);
-    xb[e].s[3] = bf16hi(x.s2);
+    xb[e].s[0] = sc_lo<F16>(x.s1);
+    xb[e].s[1] = sc_hi<F16>(x.s1);
+    xb[e].s[2] = sc_lo<F16>(x.s2);
+    xb[e].s[3] = sc_hi<F16>(x.s2);
   }
 }
 
@@ -778,10 +778,12 @@ __device__ __forceinline__ uint32_t dn_chunk(uint32_t ci, int j, int nkb, uint32
 struct DnQ {
   Q4Pairs q[2];
 };
+template <bool F16>
 __device__ __forceinline__ void dn_unpack(const uint2 w, uint32_t mq, Q4Pairs (&q)[2]) {
-  q[0] = unpack_q4(w.x, mq);
-  q[1] = unpack_q4(w.y, mq);
+  q[0] = unpack_q4_t<F16>(w.x, mq);
+  q[1] = unpack_q4_t<F16>(w.y, mq);
 }
+template <bool F16>
 __device__ __forceinline__ void dn_unpack(const DnQ& w, uint32_t, Q4Pairs (&q)[2]) {
   q[0] = w.q[0];
   q[1] = w.q[1];
@@ -794,18 +796,18 @@ struct DnMix {
 };
 // word (block e, k block j) of either source; e is a constant once the block
 // loops are unrolled, so the choice costs nothing
-template <int B>
+template <bool F16, int B>
 __device__ __forceinline__ void dn_word(const uint2 (&dw)[B][kDownKpw], int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
-  dn_unpack(dw[e][j], mq, q);
+  dn_unpack<F16>(dw[e][j], mq, q);
 }
-template <int B>
+template <bool F16, int B>
 __device__ __forceinline__ void dn_word(const DnQ (&dw)[B][kDownKpw], int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
-  dn_unpack(dw[e][j], mq, q);
+  dn_unpack<F16>(dw[e][j], mq, q);
 }
-template <int B, int NPRE>
+template <bool F16, int B, int NPRE>
 __device__ __forceinline__ void dn_word(const DnMix<B, NPRE>& dw, int e, int j, uint32_t mq, Q4Pairs (&q)[2]) {
-  if (e < NPRE) dn_unpack(dw.pre[e < NPRE ? e : 0][j], mq, q);
-  else dn_unpack(dw.raw[e][j], mq, q);
+  if (e < NPRE) dn_unpack<F16>(dw.pre[e < NPRE ? e : 0][j], mq, q);
+  else dn_unpack<F16>(dw.raw[e][j], mq, q);
 }
 
 // One or two tokens: dot products on the VALU, for blocks [e0, e1) of the
@@ -815,12 +817,12 @@ __device__ __forceinline__ void dn_word(const DnMix<B, NPRE>& dw, int e, int j, 
 // and token has its own dot chain; the first SPLIT of a wave's k blocks
 // belong to one scale group, the rest to the next.  The four lq lanes are
 // added at the end.
-template <int BPW, int NT, int SPLIT, bool FULL, class W>
+template <int BPW, int NT, int SPLIT, bool FULL, bool F16, class W>
 __device__ __forceinline__ void dn_valu(const DecArgs& a, const DnLds& L, const DnPlan& dp, int e_lo, int e_hi,
                                         const W& dw, const DnBlockF<NT> (&xb)[BPW], float (&acc)[NT][2]) {
   constexpr int KPW = kDownKpw;
   const int cps = a.I >> 3;
-  const uint32_t mq = q4_magic();
+  const uint32_t mq = q4_magic_t<F16>();
   const uint32_t zc = (uint32_t)(a.S * cps);  // the zero row
 #pragma unroll
   for (int e = 0; e < BPW; ++e) {
@@ -830,14 +832,14 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DnLds& L, const 
 #pragma unroll
       for (int j = 0; j < KPW; ++j) {
         Q4Pairs q[2];
-        dn_word(dw, e, j, mq, q);
+        dn_word<F16>(dw, e, j, mq, q);
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           const uint32_t ci = dn_chunk<FULL>(x.ci[t], j, dp.nkb, zc);
           const uint4 A = L.sact[ci];
-          const float b = L.abias[ci];
+          const float b = F16 ? 0.f : L.abias[ci];  // fp16: q - 8 operands, no offset
 #pragma unroll
-          for (int h = 0; h < 2; ++h) d[j][t][h] = dot_chunk(A, q[h], b);
+          for (int h = 0; h < 2; ++h) d[j][t][h] = dot_chunk<F16>(A, q[h], b);
         }
       }
 #pragma unroll
@@ -865,14 +867,14 @@ __device__ __forceinline__ void dn_valu(const DecArgs& a, const DnLds& L, const 
 // with a constant -24 operand for the int4 offset, accumulated per scale
 // group (the first SPLIT of the wave's k blocks, then the rest) and scaled
 // by the group scale and routing weight into acc[h] (rows 4lq + jj).
-template <int BPW, int SPLIT, bool FULL, class W>
+template <int BPW, int SPLIT, bool FULL, bool F16, class W>
 __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                         int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi,
                                         const W& dw, f32x4_t (&acc)[2]) {
   constexpr int KPW = kDownKpw;
   const int lane = threadIdx.x & (kWave - 1), lq = lane >> 4;
   const int cps = a.I >> 3;
-  const uint32_t mq = q4_magic();
+  const uint32_t mq = q4_magic_t<F16>();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(kQ4BiasPair, kQ4BiasPair, kQ4BiasPair, kQ4BiasPair);
   const int g1 = min(dp.kbw0 >> a.gsh, a.Gd - 1), g2 = min((dp.kbw0 + KPW - 1) >> a.gsh, a.Gd - 1);
@@ -898,19 +900,19 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
         const int sgi = j < SPLIT ? 0 : 1;
         const uint4 A = L.sact[dn_chunk<FULL>(x.ci[0], j, dp.nkb, zc)];
         Q4Pairs q[2];
-        dn_word(dw, e, j, mq, q);
-        D[sgi][0] = mfma_bf16(A, make_uint4(q[0].p0, q[0].p1, q[0].p2, q[0].p3), D[sgi][0]);
-        D[sgi][1] = mfma_bf16(A, make_uint4(q[1].p0, q[1].p1, q[1].p2, q[1].p3), D[sgi][1]);
-        Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
+        dn_word<F16>(dw, e, j, mq, q);
+        D[sgi][0] = mfma_act<F16>(A, make_uint4(q[0].p0, q[0].p1, q[0].p2, q[0].p3), D[sgi][0]);
+        D[sgi][1] = mfma_act<F16>(A, make_uint4(q[1].p0, q[1].p1, q[1].p2, q[1].p3), D[sgi][1]);
+        if constexpr (!F16) Db[sgi] = mfma_bf16(A, bc, Db[sgi]);
       }
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const float sa = h ? bf16hi(x.s1) : bf16lo(x.s1);
-        const float sb = h ? bf16hi(x.s2) : bf16lo(x.s2);
+        const float sa = h ? sc_hi<F16>(x.s1) : sc_lo<F16>(x.s1);
+        const float sb = h ? sc_hi<F16>(x.s2) : sc_lo<F16>(x.s2);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          float v = sa * (D[0][h][jj] + Db[0][jj]);
-          if constexpr (SPLIT < KPW) v += sb * (D[1][h][jj] + Db[1][jj]);
+          float v = sa * (F16 ? D[0][h][jj] : D[0][h][jj] + Db[0][jj]);
+          if constexpr (SPLIT < KPW) v += sb * (F16 ? D[1][h][jj] : D[1][h][jj] + Db[1][jj]);
           acc[h][jj] += wv[jj] * v;
         }
       }
@@ -921,29 +923,29 @@ __device__ __forceinline__ void dn_mfma(const DecArgs& a, const DecPrologue& P, 
 // Blocks [e_lo, e_hi) with the wave's variant: k blocks in its first scale
 // group (1, 2 or all KPW; a group has at least KPW blocks) and whether the
 // wave has all KPW k blocks.
-template <int BPW, int MODE, int SPLIT, class W>
+template <int BPW, int MODE, bool F16, int SPLIT, class W>
 __device__ __forceinline__ void dn_run_split(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v,
                                              int tm_v, int U, const DnPlan& dp, int e_lo, int e_hi, const W& dw,
                                              const DnBlockF<(MODE > 0 ? MODE : 1)> (&xb)[BPW],
                                              float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   constexpr int NT = MODE > 0 ? MODE : 1;
   if (dp.nkb == kDownKpw) {
-    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, true>(a, L, dp, e_lo, e_hi, dw, xb, accv);
-    else dn_mfma<BPW, SPLIT, true>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, true, F16>(a, L, dp, e_lo, e_hi, dw, xb, accv);
+    else dn_mfma<BPW, SPLIT, true, F16>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
   } else {
-    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, false>(a, L, dp, e_lo, e_hi, dw, xb, accv);
-    else dn_mfma<BPW, SPLIT, false>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
+    if constexpr (MODE > 0) dn_valu<BPW, NT, SPLIT, false, F16>(a, L, dp, e_lo, e_hi, dw, xb, accv);
+    else dn_mfma<BPW, SPLIT, false, F16>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, accm);
   }
 }
-template <int BPW, int MODE, class W>
+template <int BPW, int MODE, bool F16, class W>
 __device__ __forceinline__ void dn_run(const DecArgs& a, const DecPrologue& P, const DnLds& L, int epos_v, int tm_v,
                                        int U, const DnPlan& dp, int e_lo, int e_hi, const W& dw,
                                        const DnBlockF<(MODE > 0 ? MODE : 1)> (&xb)[BPW],
                                        float (&accv)[MODE > 0 ? MODE : 1][2], f32x4_t (&accm)[2]) {
   const int split = min(kDownKpw, (1 << a.gsh) - (dp.kbw0 & ((1 << a.gsh) - 1)));
-  if (split == 1) dn_run_split<BPW, MODE, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
-  else if (split == 2) dn_run_split<BPW, MODE, 2>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
-  else dn_run_split<BPW, MODE, kDownKpw>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
+  if (split == 1) dn_run_split<BPW, MODE, F16, 1>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
+  else if (split == 2) dn_run_split<BPW, MODE, F16, 2>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
+  else dn_run_split<BPW, MODE, F16, kDownKpw>(a, P, L, epos_v, tm_v, U, dp, e_lo, e_hi, dw, xb, accv, accm);
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -1059,7 +1061,7 @@ __device__ __forceinline__ uint32_t f32_signal_bits(float v) {
 // read, the products, the sums over the waves, then per unit either the
 // output (a unit held whole, or the unit's first workgroup once the others'
 // partial sums are in) or this workgroup's partial sum for the first one.
-template <int BPW, int MODE, int CPT, bool PRE>
+template <int BPW, int MODE, int CPT, bool PRE, bool F16>
 __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& P, char* lds, const DnLayout& ly,
                                            int U, int uexp_v, const uint16_t* act, float* part, int blo, int bhi,
                                            DnPlan dp, const uint2 (&dw0)[BPW][kDownKpw]) {
@@ -1127,12 +1129,12 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   constexpr int NPRE = PRE ? BPW : (MODE == 0 ? (BPW < kDownPreMfma ? BPW : kDownPreMfma) : 0);
   DnQ dq[NPRE > 0 ? NPRE : 1][kDownKpw];
   if constexpr (NPRE > 0) {
-    const uint32_t mq = q4_magic();
+    const uint32_t mq = q4_magic_t<F16>();
 #pragma unroll
     for (int e = 0; e < NPRE; ++e)
 #pragma unroll
       for (int j = 0; j < kDownKpw; ++j) {
-        dn_unpack(dw0[e][j], mq, dq[e][j].q);
+        dn_unpack<F16>(dw0[e][j], mq, dq[e][j].q);
         // here, not next to the products: the unpacking overlaps the wait
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -1148,9 +1150,9 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
   dp.d_a = d_first;
   dp.n0 = min(dp.nb, (d_first + 1) * U - blo);
   DnBlockF<NT> xb[BPW];
-  if constexpr (MODE > 0) dn_blocks_valu<BPW, NT>(a, P, L, epos_v, tm_v, U, dp, xb);
+  if constexpr (MODE > 0) dn_blocks_valu<BPW, NT, F16>(a, P, L, epos_v, tm_v, U, dp, xb);
   int* bad = const_cast<int*>(&P.bad);
-  stage_acts<CPT, (MODE > 0)>(a, L, act, c0, c1, x0, x1, bad);  // waits for every load of the wave
+  stage_acts<CPT, (MODE > 0 && !F16)>(a, L, act, c0, c1, x0, x1, bad);  // waits for every load of the wave
   lds_barrier();
   GI_STAMP(5);
 
@@ -1166,15 +1168,15 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
       for (int t = 0; t < NT; ++t) accv[p][t][h] = 0.f;
     }
   if constexpr (NPRE == BPW) {
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, xb, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, xb, accv[1], accm[1]);
+    dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dq, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dq, xb, accv[1], accm[1]);
   } else if constexpr (NPRE > 0) {
     const DnMix<BPW, NPRE> mix{dw0, dq};
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, mix, xb, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, mix, xb, accv[1], accm[1]);
+    dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, mix, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, mix, xb, accv[1], accm[1]);
   } else {
-    dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, xb, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, xb, accv[1], accm[1]);
+    dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw0, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw0, xb, accv[1], accm[1]);
   }
   // further batches (more blocks than the registers hold)
   for (int b0 = blo + BPW; b0 < bhi; b0 += BPW) {
@@ -1185,9 +1187,9 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
     dp.n0 = max(0, min(dp.nb, (d_first + 1) * U - b0));
     uint2 dw[BPW][kDownKpw];
     dn_load<BPW>(a, uexp_v, U, dp, dw);
-    if constexpr (MODE > 0) dn_blocks_valu<BPW, NT>(a, P, L, epos_v, tm_v, U, dp, xb);
-    if (dp.n0 > 0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw, xb, accv[0], accm[0]);
-    if (dp.nb > dp.n0) dn_run<BPW, MODE>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw, xb, accv[1], accm[1]);
+    if constexpr (MODE > 0) dn_blocks_valu<BPW, NT, F16>(a, P, L, epos_v, tm_v, U, dp, xb);
+    if (dp.n0 > 0) dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, 0, dp.n0, dw, xb, accv[0], accm[0]);
+    if (dp.nb > dp.n0) dn_run<BPW, MODE, F16>(a, P, L, epos_v, tm_v, U, dp, dp.n0, dp.nb, dw, xb, accv[1], accm[1]);
   }
   // sums over the waves, fixed order (the per-wave sums alias the staged rows)
   lds_barrier();
@@ -1282,9 +1284,9 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
       lds_barrier();
     }
     if (writer) {
-      if (!a.overwrite) s += bf16_to_f32((old[p] >> (16 * (wc & 1))) & 0xffffu);
+      if (!a.overwrite) s += act_to_f32<F16>((old[p] >> (16 * (wc & 1))) & 0xffffu);
       if (P.bad) s = __uint_as_float(0x7fc00000u);  // never a wrong finite value
-      a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_bf16(s);
+      a.out[(size_t)wt * a.H + kUnitCols * d + wc] = f32_to_act<F16>(s);
     }
   }
   GI_STAMP(8);
@@ -1299,7 +1301,7 @@ __device__ __forceinline__ void down_phase(const DecArgs& a, const DecPrologue& 
 // NI = 3 is the general path (two items in flight, the next one loaded as
 // each finishes), which issues the down words after its items (registers: a
 // rare case).
-template <int KBW, int NI, int BPW>
+template <int KBW, int NI, int BPW, bool F16>
 __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P, const GuLds& L, int U,
                                          int uexp_v, uint16_t* act, const DnPlan& dp, int n_items,
                                          uint2 (&dw)[BPW][kDownKpw]) {
@@ -1309,14 +1311,14 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
   if constexpr (NI >= 2) gu_load<KBW>(a, uexp_v, it0 + G, n_items, b1);
   GI_STAMP(3);
   if constexpr (NI == 1) {
-    gu_item<KBW, true>(a, P, it0, b0, L, act);
+    gu_item<KBW, F16, true>(a, P, it0, b0, L, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
   } else if constexpr (NI == 2) {
-    gu_item<KBW, true>(a, P, it0, b0, L, act);
+    gu_item<KBW, F16, true>(a, P, it0, b0, L, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
-    gu_item<KBW, true>(a, P, it0 + G, b1, L, act);
+    gu_item<KBW, F16, true>(a, P, it0 + G, b1, L, act);
   } else {
-    gu_items<KBW, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
+    gu_items<KBW, F16, 0>(a, P, L, uexp_v, it0, G, n_items, b0, b1, act);
     dn_load<BPW>(a, uexp_v, U, dp, dw);
   }
   GI_STAMP(4);
@@ -1330,13 +1332,13 @@ __device__ __forceinline__ void up_phase(const DecArgs& a, const DecPrologue& P,
 // routing and the Token-Union tables.  The epoch is read after the routing:
 // a value needed in scalar registers is otherwise read right after its load,
 // and the routing would wait for it.
-template <int KBW, int VPL>
+template <int KBW, int VPL, bool F16>
 __device__ __forceinline__ u32x2_t dec_start(const DecArgs& a, DecPrologue& P, XRegs<KBW>& xr) {
   DecIn<VPL> in;
   dec_issue<VPL>(a, in);
   u32x2_t ep = load_epoch(a);
   load_x<KBW>(a, xr);
-  dec_prologue<VPL>(a, P, in);
+  dec_prologue<VPL, F16>(a, P, in);
   asm volatile("" : "+v"(ep));
   return ep;
 }
@@ -1358,7 +1360,7 @@ __device__ __forceinline__ void dec_end(const DecArgs& a, const DecPrologue& P, 
   }
 }
 
-template <int KBW, int MODE, int BPW, int CPT>
+template <int KBW, int MODE, int BPW, int CPT, bool F16>
 __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   __shared__ DecPrologue P;
   extern __shared__ __attribute__((aligned(16))) char dyn_lds[];
@@ -1368,9 +1370,9 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   GI_STAMP(0);
   XRegs<KBW> xr;
   u32x2_t epr;
-  if (a.E <= 2 * kWave) epr = dec_start<KBW, 2>(a, P, xr);
-  else if (a.E <= 4 * kWave) epr = dec_start<KBW, 4>(a, P, xr);
-  else epr = dec_start<KBW, kRouteMaxExperts / kWave>(a, P, xr);
+  if (a.E <= 2 * kWave) epr = dec_start<KBW, 2, F16>(a, P, xr);
+  else if (a.E <= 4 * kWave) epr = dec_start<KBW, 4, F16>(a, P, xr);
+  else epr = dec_start<KBW, kRouteMaxExperts / kWave, F16>(a, P, xr);
   const unsigned long long ep = moe_state::epoch_count(((unsigned long long)epr.y << 32) | epr.x) + 1ull;
   const int parity = (int)(ep & 1ull);
   uint16_t* act = a.act + (size_t)parity * (kActParity / 2);
@@ -1421,11 +1423,11 @@ __global__ __launch_bounds__(kThreads) void moe_decode_kernel(DecArgs a) {
   dp.nkb = (wave + 1) * a.Tk / kWaves - dp.kbw0;
   uint2 dw[BPW][kDownKpw];
   if (n_my == 0) dn_load<BPW>(a, uexp_v, U, dp, dw);
-  else if (n_my == 1) up_phase<KBW, 1, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
-  else if (n_my == 2) up_phase<KBW, 2, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
-  else up_phase<KBW, 3, BPW>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  else if (n_my == 1) up_phase<KBW, 1, BPW, F16>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  else if (n_my == 2) up_phase<KBW, 2, BPW, F16>(a, P, L, U, uexp_v, act, dp, n_items, dw);
+  else up_phase<KBW, 3, BPW, F16>(a, P, L, U, uexp_v, act, dp, n_items, dw);
   if (bhi > blo)
-    down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4>(a, P, dyn_lds, ly, U, uexp_v, act, part, blo, bhi, dp, dw);
+    down_phase<BPW, MODE, CPT, MODE == 1 && BPW <= 4, F16>(a, P, dyn_lds, ly, U, uexp_v, act, part, blo, bhi, dp, dw);
   dec_end(a, P, ep, parity);
 #ifdef GI_TIMELINE
   GI_STAMP(9);
@@ -1512,15 +1514,17 @@ bool decode_plan(int M, int S, int H, int I, int cus, DecodePlan& pl) {
   return true;
 }
 
-template <int KBW>
+template <int KBW, bool F16>
 const void* plan_kernel(const DecodePlan& pl) {
-  if (pl.mode == 1 && pl.bpw == 4 && pl.cpt == 2) return (const void*)moe_decode_kernel<KBW, 1, 4, 2>;
-  if (pl.mode == 1) return (const void*)moe_decode_kernel<KBW, 1, 8, kMaxStage>;
-  if (pl.mode == 2) return (const void*)moe_decode_kernel<KBW, 2, 8, kMaxStage>;
-  return (const void*)moe_decode_kernel<KBW, 0, 8, kMaxStage>;
+  if (pl.mode == 1 && pl.bpw == 4 && pl.cpt == 2) return (const void*)moe_decode_kernel<KBW, 1, 4, 2, F16>;
+  if (pl.mode == 1) return (const void*)moe_decode_kernel<KBW, 1, 8, kMaxStage, F16>;
+  if (pl.mode == 2) return (const void*)moe_decode_kernel<KBW, 2, 8, kMaxStage, F16>;
+  return (const void*)moe_decode_kernel<KBW, 0, 8, kMaxStage, F16>;
 }
-const void* decode_kernel(int kbw, const DecodePlan& pl) {
-  return kbw == 2 ? plan_kernel<2>(pl) : plan_kernel<11>(pl);
+// f16: fp16 activations, scales and out (fp16 products on q - 8 operands)
+const void* decode_kernel(int kbw, const DecodePlan& pl, bool f16) {
+  if (f16) return kbw == 2 ? plan_kernel<2, true>(pl) : plan_kernel<11, true>(pl);
+  return kbw == 2 ? plan_kernel<2, false>(pl) : plan_kernel<11, false>(pl);
 }
 
 int log2_exact(int v) {
@@ -1569,6 +1573,8 @@ int moe_decode_rows_per_launch(int top_k) {
 }
 
 bool moe_decode_supported(const MoeHostArgs& h) {
+  // bf16 activations, or fp16 ones with caller-given routing
+  if (h.x_dtype != GI_DTYPE_BF16 && !(h.x_dtype == GI_DTYPE_FP16 && !h.logits)) return false;
   if (h.H % 32 || h.I % 32 || h.H > kMaxUnits * kUnitCols || h.I > kMaxI) return false;
   if (h.gs % 32 || log2_exact(h.gs / 32) < 0) return false;
   // a scale group covers at least 2 k blocks: a wave's gate/up blocks span at
@@ -1592,7 +1598,8 @@ bool moe_decode_supported(const MoeHostArgs& h) {
   if (lds > kMaxDynLds) return false;
   // every workgroup of the grid (one per CU) must be resident at once
   int blocks = 0;
-  if (blocks_per_cu(decode_kernel(kbw_for(h.H), pl), lds, &blocks) != GI_OK || blocks < 1) return false;
+  if (blocks_per_cu(decode_kernel(kbw_for(h.H), pl, h.x_dtype == GI_DTYPE_FP16), lds, &blocks) != GI_OK || blocks < 1)
+    return false;
   return true;
 }
 
@@ -1652,7 +1659,7 @@ int launch_moe_decode(const MoeHostArgs& h, void* state, int* status) {
     k.out_idx = h.out_idx ? h.out_idx + (size_t)r0 * h.top_k : nullptr;
     k.out_w = h.out_w ? (uint16_t*)h.out_w + (size_t)r0 * h.top_k : nullptr;
     const size_t lds = lds_for(kbw, k.S, k.I, k.Gd, k.units, pl.grid);
-    const void* fn = decode_kernel(kbw, pl);
+    const void* fn = decode_kernel(kbw, pl, h.x_dtype == GI_DTYPE_FP16);
     int blocks = 0;
     int st = blocks_per_cu(fn, lds, &blocks);  // also raises the kernel's dynamic-LDS limit
     if (st != GI_OK) return st;

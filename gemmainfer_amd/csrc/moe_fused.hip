@@ -1165,12 +1165,16 @@ int launch_fused_moe(const MoeHostArgs& h) {
                 "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
   if (((uintptr_t)h.workspace) % kAlign)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace must be 256-byte aligned");
-  if (h.x_dtype == GI_DTYPE_FP16 && h.M == 1 && moe_decode1_supported(h)) {
-    // one fp16 token: the one-token kernel's fp16 variant (split bf16 operands)
+  if (h.x_dtype == GI_DTYPE_FP16) {
+    // one fp16 token: the one-token kernel's fp16 variant (split bf16
+    // operands); up to one launch of rows: the 8-row kernel's fp16 variant
+    // (fp16 products on q - 8 operands)
     const int per = moe_rows_per_launch(h.top_k);
     const WsLayout L = ws_layout((h.M < per ? h.M : per) * h.top_k, h.H, h.I, kTaskCols);
     char* ws0 = (char*)h.workspace;
-    return launch_moe_decode1(h, ws0 + L.state, (int*)(ws0 + L.status));
+    if (h.M == 1 && moe_decode1_supported(h)) return launch_moe_decode1(h, ws0 + L.state, (int*)(ws0 + L.status));
+    if (h.M <= moe_decode_rows_per_launch(h.top_k) && moe_decode_supported(h))
+      return launch_moe_decode(h, ws0 + L.state, (int*)(ws0 + L.status));
   }
   if (h.x_dtype != GI_DTYPE_BF16) {
     const size_t base = prefill_base(h.H, h.I);

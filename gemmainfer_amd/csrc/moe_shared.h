@@ -253,6 +253,63 @@ __device__ __forceinline__ void f16_split(const uint4 v, uint4& hi, uint4& lo) {
   f16_split2(v.z, hi.z, lo.z);
   f16_split2(v.w, hi.w, lo.w);
 }
+// fp16 weight operands for fp16 activations on the fp16 products: a half
+// whose high byte is 0x58 and low byte 0x80 | q << 3 is exactly 144 + q
+// (exponent 2^7, q in mantissa bits 3-6), so the bytes of the bf16 16 + q
+// operands under 0x58 give 144 + q, and one packed fp16 add of -152 makes
+// q - 8 exactly.  The products then need no offset term, and every operand
+// and product is exact (fp16 x times a 4-bit integer, summed in fp32).
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t q4_magic_f16() {
+  uint32_t v = 0x58585858u;
+  asm volatile("" : "+v"(v));
+  return v;
+}
+__device__ __forceinline__ uint32_t f16_pair_less152(uint32_t p) {
+  const f16x2_t c = {(_Float16)-152.0f, (_Float16)-152.0f};
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, p) + c);
+}
+// the four pairs (q0,q4) (q2,q6) (q1,q5) (q3,q7) as fp16 q - 8
+__device__ __forceinline__ Q4Pairs unpack_q4_f16(uint32_t w, uint32_t mq16) {
+  const Q4Pairs q = unpack_q4(w, mq16);
+  return Q4Pairs{f16_pair_less152(q.p0), f16_pair_less152(q.p1), f16_pair_less152(q.p2), f16_pair_less152(q.p3)};
+}
+__device__ __forceinline__ f32x4_t mfma_f16(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c,
+                                                0, 0, 0);
+}
+__device__ __forceinline__ float fdot2_f16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, a), __builtin_bit_cast(f16x2_t, b), c, false);
+}
+// The activation type's forms: bf16 (16 + q operands, an offset term) or
+// fp16 (q - 8 operands, none).
+template <bool F16>
+__device__ __forceinline__ uint32_t q4_magic_t() {
+  if constexpr (F16) return q4_magic_f16();
+  else return q4_magic();
+}
+template <bool F16>
+__device__ __forceinline__ Q4Pairs unpack_q4_t(uint32_t w, uint32_t mq) {
+  if constexpr (F16) return unpack_q4_f16(w, mq);
+  else return unpack_q4(w, mq);
+}
+template <bool F16>
+__device__ __forceinline__ uint4 q4_operand_t(uint32_t w, uint32_t mq) {
+  const Q4Pairs q = unpack_q4_t<F16>(w, mq);
+  return make_uint4(q.p0, q.p1, q.p2, q.p3);
+}
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma_act(uint4 a, uint4 b, f32x4_t c) {
+  if constexpr (F16) return mfma_f16(a, b, c);
+  else return mfma_bf16(a, b, c);
+}
+template <bool F16>
+__device__ __forceinline__ float fdot2_act(uint32_t a, uint32_t b, float c) {
+  if constexpr (F16) return fdot2_f16(a, b, c);
+  else return fdot2(a, b, c);
+}
+
 template <bool F16>
 __device__ __forceinline__ float sc_lo(uint32_t v) {
   if constexpr (F16) return fp16_to_f32((uint16_t)(v & 0xffffu));

@@ -105,6 +105,53 @@ def test_moe_fp16_one_token_edge_cases(gs):
     assert torch.equal(out, out_in)
 
 
+@pytest.mark.parametrize("gs", [64, 128])
+@pytest.mark.parametrize("m", [2, 5, 8])
+def test_moe_fp16_rows_edge_cases(gs, m):
+    """fp16 at 2-8 rows runs the 8-row kernel's fp16 variant (fp16 products
+    with the int4 codes unpacked exactly to q - 8): the two-token dot-product
+    path (m=2) and the matrix-core path (m=5, 8), ids outside [0, E) skipped
+    (marlin.cu:304, :473), one expert in several slots of a token, every
+    token on one expert, int64 ids and fp32 weights cast to fp16
+    (marlin.cu:631-636), activations spread over 1/16 .. 4 times their
+    scale plus subnormals and full-significand values, accumulation into a
+    non-zero out, and all ids invalid (out unchanged).  The magnitudes keep
+    outputs in the hundreds: in the thousands, one-ulp flips of the fp16
+    activation rounding (marlin.cu:421-423) under any fp32 sum order exceed
+    one output ulp (a float32 evaluation of the same semantics fails the
+    bound there too); on these inputs it stays within 0.75 of it."""
+    dt = torch.float16
+    W = _moe_weights(E, H, I, gs, seed=930 + gs, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    g = torch.Generator().manual_seed(931 + m)
+    mag = torch.exp(0.5 * torch.randn(m, H, generator=g)).clamp(max=4.0)
+    x = (synth.activations(m, H, seed=932 + m) * mag).to(dt)
+    x[0, :8] = torch.tensor([6e-8, -6e-8, 1e-6, -3e-5, 0.0, 17.0078125, -1.0009765625, 0.33325195]).to(dt)
+    ids = torch.stack([torch.randperm(E, generator=g)[:8] for _ in range(m)])
+    ids[0, 1], ids[0, 4], ids[m - 1, 2] = -1, E, ids[m - 1, 6]       # invalid ids, a repeated expert
+    cases = [
+        (ids.to(torch.int64), torch.rand(m, 8, generator=g)),
+        (torch.full((m, 8), 3, dtype=torch.int32), (torch.rand(m, 8, generator=g) / 4).to(dt)),
+        (ids.clamp(0, E - 1).to(torch.int32), torch.softmax(torch.randn(m, 8, generator=g), dim=-1).to(torch.bfloat16)),
+    ]
+    for n, (idx, w) in enumerate(cases):
+        out_in = (torch.randn(m, H, generator=g) * 0.1).to(dt)
+        out = out_in.to(DEV).clone()
+        gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"],
+                                          Wd["down_packed"], Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+        torch.cuda.synchronize()
+        ref = _oracle(W, x, idx, w.to(dt), out_in, gs, "fp16")
+        assert_dtype_close(out, ref, "fp16", f"fp16 rows m={m} gs={gs} case {n}")
+    idx = torch.full((m, 8), -1, dtype=torch.int32)
+    idx[:, ::2] = E
+    out_in = (torch.randn(m, H, generator=g) * 0.1).to(dt).to(DEV)
+    out = out_in.clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), torch.ones(m, 8, dtype=dt).to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_in)
+
+
 @pytest.mark.parametrize("tag", ["fp16", "fp32"])
 def test_moe_duplicates_invalid_ids_and_many_rows(tag):
     dt = DT[tag]
