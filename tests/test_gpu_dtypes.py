@@ -152,6 +152,31 @@ def test_moe_fp16_rows_edge_cases(gs, m):
     assert torch.equal(out, out_in)
 
 
+@pytest.mark.parametrize("h,i,e,gs", [(256, 128, 32, 64), (2816, 704, 128, 128)])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_moe_fp16_eight_row_modes(h, i, e, gs, m):
+    """top_k = 16, more experts per token than the one-token kernel holds:
+    every call of 1-4 rows is one launch of the 8-row kernel's fp16 variant,
+    in its one-row (m=1) and two-row (m=2) dot-product modes and its
+    matrix-core mode (m=4), at a hidden size of at most 512 and at the Gemma
+    size; an id outside [0, E) and a repeated expert in a token
+    (marlin.cu:304, :473)."""
+    dt, k = torch.float16, 16
+    W = _moe_weights(e, h, i, gs, seed=950 + m, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    g = torch.Generator().manual_seed(951 + m)
+    idx = torch.stack([torch.randperm(e, generator=g)[:k] for _ in range(m)]).to(torch.int32)
+    idx[0, 3], idx[m - 1, 5] = -1, idx[m - 1, 9]
+    w = torch.softmax(torch.randn(m, k, generator=g), dim=-1).to(dt)
+    x = synth.activations(m, h, seed=952 + m).to(dt)
+    out_in = (torch.randn(m, h, generator=g) * 0.1).to(dt)
+    out = out_in.to(DEV).clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, "fp16"), "fp16", f"fp16 top-16 h={h} m={m}")
+
+
 @pytest.mark.parametrize("tag", ["fp16", "fp32"])
 def test_moe_duplicates_invalid_ids_and_many_rows(tag):
     dt = DT[tag]
