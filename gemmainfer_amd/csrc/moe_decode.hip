@@ -58,6 +58,15 @@
 // on this part a returning atomic on one address costs microseconds when 256
 // workgroups issue it.
 //
+// fp16 activations (template parameter F16; x, scales and out in fp16, the
+// routing caller-given): the same kernel with fp16 products.  The int4 codes
+// are unpacked exactly to fp16 q - 8 (the bytes of the bf16 16 + q operands
+// under a 0x58 high byte are the half 144 + q; a packed fp16 add of -152), so
+// the offset products and the offset sums drop out, and the activation, the
+// routing weights and out are rounded to fp16 where the bf16 kernel rounds to
+// bf16.  Everything else (tables, exchange, partial sums) is shared: the
+// exchange and the LDS hold 16-bit values of either type.
+//
 // Code shape: the hot loops are straight-line with register indices fixed at
 // compile time, per-expert values are read from registers with readlane (no
 // LDS round trip before a weight load), no integer division in a loop (group
@@ -131,7 +140,7 @@ struct DecArgs {
   uint16_t* out;
   unsigned long long* epochs;  // [kEpochSlots]
   uint16_t* act;               // [2][kSlots][I] (parity stride kActParity bytes): rows in expert
-                               // order, inverted bf16, matrix-core k order
+                               // order, inverted bf16 (fp16), matrix-core k order
   float* part;                 // [2][units][kPartSlots][kRows][32] partial sums, inverted bits
   int* status;
   int* host_flag;              // host-visible error flag of the device (may be null)
@@ -610,9 +619,9 @@ __host__ __device__ inline int blk_lo(int w, int NB, int G) { return w * NB / G;
 __host__ __device__ inline int blk_owner(int b, int NB, int G) { return ((b + 1) * G - 1) / NB; }
 
 struct DnLds {
-  uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16, k order); row S is zero
+  uint4* sact;    // [S + 1][I/8] activation chunks (plain bf16 or fp16, k order); row S is zero
   float* abias;   // [S + 1][I/8] -24 * sum of each chunk's 8 values
-  uint32_t* dsc;  // [block of the workgroup][Gd][16] bf16 scale pairs of each lane's two columns
+  uint32_t* dsc;  // [block of the workgroup][Gd][16] scale pairs (bf16 or fp16) of each lane's two columns
   float* red;     // [2][kWaves][kRows][32] per-wave output sums (aliases sact once it is consumed)
   float* pbuf;    // [kPartSlots][kRows][32] partial sums of a unit's other workgroups (after red)
 };

@@ -43,6 +43,13 @@
 //
 // Deterministic: every sum has a fixed order, whatever the timing.
 //
+// fp16 activations (template parameter F16; x, scales and out in fp16, the
+// routing caller-given): the same bf16 products, each fp16 value of x and of
+// the activations split exactly into a bf16 hi and a bf16 lo part that take
+// two A operand rows (items: rows 0 and 1; units: rows 0-3 for the two k
+// blocks' hi and lo parts), the rows' products added in fp32.  The unpack of
+// the int4 words, which the items wait on, stays the bf16 kernel's.
+//
 // Exchange (moe_state.h): activations are stored bit-inverted, 16 bytes at a
 // time, into the activation buffer of the launch's parity (expert-major rows
 // of I values, matrix-core k order within each 8); partial sums, inverted,
