@@ -177,6 +177,30 @@ def test_moe_fp16_eight_row_modes(h, i, e, gs, m):
     assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, "fp16"), "fp16", f"fp16 top-16 h={h} m={m}")
 
 
+@pytest.mark.parametrize("m", [7, 12])
+def test_moe_fp16_deterministic_and_multi_launch(m):
+    """fp16 on the 8-row kernel: one launch (m=7) and two launches of 8 and 4
+    rows (m=12), against the oracle, and bitwise the same result on a second
+    call (every sum has a fixed order)."""
+    dt, gs = torch.float16, 128
+    W = _moe_weights(E, H, I, gs, seed=970 + m, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    x = synth.activations(m, H, seed=971 + m).to(dt)
+    logits = synth.router_logits(m, E, seed=972 + m, verify_noise=0.5)
+    top, idx = torch.topk(logits, 8, dim=-1)
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(dt)
+    idx = idx.to(torch.int32)
+    outs = []
+    for _ in range(2):
+        out = torch.zeros(m, H, dtype=dt, device=DEV)
+        gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                          Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+        torch.cuda.synchronize()
+        outs.append(out)
+    assert torch.equal(outs[0].view(torch.int16), outs[1].view(torch.int16))
+    assert_dtype_close(outs[0], _oracle(W, x, idx, w, torch.zeros(m, H), gs, "fp16"), "fp16", f"fp16 m={m}")
+
+
 @pytest.mark.parametrize("tag", ["fp16", "fp32"])
 def test_moe_duplicates_invalid_ids_and_many_rows(tag):
     dt = DT[tag]
