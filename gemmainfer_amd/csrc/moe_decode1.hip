@@ -44,11 +44,13 @@
 // Deterministic: every sum has a fixed order, whatever the timing.
 //
 // fp16 activations (template parameter F16; x, scales and out in fp16, the
-// routing caller-given): the same bf16 products, each fp16 value of x and of
-// the activations split exactly into a bf16 hi and a bf16 lo part that take
-// two A operand rows (items: rows 0 and 1; units: rows 0-3 for the two k
-// blocks' hi and lo parts), the rows' products added in fp32.  The unpack of
-// the int4 words, which the items wait on, stays the bf16 kernel's.
+// routing caller-given).  Items: the same bf16 products, each fp16 value of x
+// split exactly into a bf16 hi and a bf16 lo part that take A rows 0 and 1,
+// the rows' products added in fp32; their int4 unpack, which the items wait
+// on, stays the bf16 kernel's.  Units, which unpack their words before the
+// activations arrive: fp16 products with the codes unpacked exactly to fp16
+// q - 8 (the same bytes under 0x58, less 152), so the activations are staged
+// as they arrive, with no split and no offset sums.
 //
 // Exchange (moe_state.h): activations are stored bit-inverted, 16 bytes at a
 // time, into the activation buffer of the launch's parity (expert-major rows
@@ -170,9 +172,8 @@ struct ItemLds {
 };
 template <bool F16>
 struct UnitLds {
-  uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 in matrix-core k order (fp16: hi)
-  uint4 sact_lo[F16 ? kMaxU * kMaxTk * 4 : 1];  // fp16: the bf16 lo parts
-  float cbias[kMaxU * kMaxTk * 4];  // -24 * each chunk's sum
+  uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 or fp16 in matrix-core k order
+  float cbias[kMaxU * kMaxTk * 4];  // -24 * each chunk's sum (bf16; the fp16 products need none)
   uint4 dsc[kMaxU * kMaxGd * 4];    // down scales of the unit's columns [u][g][32]
   float4 red[kW][16];
 };
@@ -207,6 +208,20 @@ __device__ __forceinline__ float dot_chunk(const uint4 A, const Q4Pairs& q, floa
 // q4_operand (moe_shared.h) in 8 VALU operations per word: the byte of code
 // q is 0x80 | q << 3, and v_perm_b32 pairs those bytes with 0x41 bytes into
 // bf16 16 + q, in the matrix-core k order (0,4) (2,6) (1,5) (3,7).
+__device__ __forceinline__ uint4 q4_operand_fast(uint32_t w, uint32_t mq, uint32_t mc);
+// The same bytes as fp16 operands (mq holding 0x58 bytes: 144 + q), less 152:
+// exact q - 8 for the fp16 products.
+template <bool F16>
+__device__ __forceinline__ uint4 q4_operand_fast_t(uint32_t w, uint32_t mq, uint32_t mc) {
+  uint4 r = q4_operand_fast(w, mq, mc);
+  if constexpr (F16) {
+    r.x = f16_pair_less152(r.x);
+    r.y = f16_pair_less152(r.y);
+    r.z = f16_pair_less152(r.z);
+    r.w = f16_pair_less152(r.w);
+  }
+  return r;
+}
 __device__ __forceinline__ uint4 q4_operand_fast(uint32_t w, uint32_t mq, uint32_t mc) {
   const uint32_t lo = ((w << 3) & 0x78787878u) | mc;
   const uint32_t hi = ((w >> 1) & 0x78787878u) | mc;
@@ -843,11 +858,12 @@ __device__ __forceinline__ void unit_load(const D1Args& a, const D1Pro& P, int d
 
 // One wave polls the n chunks (16 bytes each, lane + 64j) of `src` into dst
 // (all of them present: no 16-bit half zero), inverted back, with each
-// chunk's -24 * sum of its 8 values into bias.  Bounded: on timeout the status
-// word and host flag are set, *bad is set and the wave goes on.
+// chunk's -24 * sum of its 8 values into bias (bf16; the fp16 products on
+// q - 8 operands need none).  Bounded: on timeout the status word and host
+// flag are set, *bad is set and the wave goes on.
 template <int CPT, bool F16>
 __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buffer_rsrc_t src, uint4* dst,
-                                            uint4* dst_lo, float* bias, int n, int* bad) {
+                                            float* bias, int n, int* bad) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t pending = 0u;
 #pragma unroll
@@ -864,16 +880,8 @@ __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buff
     for (int j = 0; j < CPT; ++j) {
       if (((pending >> j) & 1u) && chunk_ready(v[j])) {
         const uint4 x = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
-        if constexpr (F16) {
-          uint4 xh, xl;
-          f16_split(x, xh, xl);
-          dst[lane + j * kWave] = xh;
-          dst_lo[lane + j * kWave] = xl;
-          bias[lane + j * kWave] = q4_bias(xh) + q4_bias(xl);
-        } else {
-          dst[lane + j * kWave] = x;
-          bias[lane + j * kWave] = q4_bias(x);
-        }
+        dst[lane + j * kWave] = x;
+        if constexpr (!F16) bias[lane + j * kWave] = q4_bias(x);
         pending &= ~(1u << j);
       }
     }
@@ -903,16 +911,12 @@ __device__ __forceinline__ void folded_poll(const __amdgpu_buffer_rsrc_t rp, int
 // The products of one scale group, finished: y += scale * (the group's sum +
 // its -24 * sum of activations); lanes lr < 8 take A row 0 (k block 2s),
 // lanes lr >= 8 row 1 (k block 2s + 1).
-// (fp16: rows 0 and 1 are k block 2s's hi and lo parts, rows 2 and 3 k block
-// 2s + 1's)
+// (fp16: the same rows, fp16 products on q - 8 operands, bacc zero)
 template <bool F16>
 __device__ __forceinline__ void group_epilogue(float (&y)[4], const f32x4_t (&D)[4], uint2 s2, float bacc, int h) {
   const float sc[4] = {sc_lo<F16>(s2.x), sc_hi<F16>(s2.x), sc_lo<F16>(s2.y), sc_hi<F16>(s2.y)};
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float d = F16 ? (h ? D[i][2] + D[i][3] : D[i][0] + D[i][1]) : (h ? D[i][1] : D[i][0]);
-    y[i] += sc[i] * (d + bacc);
-  }
+  for (int i = 0; i < 4; ++i) y[i] += sc[i] * ((h ? D[i][1] : D[i][0]) + bacc);
 }
 
 template <int NS, int GSH, bool F16>
@@ -924,16 +928,17 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
   int* bad = &P.bad;
   if (tid < U * a.Gd * 4) L.dsc[tid] = r.sc;
   // the words as matrix-core operands, while the activations are on their way
-  const uint32_t mq = q4_magic();
+  // (fp16: exact fp16 q - 8, for fp16 products with no offset term)
+  const uint32_t mq = q4_magic_t<F16>();
   const uint32_t mc = q4_high_bits();
   uint4 B[NS][4];
 #pragma unroll
   for (int s = 0; s < NS; ++s) {
     const uint4 w = r.w[s];
-    B[s][0] = q4_operand_fast(w.x, mq, mc);
-    B[s][1] = q4_operand_fast(w.y, mq, mc);
-    B[s][2] = q4_operand_fast(w.z, mq, mc);
-    B[s][3] = q4_operand_fast(w.w, mq, mc);
+    B[s][0] = q4_operand_fast_t<F16>(w.x, mq, mc);
+    B[s][1] = q4_operand_fast_t<F16>(w.y, mq, mc);
+    B[s][2] = q4_operand_fast_t<F16>(w.z, mq, mc);
+    B[s][3] = q4_operand_fast_t<F16>(w.w, mq, mc);
     // here, not next to the products: the unpacking overlaps the wait
 #pragma unroll
     for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(B[s][i].x), "+v"(B[s][i].y), "+v"(B[s][i].z), "+v"(B[s][i].w));
@@ -957,19 +962,21 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
     // wave u waits for expert u's activations only (its products start as
     // soon as they are there), with each chunk's -24 * sum
     poll_chunks<2, F16>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps,
-                        F16 ? L.sact_lo + u * cps : nullptr, L.cbias + u * cps, cps, bad);
+                        L.cbias + u * cps, cps, bad);
     GI_STAMP(4);
     GI_STAMP_BY(20, (U - 1) * kWave);
     // lane l holds k block l's -24 * sum of the expert's activations (this
-    // wave's own LDS writes, read back in order)
-    const float* cb = L.cbias + u * cps + 4 * min(lane, Tk - 1);
-    const float kv = ((cb[0] + cb[1]) + cb[2]) + cb[3];
+    // wave's own LDS writes, read back in order; fp16: none)
+    float kv = 0.f;
+    if constexpr (!F16) {
+      const float* cb = L.cbias + u * cps + 4 * min(lane, Tk - 1);
+      kv = ((cb[0] + cb[1]) + cb[2]) + cb[3];
+    }
     // A rows 0, 1: k blocks 2s, 2s+1 (lanes lr < 2), read three steps ahead
-    // (fp16: rows 0-3 = k block 2s hi, lo, k block 2s+1 hi, lo; lanes lr < 4)
     const int rowoff = uc * cps + lq;
-    const int kbo = F16 ? ((lr >> 1) & 1) : (lr & 1);
-    const uint4* srow = (F16 && (lr & 1)) ? L.sact_lo : L.sact;
-    constexpr int kArows = F16 ? 4 : 2;
+    const int kbo = lr & 1;
+    const uint4* srow = L.sact;
+    constexpr int kArows = 2;
     constexpr int kAhead = 3;
     uint4 an[kAhead];
 #pragma unroll
@@ -989,10 +996,13 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
         s2c = *(const uint2*)((const uint16_t*)&L.dsc[(uc * a.Gd + gg) * 4] + 4 * (lr & 7));
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) Dc[i] = mfma_bf16(A, B[s][i], gstart ? zf : Dc[i]);
-      const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
-      const float b1 = 2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
-      bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
+      for (int i = 0; i < 4; ++i) Dc[i] = mfma_act<F16>(A, B[s][i], gstart ? zf : Dc[i]);
+      if constexpr (!F16) {
+        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
+        const float b1 =
+            2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
+        bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
+      }
       if (epi) group_epilogue<F16>(y, Dp, s2p, bp, h);
     };
 #pragma unroll
