@@ -173,7 +173,6 @@ struct ItemLds {
 template <bool F16>
 struct UnitLds {
   uint4 sact[kMaxU * kMaxTk * 4];   // activation chunks [u][I/8], plain bf16 or fp16 in matrix-core k order
-  float cbias[kMaxU * kMaxTk * 4];  // -24 * each chunk's sum (bf16; the fp16 products need none)
   uint4 dsc[kMaxU * kMaxGd * 4];    // down scales of the unit's columns [u][g][32]
   float4 red[kW][16];
 };
@@ -857,18 +856,20 @@ __device__ __forceinline__ void unit_load(const D1Args& a, const D1Pro& P, int d
 }
 
 // One wave polls the n chunks (16 bytes each, lane + 64j) of `src` into dst
-// (all of them present: no 16-bit half zero), inverted back, with each
-// chunk's -24 * sum of its 8 values into bias (bf16; the fp16 products on
-// q - 8 operands need none).  Bounded: on timeout the status word and host
+// (all of them present: no 16-bit half zero), inverted back, with chunk
+// lane + 64j's -24 * sum of its 8 values in bias[j] (bf16; the fp16 products
+// on q - 8 operands need none).  Bounded: on timeout the status word and host
 // flag are set, *bad is set and the wave goes on.
 template <int CPT, bool F16>
 __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buffer_rsrc_t src, uint4* dst,
-                                            float* bias, int n, int* bad) {
+                                            float (&bias)[CPT], int n, int* bad) {
   const int lane = threadIdx.x & (kWave - 1);
   uint32_t pending = 0u;
 #pragma unroll
-  for (int j = 0; j < CPT; ++j)
+  for (int j = 0; j < CPT; ++j) {
+    bias[j] = 0.f;
     if (lane + j * kWave < n) pending |= 1u << j;
+  }
   int spins = 0;
   while (true) {
     u32x4_t v[CPT];
@@ -881,7 +882,7 @@ __device__ __forceinline__ void poll_chunks(const D1Args& a, const __amdgpu_buff
       if (((pending >> j) & 1u) && chunk_ready(v[j])) {
         const uint4 x = make_uint4(~v[j].x, ~v[j].y, ~v[j].z, ~v[j].w);
         dst[lane + j * kWave] = x;
-        if constexpr (!F16) bias[lane + j * kWave] = q4_bias(x);
+        if constexpr (!F16) bias[j] = q4_bias(x);
         pending &= ~(1u << j);
       }
     }
@@ -961,16 +962,24 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
   if (u < U) {
     // wave u waits for expert u's activations only (its products start as
     // soon as they are there), with each chunk's -24 * sum
-    poll_chunks<2, F16>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps,
-                        L.cbias + u * cps, cps, bad);
+    float cb[2];
+    poll_chunks<2, F16>(a, buffer_rsrc(act + (size_t)u * a.I * 2, (uint32_t)(a.I * 2)), L.sact + u * cps, cb, cps,
+                        bad);
     GI_STAMP(4);
     GI_STAMP_BY(20, (U - 1) * kWave);
-    // lane l holds k block l's -24 * sum of the expert's activations (this
-    // wave's own LDS writes, read back in order; fp16: none)
-    float kv = 0.f;
+    // -24 * the sum of k block kb's activations: k block kb is chunks 4kb ..
+    // 4kb+3, held by lanes 4(kb % 16) .. +3 in cb[kb / 16]; summed over each
+    // quad of lanes in registers ((c0 + c1) + (c2 + c3) in every lane of it),
+    // read with readlane per step (fp16: none)
+    float kq[2] = {0.f, 0.f};
     if constexpr (!F16) {
-      const float* cb = L.cbias + u * cps + 4 * min(lane, Tk - 1);
-      kv = ((cb[0] + cb[1]) + cb[2]) + cb[3];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float v = cb[j] + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(cb[j]), 0xB1, 0xF, 0xF,
+                                                                            false));  // quad_perm [1,0,3,2]
+        kq[j] = v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF,
+                                                                false));  // quad_perm [2,3,0,1]
+      }
     }
     // A rows 0, 1: k blocks 2s, 2s+1 (lanes lr < 2), read three steps ahead
     const int rowoff = uc * cps + lq;
@@ -998,9 +1007,12 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
 #pragma unroll
       for (int i = 0; i < 4; ++i) Dc[i] = mfma_act<F16>(A, B[s][i], gstart ? zf : Dc[i]);
       if constexpr (!F16) {
-        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s));
+        // k blocks 2s and 2s + 1 (compile-time after unrolling; past Tk: zero)
+        const int k0 = 2 * s, k1 = 2 * s + 1;
+        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k0 >> 4) & 1]), 4 * (k0 & 15)));
         const float b1 =
-            2 * s + 1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kv), 2 * s + 1)) : 0.f;
+            k1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k1 >> 4) & 1]), 4 * (k1 & 15)))
+                    : 0.f;
         bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
       }
       if (epi) group_epilogue<F16>(y, Dp, s2p, bp, h);
