@@ -995,6 +995,20 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
     // epilogue does not wait for the matrix cores (the sets are named, not
     // indexed, so that they stay in registers when the group size is a
     // run-time value)
+    // each step's offset sum for this lane's k block (2s + h), read before the steps
+    float kb_off[NS];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      kb_off[s] = 0.f;
+      if constexpr (!F16) {
+        const int k0 = 2 * s, k1 = 2 * s + 1;
+        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k0 >> 4) & 1]), 4 * (k0 & 15)));
+        const float b1 =
+            k1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k1 >> 4) & 1]), 4 * (k1 & 15)))
+                    : 0.f;
+        kb_off[s] = h ? b1 : b0;
+      }
+    }
     f32x4_t D0[4], D1[4];
     uint2 s20 = make_uint2(0u, 0u), s21 = make_uint2(0u, 0u);
     float bacc0 = 0.f, bacc1 = 0.f;
@@ -1006,15 +1020,7 @@ __device__ __forceinline__ void unit_run(const D1Args& a, D1Pro& P, UnitLds<F16>
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) Dc[i] = mfma_act<F16>(A, B[s][i], gstart ? zf : Dc[i]);
-      if constexpr (!F16) {
-        // k blocks 2s and 2s + 1 (compile-time after unrolling; past Tk: zero)
-        const int k0 = 2 * s, k1 = 2 * s + 1;
-        const float b0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k0 >> 4) & 1]), 4 * (k0 & 15)));
-        const float b1 =
-            k1 < Tk ? __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kq[(k1 >> 4) & 1]), 4 * (k1 & 15)))
-                    : 0.f;
-        bc = (gstart ? 0.f : bc) + (h ? b1 : b0);
-      }
+      if constexpr (!F16) bc = (gstart ? 0.f : bc) + kb_off[s];
       if (epi) group_epilogue<F16>(y, Dp, s2p, bp, h);
     };
 #pragma unroll
