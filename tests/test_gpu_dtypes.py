@@ -177,6 +177,27 @@ def test_moe_fp16_eight_row_modes(h, i, e, gs, m):
     assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, "fp16"), "fp16", f"fp16 top-16 h={h} m={m}")
 
 
+@pytest.mark.parametrize("i,gs", [(704, 256), (768, 128), (768, 64)])
+def test_moe_fp16_one_token_other_variants(i, gs):
+    """The one-token kernel's fp16 variants with the group size read at run
+    time (group 256 at I = 704) and with 12 unit steps (I = 768), at H = 2816,
+    E = 32, top-8, from ids, against the oracle."""
+    dt, e = torch.float16, 32
+    W = _moe_weights(e, H, i, gs, seed=990 + i + gs, dt=dt)
+    Wd = {n: v.to(DEV) for n, v in W.items()}
+    x = synth.activations(1, H, seed=991).to(dt)
+    logits = synth.router_logits(1, e, seed=992)
+    top, idx = torch.topk(logits, 8, dim=-1)
+    w = torch.softmax(top, dim=-1, dtype=torch.float32).to(dt)
+    idx = idx.to(torch.int32)
+    out_in = (torch.randn(1, H, generator=torch.Generator().manual_seed(993)) * 0.1).to(dt)
+    out = out_in.to(DEV).clone()
+    gemmainfer_csrc.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                                      Wd["down_scales"], idx.to(DEV), w.to(DEV), out, gs)
+    torch.cuda.synchronize()
+    assert_dtype_close(out, _oracle(W, x, idx, w, out_in, gs, "fp16"), "fp16", f"fp16 one-token I={i} gs={gs}")
+
+
 @pytest.mark.parametrize("m", [7, 12])
 def test_moe_fp16_deterministic_and_multi_launch(m):
     """fp16 on the 8-row kernel: one launch (m=7) and two launches of 8 and 4
