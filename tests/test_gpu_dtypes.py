@@ -67,8 +67,9 @@ def test_moe_gemma_shape(gemma, m, noise):
 
 @pytest.mark.parametrize("gs", [64, 128])
 def test_moe_fp16_one_token_edge_cases(gs):
-    """fp16 at one token runs the one-token kernel's fp16 variant (each fp16
-    value split exactly into bf16 hi + lo operand rows): ids outside [0, E)
+    """fp16 at one token runs the one-token kernel's fp16 variant (its items
+    split each fp16 value of x exactly into bf16 hi + lo operand rows, its
+    units take fp16 products on exact q - 8 operands): ids outside [0, E)
     skipped (marlin.cu:304, :473), one expert in several slots with different
     weights, int64 ids and fp32 weights cast to fp16 (marlin.cu:631-636),
     activations spread over fp16's whole range (every significand bit and
@@ -152,15 +153,15 @@ def test_moe_fp16_rows_edge_cases(gs, m):
     assert torch.equal(out, out_in)
 
 
-@pytest.mark.parametrize("h,i,e,gs", [(256, 128, 32, 64), (2816, 704, 128, 128)])
+@pytest.mark.parametrize("h,i,e,gs", [(256, 128, 32, 64), (2816, 704, 128, 128), (2816, 704, 32, 256)])
 @pytest.mark.parametrize("m", [1, 2, 4])
 def test_moe_fp16_eight_row_modes(h, i, e, gs, m):
     """top_k = 16, more experts per token than the one-token kernel holds:
     every call of 1-4 rows is one launch of the 8-row kernel's fp16 variant,
     in its one-row (m=1) and two-row (m=2) dot-product modes and its
     matrix-core mode (m=4), at a hidden size of at most 512 and at the Gemma
-    size; an id outside [0, E) and a repeated expert in a token
-    (marlin.cu:304, :473)."""
+    size (group size 256: the scale groups read at run time); an id outside
+    [0, E) and a repeated expert in a token (marlin.cu:304, :473)."""
     dt, k = torch.float16, 16
     W = _moe_weights(e, h, i, gs, seed=950 + m, dt=dt)
     Wd = {n: v.to(DEV) for n, v in W.items()}
