@@ -81,7 +81,9 @@ int launch_fused_moe_static(MoeHostArgs h);
 constexpr int kPrefillMinRows = 64;
 bool moe_prefill_supported(const MoeHostArgs& h);
 size_t moe_prefill_workspace_bytes(int M, int top_k, int H, int I, int E);
-int launch_moe_prefill(const MoeHostArgs& h, void* ws, size_t ws_bytes);
+// arrive: a counter word of the workspace that is zero between launches (the
+// prefill's front launch counts its routing workgroups there)
+int launch_moe_prefill(const MoeHostArgs& h, void* ws, size_t ws_bytes, int* arrive);
 int launch_moe_align(const void* idx, int is64, int M, int top_k, int E, int32_t* uniq,
                      int32_t* nuniq, int32_t* s2u, int32_t* offsets, int32_t* slots,
                      hipStream_t stream);

@@ -53,6 +53,7 @@ constexpr int kMaxExperts = 1024;
 constexpr int kMaxWaves = 16;
 constexpr int kDefaultSpin = 1 << 22;
 constexpr int kCtrStride = 32;     // ints between counters (128 bytes: separate lines)
+constexpr int kCtrSlots = 5;       // counter words (the last one: prefill arrivals)
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef const __attribute__((address_space(1))) void* gbl_ptr_t;
@@ -74,6 +75,7 @@ struct Args {
   uint32_t part_bytes;
   int* ctr;         // grid barrier: [0] launch epoch, [(1 + p) * kCtrStride] arrivals of parity p,
                     // [3 * kCtrStride] the last epoch whose barrier wait timed out
+                    // ([4 * kCtrStride]: the prefill front launch's arrivals)
   int* status;
   int* host_flag;   // host-visible error flag of the device (may be null)
   int idx_is64, w_dtype, logits_dtype;
@@ -980,7 +982,7 @@ WsLayout ws_layout(int S, int H, int I, int cg) {
   L.status = 0;
   L.state = kAlign;
   L.ctr = L.state + round_up(moe_decode_state_bytes());
-  L.part = L.ctr + round_up((size_t)4 * kCtrStride * sizeof(int));
+  L.part = L.ctr + round_up((size_t)kCtrSlots * kCtrStride * sizeof(int));
   L.total = round_up(L.part + (size_t)S * tiles_per_expert(I, cg) * H * sizeof(float));
   return L;
 }
@@ -1182,7 +1184,9 @@ int launch_fused_moe(const MoeHostArgs& h) {
   }
   if (moe_prefill_supported(h)) {
     const size_t base = prefill_base(h.H, h.I);
-    return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base);
+    const WsLayout L = ws_layout(1, h.H, h.I, kTaskCols);
+    return launch_moe_prefill(h, (char*)h.workspace + base, h.workspace_bytes - base,
+                              (int*)((char*)h.workspace + L.ctr) + 4 * kCtrStride);
   }
   if (moe_decode1_supported(h) || moe_decode_supported(h)) {
     // the same layout as the size query (gi_fused_moe_workspace_bytes)

@@ -8,18 +8,21 @@
 // rows).  Here every (token, slot) pair is grouped by expert once and each
 // active expert's weights stream through the GPU once:
 //
-//   align    one workgroup: per-expert counts, offsets, the pairs of each
-//            expert (pos -> pair) and the inverse map (pair -> pos); the
-//            routing weights rounded to bf16 (marlin.cu:631-636)
-//   gate/up  grid (I/32 column tiles, E): 16-token row tiles of the expert's
+//   front    one launch: routing (layer mode, 16 tokens per workgroup); the
+//            align in the last routing workgroup to finish (per-expert
+//            counts, offsets, the pairs of each expert (pos -> pair) and the
+//            inverse map (pair -> pos)); beside them the reorder of x into the
+//            matrix-core k order
+//   gate/up  grid (I/128 column tiles, E): 16-token row tiles of the expert's
 //            pairs (A = gathered x rows) times the unpacked int4 words (B),
-//            v_mfma_f32_16x16x32_bf16; k split over the 8 waves, summed in
-//            wave order; act = bf16(gelu_tanh(gate) * up) (marlin.cu:414-423)
-//   down     grid (H/64 column units, E): the same over the act rows, fp32
+//            v_mfma_f32_16x16x32_bf16, 48 pairs per pass; act =
+//            bf16(gelu_tanh(gate) * up) (marlin.cu:414-423)
+//   down     grid (H/256 column units, E): the same over the act rows, fp32
 //            results per pair
 //   combine  one workgroup per token: out[t] (+)= sum over its slots in slot
-//            order of w * y, one bf16 rounding (the reference adds bf16
-//            atomics, marlin.cu:583; the order here is fixed)
+//            order of w * y, the weights rounded to bf16 (marlin.cu:631-636),
+//            one bf16 rounding of the sum (the reference adds bf16 atomics,
+//            marlin.cu:583; the order here is fixed)
 //
 // The int4 words enter the products as bf16 16 + q (byte permutes) with one
 // more product against a constant -24 operand per 32-k block for the offset,
@@ -49,7 +52,7 @@ struct PfArgs {
   const uint16_t* gus;
   const int32_t* dn;
   const uint16_t* dns;
-  const int* offsets;  // [E + 1]
+  const int* offsets;  // [E + 1] first position of each expert
   const int* order;    // [P] pair at each position
   uint16_t* act;       // [P][I] bf16, positions in expert order, chunks in k order
   float* y;            // [P][H] fp32
@@ -57,65 +60,75 @@ struct PfArgs {
   uint32_t x_bytes, gu_bytes, gu_total, dn_bytes, dn_total, act_bytes;
 };
 
+// Router inputs of the front launch (the fields the shared routing reads).
+struct PfRoute {
+  const void* logits;
+  int logits_dtype;
+  const float* expert_scale;
+  int M, E, top_k;
+};
+
 // ---------------------------------------------------------------------------
-// align
+// align (one workgroup of kAlignThreads)
 // ---------------------------------------------------------------------------
 constexpr int kAlignPer = 8;  // pairs per thread kept in registers
 
-__global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
-    const void* idx, int idx_is64, const void* w, int w_dtype, int P, int E, int* offsets, int* order,
-    int* posmap, float* wts) {
-  __shared__ int cnt[1024];
-  __shared__ int fill[1024];
-  __shared__ int wsum[kAlignThreads / kWave];
+// Per-expert offsets [E + 1], the pairs of each expert (order: pos -> pair)
+// and the inverse map (posmap: pair -> pos, -1 for an id outside [0, E),
+// skipped as at marlin.cu:288-289); load_id(p) reads pair p's id.
+struct AlignLds {
+  int cnt[1024];
+  int fill[1024];
+  int wsum[kAlignThreads / kWave];
+};
+template <class LoadId>
+__device__ __forceinline__ void align_block(LoadId load_id, int P, int E, int* offsets, int* order, int* posmap,
+                                            AlignLds& s) {
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += kAlignThreads) {
-    cnt[e] = 0;
-    fill[e] = 0;
+    s.cnt[e] = 0;
+    s.fill[e] = 0;
   }
   __syncthreads();
-  // Up to kAlignPer pairs per thread: every id and weight is loaded once, up
-  // front (indices clamped to the last pair, so no load sits under a per-lane
+  // Up to kAlignPer pairs per thread: every id is loaded once, up front
+  // (indices clamped to the last pair, so no load sits under a per-lane
   // condition), and both passes below reuse the registers.
   const bool cached = P > 0 && P <= kAlignThreads * kAlignPer;
   int ev[kAlignPer];
-  float wv[kAlignPer];
   if (cached) {
 #pragma unroll
     for (int i = 0; i < kAlignPer; ++i) {
       const int p = tid + kAlignThreads * i;
-      const int pc = p < P ? p : P - 1;
-      ev[i] = load_expert_id(idx, idx_is64, pc);
-      wv[i] = load_weight_as_bf16(w, w_dtype, pc);
+      ev[i] = load_id(p < P ? p : P - 1);
       if (p >= P) ev[i] = -1;
     }
 #pragma unroll
     for (int i = 0; i < kAlignPer; ++i)
-      if (ev[i] >= 0 && ev[i] < E) atomicAdd(&cnt[ev[i]], 1);
+      if (ev[i] >= 0 && ev[i] < E) atomicAdd(&s.cnt[ev[i]], 1);
   } else {
     for (int p = tid; p < P; p += kAlignThreads) {
-      const int e = load_expert_id(idx, idx_is64, p);
-      if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+      const int e = load_id(p);
+      if (e >= 0 && e < E) atomicAdd(&s.cnt[e], 1);
     }
   }
   __syncthreads();
   // exclusive scan of the counts (E <= 1024: one expert per thread)
   const int lane = tid & (kWave - 1), wave = tid >> 6;
-  const int c = tid < E ? cnt[tid] : 0;
+  const int c = tid < E ? s.cnt[tid] : 0;
   int incl = c;
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) {
     const int v = __shfl_up(incl, off, kWave);
     if (lane >= off) incl += v;
   }
-  if (lane == kWave - 1) wsum[wave] = incl;
+  if (lane == kWave - 1) s.wsum[wave] = incl;
   __syncthreads();
   int base = 0;
-  for (int w2 = 0; w2 < wave; ++w2) base += wsum[w2];
+  for (int w2 = 0; w2 < wave; ++w2) base += s.wsum[w2];
   const int excl = base + incl - c;
   if (tid < E) {
     offsets[tid] = excl;
-    cnt[tid] = excl;
+    s.cnt[tid] = excl;
   }
   if (tid == E - 1) offsets[E] = excl + c;
   __syncthreads();
@@ -127,32 +140,88 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_align_kernel(
         const int e = ev[i];
         int pos = -1;
         if (e >= 0 && e < E) {
-          pos = cnt[e] + atomicAdd(&fill[e], 1);
+          pos = s.cnt[e] + atomicAdd(&s.fill[e], 1);
           order[pos] = p;
         }
         posmap[p] = pos;
-        wts[p] = wv[i];
       }
     }
     return;
   }
   for (int p = tid; p < P; p += kAlignThreads) {
-    const int e = load_expert_id(idx, idx_is64, p);
+    const int e = load_id(p);
     int pos = -1;
     if (e >= 0 && e < E) {
-      pos = cnt[e] + atomicAdd(&fill[e], 1);
+      pos = s.cnt[e] + atomicAdd(&s.fill[e], 1);
       order[pos] = p;
     }
     posmap[p] = pos;
-    wts[p] = load_weight_as_bf16(w, w_dtype, p);
   }
 }
 
-// x rows with every 8-value chunk in the matrix-core k order (one pass over x
-// instead of a reorder per product operand).
-__global__ __launch_bounds__(256) void prefill_xperm_kernel(const uint4* x, uint4* xk, int n) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < n) xk[i] = moe::mfma_k_order(x[i]);
+// ---------------------------------------------------------------------------
+// front launch: routing, align and the x reorder in one launch
+// ---------------------------------------------------------------------------
+struct PfFront {
+  PfRoute r;
+  int nroute;            // routing workgroups (0: the caller gave the ids)
+  int32_t* out_idx;      // routed ids (int32)
+  uint16_t* out_w;       // routed weights (bf16, marlin.cu:631-636)
+  const void* idx;       // the ids the align reads (the routed ones, or the caller's)
+  int idx_is64, P;
+  int* offsets;          // [E + 1]
+  int* order;            // [P]
+  int* posmap;           // [P]
+  int* arrive;           // arrivals of the routing workgroups (zero between launches)
+  const uint4* x;
+  uint4* xk;             // x with each 8-value chunk in the matrix-core k order
+  int nx;                // 16-byte chunks of x
+};
+
+// Workgroups [0, nroute) route 16 tokens each (one wave per token) and the
+// last of them to finish runs the align over every routed id; with the ids
+// from the caller, workgroup 0 runs the align.  The other workgroups reorder
+// x (one pass instead of a reorder per product operand), one 16-byte chunk
+// per thread, beside them.  The routed ids are handed to the aligning
+// workgroup through the device coherence point: agent-scope stores, each
+// wave's stores complete before the workgroup barrier and the arrival, and
+// agent-scope loads after it.
+__global__ __launch_bounds__(kAlignThreads) void prefill_front_kernel(PfFront f) {
+  __shared__ AlignLds als;
+  __shared__ int r_idx[kAlignThreads / kWave][64];
+  __shared__ float r_w[kAlignThreads / kWave][64];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
+  const int nlead = f.nroute > 0 ? f.nroute : 1;
+  if ((int)blockIdx.x >= nlead) {
+    const int i = (blockIdx.x - nlead) * kAlignThreads + tid;
+    if (i < f.nx) f.xk[i] = moe::mfma_k_order(f.x[i]);
+    return;
+  }
+  const int E = f.r.E;
+  if (f.nroute == 0) {
+    align_block([&](int p) { return load_expert_id(f.idx, f.idx_is64, p); }, f.P, E, f.offsets, f.order, f.posmap,
+                als);
+    return;
+  }
+  const int t = blockIdx.x * (kAlignThreads / kWave) + wave;
+  if (t < f.r.M) {
+    moe::route_token_any(f.r, t, lane, r_idx[wave], r_w[wave]);
+    if (lane < f.r.top_k) {
+      const int s = t * f.r.top_k + lane;
+      __hip_atomic_store(f.out_idx + s, r_idx[wave][lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      f.out_w[s] = f32_to_bf16(r_w[wave][lane]);
+    }
+  }
+  wait_vmem();
+  __syncthreads();
+  if (tid == 0) last = atomic_add_relaxed(f.arrive, 1) == f.nroute - 1;
+  __syncthreads();
+  if (!last) return;
+  if (tid == 0) store_relaxed(f.arrive, 0);  // every routing workgroup has arrived: zero for the next launch
+  const int32_t* ids = f.out_idx;
+  align_block([&](int p) { return __hip_atomic_load(ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }, f.P, E,
+              f.offsets, f.order, f.posmap, als);
 }
 
 // ---------------------------------------------------------------------------
@@ -296,6 +365,52 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
   }
 }
 
+// A workgroup's scale table in LDS: entry i (group i >> 6, column quad
+// i & 63, whose first column is col_of(quad)) holds the quad's 4 scales of
+// the group, from one expert's [G][N] table.  Loads go out kScB per thread
+// before any LDS write (one memory round trip per 2048 entries instead of one
+// per 256); quads past N read zeros without a memory access.  The first batch
+// is issued on its own (issue(0), before the workgroup's other start-up
+// loads); store() writes it and stages the rest, if any.
+constexpr int kScB = 8;
+template <class ColOf>
+struct ScaleStage {
+  __amdgpu_buffer_rsrc_t r;
+  int n, N;
+  ColOf col_of;
+  u32x2_t v[kScB];
+  __device__ __forceinline__ ScaleStage(const uint16_t* sc_e, int G, int N_, ColOf c)
+      : r(buffer_rsrc(sc_e, (uint32_t)G * (uint32_t)N_ * 2u)), n(G * 64), N(N_), col_of(c) {}
+  __device__ __forceinline__ void issue(int b) {
+#pragma unroll
+    for (int j = 0; j < kScB; ++j) {
+      const int i = b + j * kPThreads + (int)threadIdx.x;
+      const int col = col_of(i & 63);
+      const uint32_t off = i < n && col + 4 <= N ? ((uint32_t)(i >> 6) * (uint32_t)N + (uint32_t)col) * 2u : kOob;
+      v[j] = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    }
+  }
+  __device__ __forceinline__ void write(int b, uint2* lds) const {
+#pragma unroll
+    for (int j = 0; j < kScB; ++j) {
+      const int i = b + j * kPThreads + (int)threadIdx.x;
+      if (i < n) lds[i] = make_uint2(v[j].x, v[j].y);
+    }
+  }
+  __device__ __forceinline__ void store(uint2* lds) {
+    write(0, lds);
+    for (int b = kPThreads * kScB; b < n; b += kPThreads * kScB) {
+      issue(b);
+      write(b, lds);
+    }
+  }
+};
+template <class ColOf>
+__device__ __forceinline__ ScaleStage<ColOf> scale_stage(const uint16_t* sc_e, int G, int N, ColOf c) {
+  return ScaleStage<ColOf>(sc_e, G, N, c);
+}
+
+
 // gate/up: workgroup (tile t, expert e) owns gate columns [128t, 128t+128)
 // (waves 0, 1) and the same up columns (waves 2, 3); act = bf16(gelu(g)*u).
 template <int GSH>
@@ -306,16 +421,14 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const int tile = blockIdx.x, e = blockIdx.y;
-  const int off_e = a.offsets[e], n_e = a.offsets[e + 1] - off_e;
-  if (n_e <= 0) return;
   const int twoI = 2 * a.I;
   // column of quad c (0..63) of this workgroup: waves 0-1 gate, 2-3 up
   auto quad_col = [&](int c) { return (c < 32 ? 0 : a.I) + 128 * tile + 4 * (c & 31); };
-  for (int i = tid; i < a.Ggu * 64; i += kPThreads) {
-    const int g = i >> 6, c = i & 63;
-    const int col = quad_col(c);
-    gsc[i] = col + 4 <= twoI ? *(const uint2*)(a.gus + ((size_t)e * a.Ggu + g) * twoI + col) : make_uint2(0u, 0u);
-  }
+  const int off_e = a.offsets[e], n_e = a.offsets[e + 1] - off_e;
+  if (n_e <= 0) return;
+  auto scales = scale_stage(a.gus + (size_t)e * a.Ggu * twoI, a.Ggu, twoI, quad_col);
+  scales.issue(0);
+  scales.store(gsc);
   __syncthreads();
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(a.gu, a.gu_total);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.xk, a.x_bytes);
@@ -361,11 +474,9 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
   const int unit = blockIdx.x, e = blockIdx.y;
   const int off_e = a.offsets[e], n_e = a.offsets[e + 1] - off_e;
   if (n_e <= 0) return;
-  for (int i = tid; i < a.Gd * 64; i += kPThreads) {
-    const int g = i >> 6, c = i & 63;
-    const int col = 256 * unit + 4 * c;
-    dsc[i] = col + 4 <= a.H ? *(const uint2*)(a.dns + ((size_t)e * a.Gd + g) * a.H + col) : make_uint2(0u, 0u);
-  }
+  auto scales = scale_stage(a.dns + (size_t)e * a.Gd * a.H, a.Gd, a.H, [unit](int c) { return 256 * unit + 4 * c; });
+  scales.issue(0);
+  scales.store(dsc);
   __syncthreads();
   const int col = 256 * unit + 64 * wave + 4 * lr;
   const bool live = 256 * unit + 64 * wave < a.H;  // a partial last unit: the wave still joins the barriers
@@ -394,8 +505,22 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
 // ---------------------------------------------------------------------------
 // combine: out[t] (+)= sum over slots, in slot order, of w * y[pos]
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, const int* posmap, const float* wts,
-                                                              uint16_t* out, int H, int top_k, int overwrite) {
+// A pair's routing as the combine reads it: the position of its result row
+// (-1: its id is outside [0, E), skipped as at marlin.cu:288-289) and its
+// weight rounded to bf16 (marlin.cu:631-636), read from the caller's (or the
+// routed) weights.
+struct PfSlots {
+  const int* posmap;
+  const void* w;
+  int w_dtype;
+};
+__device__ __forceinline__ void slot_of(const PfSlots& s, int p, int& pos, float& wv) {
+  pos = s.posmap[p];
+  wv = load_weight_as_bf16(s.w, s.w_dtype, p);
+}
+
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, PfSlots sl, uint16_t* out, int H,
+                                                              int top_k, int overwrite) {
   const int t = blockIdx.x;
   for (int c = threadIdx.x * 4; c < H; c += 256 * 4) {
     float4 s = overwrite ? make_float4(0.f, 0.f, 0.f, 0.f)
@@ -403,10 +528,10 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, co
                                        bf16_to_f32(out[(size_t)t * H + c + 2]), bf16_to_f32(out[(size_t)t * H + c + 3]));
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < top_k; ++k) {
-      const int p = t * top_k + k;
-      const int pos = posmap[p];
+      int pos;
+      float wv;
+      slot_of(sl, t * top_k + k, pos, wv);
       if (pos < 0) continue;
-      const float wv = wts[p];
       const float4 v = *(const float4*)(y + (size_t)pos * H + c);
       acc.x += wv * v.x;
       acc.y += wv * v.y;
@@ -430,15 +555,17 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, co
 // chunk).  Same arithmetic and order as prefill_combine_kernel.
 constexpr int kCombineSlots = 8;
 constexpr int kCombineChunks = 3;
-__global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, const int* posmap, const float* wts,
-                                                               uint16_t* out, int H, int top_k, int overwrite) {
+__global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, PfSlots sl, uint16_t* out, int H,
+                                                               int top_k, int overwrite) {
   const int t = blockIdx.x;
   __shared__ int spos[kCombineSlots];
   __shared__ float swt[kCombineSlots];
   if (threadIdx.x < kCombineSlots) {
-    const bool ok = (int)threadIdx.x < top_k;
-    spos[threadIdx.x] = ok ? posmap[(size_t)t * top_k + threadIdx.x] : -1;
-    swt[threadIdx.x] = ok ? wts[(size_t)t * top_k + threadIdx.x] : 0.f;
+    int pos = -1;
+    float wv = 0.f;
+    if ((int)threadIdx.x < top_k) slot_of(sl, t * top_k + threadIdx.x, pos, wv);
+    spos[threadIdx.x] = pos;
+    swt[threadIdx.x] = wv;
   }
   __syncthreads();
   int pos[kCombineSlots];
@@ -498,7 +625,7 @@ constexpr size_t kPAlign = 256;
 inline size_t pround(size_t v) { return (v + kPAlign - 1) / kPAlign * kPAlign; }
 
 struct PfLayout {
-  size_t idx, w, offsets, order, posmap, wts, xk, act, y, total;
+  size_t idx, w, offsets, order, posmap, xk, act, y, total;
 };
 PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   const size_t P = (size_t)M * top_k;
@@ -508,8 +635,7 @@ PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   l.offsets = pround(l.w + P * 2);
   l.order = pround(l.offsets + (size_t)(E + 1) * 4);
   l.posmap = pround(l.order + P * 4);
-  l.wts = pround(l.posmap + P * 4);
-  l.xk = pround(l.wts + P * 4);
+  l.xk = pround(l.posmap + P * 4);
   l.act = pround(l.xk + (size_t)M * H * 2);
   l.y = pround(l.act + P * I * 2);
   l.total = pround(l.y + P * H * 4);
@@ -547,36 +673,55 @@ size_t moe_prefill_workspace_bytes(int M, int top_k, int H, int I, int E) {
   return pf_layout(M, top_k, H, I, E).total;
 }
 
-int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
+int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes, int* arrive) {
   const PfLayout L = pf_layout(h.M, h.top_k, h.H, h.I, h.E);
   if (!workspace || ws_bytes < L.total)
     return fail(GI_ERR_WORKSPACE, "fused MoE: workspace missing or smaller than gi_fused_moe_workspace_bytes()");
   char* ws = (char*)workspace;
   const int P = h.M * h.top_k;
-  const void* idx = h.idx;
-  int idx_is64 = h.idx_is64;
+  PfFront f{};
+  f.idx = h.idx;
+  f.idx_is64 = h.idx_is64;
   const void* w = h.w;
   int w_dtype = h.w_dtype;
   if (h.logits) {
     // routing into the caller's report buffers when given, else the workspace
-    int32_t* ridx = h.out_idx ? h.out_idx : (int32_t*)(ws + L.idx);
-    void* rw = h.out_w ? h.out_w : (void*)(ws + L.w);
-    const int st = launch_route(h.logits, h.logits_dtype, h.expert_scale, h.M, h.E, h.top_k, ridx, rw,
-                                GI_DTYPE_BF16, h.stream);
-    if (st != GI_OK) return st;
-    idx = ridx;
-    idx_is64 = 0;
-    w = rw;
+    // (the checks of the router-only entry point)
+    if (h.E > moe::kRouteMaxExperts || h.top_k > h.E || h.top_k > 64)
+      return fail(GI_ERR_UNSUPPORTED, "route: at most 1024 experts and top_k <= min(E, 64)");
+    if (h.logits_dtype != GI_DTYPE_BF16 && h.logits_dtype != GI_DTYPE_FP32)
+      return fail(GI_ERR_UNSUPPORTED, "route: logits must be bf16 or fp32");
+    f.out_idx = h.out_idx ? h.out_idx : (int32_t*)(ws + L.idx);
+    f.out_w = h.out_w ? (uint16_t*)h.out_w : (uint16_t*)(ws + L.w);
+    f.r.logits = h.logits;
+    f.r.logits_dtype = h.logits_dtype;
+    f.r.expert_scale = h.expert_scale;
+    f.nroute = (h.M + kAlignThreads / kWave - 1) / (kAlignThreads / kWave);
+    f.idx = f.out_idx;
+    f.idx_is64 = 0;
+    w = f.out_w;
     w_dtype = GI_DTYPE_BF16;
   }
+  f.r.M = h.M;
+  f.r.E = h.E;
+  f.r.top_k = h.top_k;
+  f.P = P;
   int* offsets = (int*)(ws + L.offsets);
   int* order = (int*)(ws + L.order);
   int* posmap = (int*)(ws + L.posmap);
-  float* wts = (float*)(ws + L.wts);
-  hipLaunchKernelGGL(prefill_align_kernel, dim3(1), dim3(kAlignThreads), 0, h.stream, idx, idx_is64, w, w_dtype,
-                     P, h.E, offsets, order, posmap, wts);
+  f.offsets = offsets;
+  f.order = order;
+  f.posmap = posmap;
+  f.arrive = arrive;
+  f.x = (const uint4*)h.x;
+  f.xk = (uint4*)(ws + L.xk);
+  f.nx = h.M * h.H / 8;
+  // one launch: routing (or the caller's ids), the align, the x reorder
+  const int nlead = f.nroute > 0 ? f.nroute : 1;
+  hipLaunchKernelGGL(prefill_front_kernel, dim3(nlead + (f.nx + kAlignThreads - 1) / kAlignThreads),
+                     dim3(kAlignThreads), 0, h.stream, f);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "prefill align launch");
+  if (e != hipSuccess) return hip_fail(e, "prefill routing / align / x reorder launch");
 
   PfArgs k{};
   k.x = (const uint16_t*)h.x;
@@ -603,11 +748,6 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   k.dn_bytes = (uint32_t)((size_t)(h.I / 8) * h.H * 4);
   k.dn_total = (uint32_t)((size_t)h.E * k.dn_bytes);
   k.act_bytes = (uint32_t)((size_t)P * h.I * 2);
-  const int nx = h.M * h.H / 8;
-  hipLaunchKernelGGL(prefill_xperm_kernel, dim3((nx + 255) / 256), dim3(256), 0, h.stream, (const uint4*)h.x,
-                     (uint4*)k.xk, nx);
-  e = hipGetLastError();
-  if (e != hipSuccess) return hip_fail(e, "prefill x reorder launch");
   const size_t gl = (size_t)h.Ggu * 64 * sizeof(uint2), dl = (size_t)h.Gd * 64 * sizeof(uint2);
   const dim3 ggrid((h.I + 127) / 128, h.E), dgrid((h.H + 255) / 256, h.E);
   switch (k.gsh) {
@@ -626,12 +766,13 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes) {
   }
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill down launch");
+  const PfSlots sl{posmap, w, w_dtype};
   if (h.top_k <= kCombineSlots)
-    hipLaunchKernelGGL(prefill_combine8_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
-                       (uint16_t*)h.out, h.H, h.top_k, h.overwrite);
+    hipLaunchKernelGGL(prefill_combine8_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, sl, (uint16_t*)h.out, h.H,
+                       h.top_k, h.overwrite);
   else
-    hipLaunchKernelGGL(prefill_combine_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, posmap, wts,
-                       (uint16_t*)h.out, h.H, h.top_k, h.overwrite);
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, sl, (uint16_t*)h.out, h.H,
+                       h.top_k, h.overwrite);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill combine launch");
   return GI_OK;

@@ -216,6 +216,38 @@ def test_prefill_duplicates_invalid_skewed(small):
     assert_bf16_close(out, ref, "prefill duplicates/invalid")
 
 
+@pytest.mark.parametrize("m,top_k,idx_dtype", [(1024, 8, torch.int32), (1025, 8, torch.int64),
+                                               (1100, 4, torch.int32), (64, 1, torch.int64)])
+def test_prefill_many_pairs_and_heavy_expert(small, m, top_k, idx_dtype):
+    """The front launch's align sorts up to 8192 (token, slot) pairs from
+    registers (1024 x 8 is the largest such call, 64 x 1 the smallest prefill
+    call) and more in a loop (1025 x 8).  Eight experts take ~500-1000 pairs
+    each, i.e. 11-22 passes of 48 pairs per workgroup, and one expert takes
+    most of them; ids outside [0, E) are skipped, duplicate ids within a
+    token each count, and the output is the same on a second call."""
+    W, Wd = small
+    g = torch.Generator().manual_seed(m + top_k)
+    idx = torch.randint(0, 8, (m, top_k), generator=g, dtype=torch.int64)
+    idx[::2, 0] = 3                        # expert 3: > 512 pairs
+    if top_k > 1:
+        idx[1::5, 1] = idx[1::5, 0]        # duplicates within a token
+        idx[3::17, 1] = 8                  # id == E: skipped
+    idx[7::23, 0] = -1                     # skipped slots
+    w = torch.rand(m, top_k, generator=g).to(torch.bfloat16)
+    x = synth.activations(m, 256, seed=m)
+    out_in = (torch.randn(m, 256, generator=g) * 0.1).to(torch.bfloat16)
+    print(f"prefill modes m={m} top_k={top_k} {idx_dtype}", flush=True)
+    out = out_in.to(DEV).clone()
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(idx_dtype).to(DEV), w.to(DEV), out, 64)
+    ref, _ = _oracle_moe(x, W, idx, w, out_in, 64)
+    assert_bf16_close(out, ref, f"prefill modes m={m} top_k={top_k}")
+    out2 = out_in.to(DEV).clone()
+    ops.fused_batched_moe(x.to(DEV), Wd["gate_up_packed"], Wd["gate_up_scales"], Wd["down_packed"],
+                          Wd["down_scales"], idx.to(idx_dtype).to(DEV), w.to(DEV), out2, 64)
+    assert torch.equal(out, out2)
+
+
 @pytest.mark.parametrize("H,I,gs", [(320, 96, 64), (320, 96, 128), (256, 96, 128), (320, 128, 128),
                                      (2816, 704, 256)])
 def test_prefill_partial_last_scale_group(H, I, gs):
@@ -257,13 +289,15 @@ def test_prefill_scale_table_at_lds_limit(I):
     assert_bf16_close(out, ref, f"prefill I={I} gs32")
 
 
-def test_prefill_layer_matches_oracle_and_is_deterministic(gemma128):
+@pytest.mark.parametrize("m", [100, 512])
+def test_prefill_layer_matches_oracle_and_is_deterministic(gemma128, m):
     """Layer mode through the prefill path: routing bit-exact, output within
-    tolerance, and bitwise-identical across calls."""
+    tolerance, and bitwise-identical across calls.  The routed ids reach the
+    align from 7 (m = 100) or 32 (m = 512) routing workgroups of the same
+    launch."""
     W, Wd = gemma128
-    m = 100
-    x = synth.activations(m, 2816, seed=77)
-    logits = synth.router_logits(m, 128, seed=77)
+    x = synth.activations(m, 2816, seed=77 + m)
+    logits = synth.router_logits(m, 128, seed=77 + m)
     outs = []
     for _ in range(2):
         out, idx, w = ops.moe_layer(x.to(DEV), logits.to(DEV), Wd["gate_up_packed"],
