@@ -620,8 +620,8 @@ def bench_prefill(steps, warmup, device):
         "dtype": "bf16",
         "data": "synthetic (N(0,1) bf16 activations, i.i.d. N(0,1) fp32 router logits, uniform int4 codes, "
                 "|N(0,1)|*0.02 bf16 scales)",
-        "config": {"workload": "MoE layer from logits at M=512: route, align, grouped gate_up, grouped down, "
-                               "combine (5 launches)", "M": m, "hidden": H, "experts": E, "top_k": TOP_K,
+        "config": {"workload": "MoE layer from logits at M=512: route + align + x reorder, grouped gate_up, "
+                               "grouped down, combine (4 launches)", "M": m, "hidden": H, "experts": E, "top_k": TOP_K,
                    "moe_intermediate": I, "group_size": GS, "weight_copies_rotated": COPIES,
                    "timing": "HIP graph of K steps, HIP events"},
         "unique_experts_mean": mean_u,
