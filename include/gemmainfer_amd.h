@@ -120,8 +120,9 @@ int gi_moe_align(const void* idx, int idx_dtype, int M, int top_k, int E,
  * of up to 64 slots, top_k <= 64: alignment, gate/up, down, combine).
  * One kernel launch per 256/top_k rows (8 rows on the decode kernel); from
  * 64 rows with top_k <= 64, a power-of-two multiple of 32 as group size,
- * H % 64 == 0 and I % 32 == 0, the grouped-GEMM prefill path (align,
- * gate/up, down, combine launches; each active expert read once).
+ * H % 64 == 0 and I % 32 == 0, the grouped-GEMM prefill path (align with
+ * the x reorder, gate/up, down, combine launches; each active expert read
+ * once).
  * Requirements: H % 8 == 0,
  * I % 8 == 0, H, I multiples of 4 columns, group_size % 8 == 0, E <= 1024,
  * top_k <= 256.  Deterministic (fixed-order fp32 reductions, no float
@@ -180,8 +181,8 @@ int gi_fused_batched_moe_static_status(int32_t* host_status, int clear, void* st
  * OVERWRITTEN with the MoE output, and out_idx/out_w (may be NULL) receive
  * the routing.  Up to 8 rows per launch; from 64 rows (group size a power of
  * two times 32, H % 64 == 0, I % 32 == 0) the sorted-by-expert grouped-GEMM
- * prefill path replaces the 8-row slices of gemma.py:99-112 (routing, align,
- * gate/up, down, combine launches).                                         */
+ * prefill path replaces the 8-row slices of gemma.py:99-112 (routing with
+ * the align and the x reorder, gate/up, down, combine launches).           */
 int gi_moe_layer_from_logits(const void* x, int x_dtype,
                              const void* logits, int logits_dtype,
                              const float* expert_scale,
