@@ -672,6 +672,9 @@ constexpr int kMfCols = 256;  // output columns per workgroup (64 per wave)
 constexpr int kMfRing = 8;    // k blocks in flight per wave
 constexpr int kMfPass = 96;   // k blocks per straight-line pass (K <= 3072 in one pass)
 constexpr int kMfMaxM = 16;
+constexpr int kMfXB = 16;  // staged x chunks per thread (the 64 KB LDS bound: at most 4096)
+constexpr int kMfSB = 8;   // scale entries per thread loaded in the first batch
+constexpr uint32_t kMfOob = 0xFFFFFFF0u;
 
 struct MfArgs {
   const uint16_t* A;  // [M, K] bf16
@@ -695,34 +698,83 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
   const int col0 = blockIdx.x * kMfCols;
   uint4* xs = mf_lds;                                     // [M + 1][Kp], row M zero
   uint2* ss = (uint2*)(mf_lds + (size_t)(a.M + 1) * Kp);  // [G][64]: scales of column quad c
-  // x rows in the matrix-core k order, and this workgroup's scales
-  for (int i = tid; i < (a.M + 1) * Kp; i += kMfThreads) {
-    const int n = i / Kp, r = i - n * Kp;
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (n < a.M) v = moe::mfma_k_order(*(const uint4*)(a.A + (size_t)n * a.K + 8 * r));
-    xs[i] = v;
+  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
+  const uint32_t rstep = (uint32_t)a.N * 16u;  // 4 packed rows
+  const uint32_t voff = (uint32_t)lq * (uint32_t)a.N * 4u + (uint32_t)(col0 + wave * 64 + 4 * lr) * 4u;
+  // Every start-up load goes out before any use: the x rows (one batch: the
+  // LDS bound of this path keeps them within kMfXB chunks per thread), the
+  // first kMfSB scale entries per thread and, for a one-pass K, the weight
+  // ring.  The staged values are written to LDS as they land, and the
+  // barrier waits for LDS only, so the ring stays in flight (staged one
+  // round trip at a time, the x rows and scales held every workgroup ~16
+  // memory round trips before its first weight load).  Offsets past the
+  // tensors read zeros (row M, the zero operand row, included).
+  const int nxs = (a.M + 1) * Kp, nss = a.G * (kMfCols / 4);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.A, (uint32_t)a.M * (uint32_t)a.K * 2u);
+  const __amdgpu_buffer_rsrc_t rs =
+      buffer_rsrc(a.S + col0, (uint32_t)(((size_t)(a.G - 1) * a.N + kMfCols) * 2));
+  u32x4_t xv[kMfXB];
+  {
+    // chunk i = j * kMfThreads + tid is chunk r of row n (i = n * Kp + r)
+    const int dn = kMfThreads / Kp, dr = kMfThreads - dn * Kp;
+    int n = tid / Kp, r = tid - n * Kp;
+#pragma unroll
+    for (int j = 0; j < kMfXB; ++j) {
+      const bool in = j * kMfThreads + tid < nxs && n < a.M;
+      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, in ? (uint32_t)(n * a.K + 8 * r) * 2u : kMfOob, 0, 0);
+      n += dn;
+      r += dr;
+      const bool wrap = r >= Kp;
+      r -= wrap ? Kp : 0;
+      n += wrap ? 1 : 0;
+    }
   }
-  for (int i = tid; i < a.G * (kMfCols / 4); i += kMfThreads) {
+  u32x2_t sv[kMfSB];
+#pragma unroll
+  for (int j = 0; j < kMfSB; ++j) {
+    const int i = j * kMfThreads + tid;
+    const uint32_t off = i < nss ? ((uint32_t)(i >> 6) * (uint32_t)a.N + 4u * (uint32_t)(i & 63)) * 2u : kMfOob;
+    sv[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+  }
+  uint4 w[kMfRing];
+  const bool one_pass = KB <= kMfPass;
+  if (one_pass) {
+#pragma unroll
+    for (int s = 0; s < kMfRing; ++s) {
+      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, voff + (uint32_t)s * rstep, 0, 2);
+      w[s] = make_uint4(v.x, v.y, v.z, v.w);
+    }
+  }
+  // x rows in the matrix-core k order, and this workgroup's scales
+#pragma unroll
+  for (int j = 0; j < kMfXB; ++j) {
+    const int i = j * kMfThreads + tid;
+    if (i < nxs) xs[i] = moe::mfma_k_order(make_uint4(xv[j].x, xv[j].y, xv[j].z, xv[j].w));
+  }
+#pragma unroll
+  for (int j = 0; j < kMfSB; ++j) {
+    const int i = j * kMfThreads + tid;
+    if (i < nss) ss[i] = make_uint2(sv[j].x, sv[j].y);
+  }
+  for (int i = kMfSB * kMfThreads + tid; i < nss; i += kMfThreads) {
     const int g = i >> 6, c = i & 63;
     ss[i] = *(const uint2*)(a.S + (size_t)g * a.N + col0 + 4 * c);
   }
-  __syncthreads();
+  lds_barrier();
 
   const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
   const uint4* xrow = xs + (size_t)(lr < a.M ? lr : a.M) * Kp + lq;
   const uint2* srow = ss + wave * 16 + lr;
-  const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
-  const uint32_t rstep = (uint32_t)a.N * 16u;  // 4 packed rows
-  const uint32_t voff = (uint32_t)lq * (uint32_t)a.N * 4u + (uint32_t)(col0 + wave * 64 + 4 * lr) * 4u;
   f32x4_t y[4] = {zf, zf, zf, zf};
   for (int kp = 0; kp < KB; kp += kMfPass) {
-    uint4 w[kMfRing];
+    if (!one_pass) {
 #pragma unroll
-    for (int s = 0; s < kMfRing; ++s) {
-      const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, voff + (uint32_t)(kp + s) * rstep, 0, 2);
-      w[s] = make_uint4(v.x, v.y, v.z, v.w);
+      for (int s = 0; s < kMfRing; ++s) {
+        const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rb, voff + (uint32_t)(kp + s) * rstep, 0, 2);
+        w[s] = make_uint4(v.x, v.y, v.z, v.w);
+      }
     }
     f32x4_t D[4] = {zf, zf, zf, zf};
     f32x4_t Db = zf;
@@ -1124,7 +1176,10 @@ bool mfma_path(int M, int K, int N, int gs, int G) {
   // 32-bit buffer offsets, including reads past the last row of a pass
   const long long kb_pad = (long long)(K / 32 + kMfPass - 1) / kMfPass * kMfPass;
   if (kb_pad * 4 * N * 4 >= (1LL << 32)) return false;
+  // 32-bit offsets into the scales (one workgroup's columns over all groups)
+  if ((long long)G * N * 2 >= (1LL << 32)) return false;
   const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)G * (kMfCols / 4) * 8;
+  static_assert((size_t)kMfXB * kMfThreads * 16 >= 64 * 1024, "the x rows fit one staging batch");
   return lds <= 64 * 1024;
 }
 
