@@ -308,17 +308,22 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
   uint4 wr[kPRing], ar[kPChunk];
   const int nch = (KB + kPChunk - 1) / kPChunk;
   __syncthreads();  // the previous call's readers of the chunk buffers are done
+  // issue order: the first chunk's A tiles, the weight ring, the next chunk's
+  // A tiles; the first chunk is written to LDS as soon as it lands (the
+  // weight ring is not waited for there: its latency overlaps the A tiles')
+  uint4 a0[kPChunk];
   if (loader) {
-    uint4 a0[kPChunk];
 #pragma unroll
     for (int j = 0; j < kPChunk; ++j) a0[j] = row_operand(ra, own(j), j, lq);
+  }
+#pragma unroll
+  for (int s = 0; s < kPRing; ++s) wr[s] = wload(s);
+  if (loader) {
 #pragma unroll
     for (int j = 0; j < kPChunk; ++j) ar[j] = row_operand(ra, own(kPChunk + j), kPChunk + j, lq);
 #pragma unroll
     for (int j = 0; j < kPChunk; ++j) abuf(0, j, wave) = a0[j];
   }
-#pragma unroll
-  for (int s = 0; s < kPRing; ++s) wr[s] = wload(s);
 #pragma unroll 1
   for (int c = 0; c < nch; ++c) {
     lds_barrier();  // chunk c is in its buffer; every reader of chunk c - 1 is done
