@@ -667,12 +667,12 @@ int launch_narrow(const void* A, int M, int K, int gs, float cap, const NarrowSe
 // are dropped like the reference's kernels (marlin.cu:128).
 // ---------------------------------------------------------------------------
 using moe::f32x4_t;
-constexpr int kMfThreads = 256;
-constexpr int kMfCols = 256;  // output columns per workgroup (64 per wave)
-constexpr int kMfRing = 8;    // k blocks in flight per wave
+constexpr int kMfThreads = 256;  // the 4-wave form (the 8-wave form: twice both)
+constexpr int kMfCols = 256;     // output columns per workgroup (64 per wave)
+constexpr int kMfRing = 8;       // k blocks in flight per wave
 constexpr int kMfPass = 96;   // k blocks per straight-line pass (K <= 3072 in one pass)
 constexpr int kMfMaxM = 16;
-constexpr int kMfXB = 16;  // staged x chunks per thread (the 64 KB LDS bound: at most 4096)
+constexpr int kMfXChunks = 4096;  // staged x chunks per workgroup at most (the 64 KB LDS bound)
 constexpr int kMfSB = 8;   // scale entries per thread loaded in the first batch
 constexpr uint32_t kMfOob = 0xFFFFFFF0u;
 
@@ -689,38 +689,46 @@ struct MfArgs {
   int ks;       // K slices over gridDim.y
 };
 
-template <int KPG>
-__global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
+// NW waves per workgroup (4 or 8): 64 NW columns.  With 8 waves a 512-column
+// workgroup stages x once for twice the columns and the lm_head grid (512
+// workgroups, two per CU) is one round; with 4 waves (256 columns) its 1024
+// workgroups, three per CU by LDS, ran a third-full second round.
+template <int KPG, int NW>
+__global__ __launch_bounds__(NW * kWave, 2) void w4a16_mfma_kernel(MfArgs a) {
+  constexpr int T = NW * kWave, kCols = 64 * NW, kQuads = 16 * NW;
+  constexpr int kXB = kMfXChunks / T;  // staged x chunks per thread
+  constexpr int kQsh = NW == 8 ? 7 : 6;
+  static_assert(kQuads == 1 << kQsh, "quads per group are a power of two");
   extern __shared__ uint4 mf_lds[];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
   const int Kp = a.K >> 3, KB = a.K >> 5;
-  const int col0 = blockIdx.x * kMfCols;
+  const int col0 = blockIdx.x * kCols;
   uint4* xs = mf_lds;                                     // [M + 1][Kp], row M zero
-  uint2* ss = (uint2*)(mf_lds + (size_t)(a.M + 1) * Kp);  // [G][64]: scales of column quad c
+  uint2* ss = (uint2*)(mf_lds + (size_t)(a.M + 1) * Kp);  // [G][kQuads]: scales of column quad c
   const __amdgpu_buffer_rsrc_t rb = buffer_rsrc(a.B, a.b_bytes);
   const uint32_t rstep = (uint32_t)a.N * 16u;  // 4 packed rows
   const uint32_t voff = (uint32_t)lq * (uint32_t)a.N * 4u + (uint32_t)(col0 + wave * 64 + 4 * lr) * 4u;
   // Every start-up load goes out before any use: the x rows (one batch: the
-  // LDS bound of this path keeps them within kMfXB chunks per thread), the
+  // LDS bound of this path keeps them within kXB chunks per thread), the
   // first kMfSB scale entries per thread and, for a one-pass K, the weight
   // ring.  The staged values are written to LDS as they land, and the
   // barrier waits for LDS only, so the ring stays in flight (staged one
   // round trip at a time, the x rows and scales held every workgroup ~16
   // memory round trips before its first weight load).  Offsets past the
   // tensors read zeros (row M, the zero operand row, included).
-  const int nxs = (a.M + 1) * Kp, nss = a.G * (kMfCols / 4);
+  const int nxs = (a.M + 1) * Kp, nss = a.G * kQuads;
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(a.A, (uint32_t)a.M * (uint32_t)a.K * 2u);
   const __amdgpu_buffer_rsrc_t rs =
-      buffer_rsrc(a.S + col0, (uint32_t)(((size_t)(a.G - 1) * a.N + kMfCols) * 2));
-  u32x4_t xv[kMfXB];
+      buffer_rsrc(a.S + col0, (uint32_t)(((size_t)(a.G - 1) * a.N + kCols) * 2));
+  u32x4_t xv[kXB];
   {
-    // chunk i = j * kMfThreads + tid is chunk r of row n (i = n * Kp + r)
-    const int dn = kMfThreads / Kp, dr = kMfThreads - dn * Kp;
+    // chunk i = j * T + tid is chunk r of row n (i = n * Kp + r)
+    const int dn = T / Kp, dr = T - dn * Kp;
     int n = tid / Kp, r = tid - n * Kp;
 #pragma unroll
-    for (int j = 0; j < kMfXB; ++j) {
-      const bool in = j * kMfThreads + tid < nxs && n < a.M;
+    for (int j = 0; j < kXB; ++j) {
+      const bool in = j * T + tid < nxs && n < a.M;
       xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, in ? (uint32_t)(n * a.K + 8 * r) * 2u : kMfOob, 0, 0);
       n += dn;
       r += dr;
@@ -732,8 +740,9 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
   u32x2_t sv[kMfSB];
 #pragma unroll
   for (int j = 0; j < kMfSB; ++j) {
-    const int i = j * kMfThreads + tid;
-    const uint32_t off = i < nss ? ((uint32_t)(i >> 6) * (uint32_t)a.N + 4u * (uint32_t)(i & 63)) * 2u : kMfOob;
+    const int i = j * T + tid;
+    const uint32_t off =
+        i < nss ? ((uint32_t)(i >> kQsh) * (uint32_t)a.N + 4u * (uint32_t)(i & (kQuads - 1))) * 2u : kMfOob;
     sv[j] = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
   }
   uint4 w[kMfRing];
@@ -747,17 +756,17 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
   }
   // x rows in the matrix-core k order, and this workgroup's scales
 #pragma unroll
-  for (int j = 0; j < kMfXB; ++j) {
-    const int i = j * kMfThreads + tid;
+  for (int j = 0; j < kXB; ++j) {
+    const int i = j * T + tid;
     if (i < nxs) xs[i] = moe::mfma_k_order(make_uint4(xv[j].x, xv[j].y, xv[j].z, xv[j].w));
   }
 #pragma unroll
   for (int j = 0; j < kMfSB; ++j) {
-    const int i = j * kMfThreads + tid;
+    const int i = j * T + tid;
     if (i < nss) ss[i] = make_uint2(sv[j].x, sv[j].y);
   }
-  for (int i = kMfSB * kMfThreads + tid; i < nss; i += kMfThreads) {
-    const int g = i >> 6, c = i & 63;
+  for (int i = kMfSB * T + tid; i < nss; i += T) {
+    const int g = i >> kQsh, c = i & (kQuads - 1);
     ss[i] = *(const uint2*)(a.S + (size_t)g * a.N + col0 + 4 * c);
   }
   lds_barrier();
@@ -794,7 +803,7 @@ __global__ __launch_bounds__(kMfThreads, 2) void w4a16_mfma_kernel(MfArgs a) {
         if ((j + 1) % KPG == 0 || kb == KB - 1) {
           const int g = kb / KPG;
           if (g < a.G) {
-            const uint2 sv = srow[g * 64];
+            const uint2 sv = srow[g * kQuads];
             const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
@@ -1179,7 +1188,7 @@ bool mfma_path(int M, int K, int N, int gs, int G) {
   // 32-bit offsets into the scales (one workgroup's columns over all groups)
   if ((long long)G * N * 2 >= (1LL << 32)) return false;
   const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)G * (kMfCols / 4) * 8;
-  static_assert((size_t)kMfXB * kMfThreads * 16 >= 64 * 1024, "the x rows fit one staging batch");
+  static_assert((size_t)kMfXChunks * 16 >= 64 * 1024, "the x rows fit one staging batch");
   return lds <= 64 * 1024;
 }
 
@@ -1273,11 +1282,19 @@ int launch_w4a16(const void* A, const int32_t* B, const void* scales, int n_grou
     k.G = n_groups;
     k.b_bytes = (uint32_t)((size_t)(K / 8) * N * 4);
     k.cap = softcap;
-    const size_t lds = (size_t)(M + 1) * (K / 8) * 16 + (size_t)n_groups * (kMfCols / 4) * 8;
-    if (gs == 64)
-      hipLaunchKernelGGL(w4a16_mfma_kernel<2>, dim3(N / kMfCols), dim3(kMfThreads), lds, stream, k);
-    else
-      hipLaunchKernelGGL(w4a16_mfma_kernel<4>, dim3(N / kMfCols), dim3(kMfThreads), lds, stream, k);
+    // 8 waves (512 columns) where N and LDS allow, else 4 (256 columns)
+    const size_t xl = (size_t)(M + 1) * (K / 8) * 16;
+    const size_t lds8 = xl + (size_t)n_groups * (2 * kMfCols / 4) * 8;
+    const bool w8 = N % (2 * kMfCols) == 0 && lds8 <= 64 * 1024;
+    const size_t lds = w8 ? lds8 : xl + (size_t)n_groups * (kMfCols / 4) * 8;
+    const dim3 grid(N / (w8 ? 2 * kMfCols : kMfCols)), block(w8 ? 2 * kMfThreads : kMfThreads);
+    if (gs == 64) {
+      if (w8) hipLaunchKernelGGL((w4a16_mfma_kernel<2, 8>), grid, block, lds, stream, k);
+      else hipLaunchKernelGGL((w4a16_mfma_kernel<2, 4>), grid, block, lds, stream, k);
+    } else {
+      if (w8) hipLaunchKernelGGL((w4a16_mfma_kernel<4, 8>), grid, block, lds, stream, k);
+      else hipLaunchKernelGGL((w4a16_mfma_kernel<4, 4>), grid, block, lds, stream, k);
+    }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return hip_fail(e, "w4a16 matrix-core launch");
     return GI_OK;
