@@ -55,7 +55,7 @@ struct PfArgs {
   const int* offsets;  // [E + 1] first position of each expert
   const int* order;    // [P] pair at each position
   uint16_t* act;       // [P][I] bf16, positions in expert order, chunks in k order
-  float* y;            // [P][H] fp32
+  float* y;            // [P][H] fp32, row = pair index
   int M, H, I, E, top_k, Ggu, Gd, gsh;  // group size = 32 << gsh
   uint32_t x_bytes, gu_bytes, gu_total, dn_bytes, dn_total, act_bytes;
 };
@@ -73,17 +73,16 @@ struct PfRoute {
 // ---------------------------------------------------------------------------
 constexpr int kAlignPer = 8;  // pairs per thread kept in registers
 
-// Per-expert offsets [E + 1], the pairs of each expert (order: pos -> pair)
-// and the inverse map (posmap: pair -> pos, -1 for an id outside [0, E),
-// skipped as at marlin.cu:288-289); load_id(p) reads pair p's id.
+// Per-expert offsets [E + 1] and the pairs of each expert (order: pos ->
+// pair; ids outside [0, E) are skipped as at marlin.cu:288-289); load_id(p)
+// reads pair p's id.
 struct AlignLds {
   int cnt[1024];
   int fill[1024];
   int wsum[kAlignThreads / kWave];
 };
 template <class LoadId>
-__device__ __forceinline__ void align_block(LoadId load_id, int P, int E, int* offsets, int* order, int* posmap,
-                                            AlignLds& s) {
+__device__ __forceinline__ void align_block(LoadId load_id, int P, int E, int* offsets, int* order, AlignLds& s) {
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += kAlignThreads) {
     s.cnt[e] = 0;
@@ -138,24 +137,14 @@ __device__ __forceinline__ void align_block(LoadId load_id, int P, int E, int* o
       const int p = tid + kAlignThreads * i;
       if (p < P) {
         const int e = ev[i];
-        int pos = -1;
-        if (e >= 0 && e < E) {
-          pos = s.cnt[e] + atomicAdd(&s.fill[e], 1);
-          order[pos] = p;
-        }
-        posmap[p] = pos;
+        if (e >= 0 && e < E) order[s.cnt[e] + atomicAdd(&s.fill[e], 1)] = p;
       }
     }
     return;
   }
   for (int p = tid; p < P; p += kAlignThreads) {
     const int e = load_id(p);
-    int pos = -1;
-    if (e >= 0 && e < E) {
-      pos = s.cnt[e] + atomicAdd(&s.fill[e], 1);
-      order[pos] = p;
-    }
-    posmap[p] = pos;
+    if (e >= 0 && e < E) order[s.cnt[e] + atomicAdd(&s.fill[e], 1)] = p;
   }
 }
 
@@ -171,7 +160,6 @@ struct PfFront {
   int idx_is64, P;
   int* offsets;          // [E + 1]
   int* order;            // [P]
-  int* posmap;           // [P]
   int* arrive;           // arrivals of the routing workgroups (zero between launches)
   const uint4* x;
   uint4* xk;             // x with each 8-value chunk in the matrix-core k order
@@ -200,8 +188,7 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_front_kernel(PfFront f)
   }
   const int E = f.r.E;
   if (f.nroute == 0) {
-    align_block([&](int p) { return load_expert_id(f.idx, f.idx_is64, p); }, f.P, E, f.offsets, f.order, f.posmap,
-                als);
+    align_block([&](int p) { return load_expert_id(f.idx, f.idx_is64, p); }, f.P, E, f.offsets, f.order, als);
     return;
   }
   const int t = blockIdx.x * (kAlignThreads / kWave) + wave;
@@ -221,7 +208,7 @@ __global__ __launch_bounds__(kAlignThreads) void prefill_front_kernel(PfFront f)
   if (tid == 0) store_relaxed(f.arrive, 0);  // every routing workgroup has arrived: zero for the next launch
   const int32_t* ids = f.out_idx;
   align_block([&](int p) { return __hip_atomic_load(ids + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }, f.P, E,
-              f.offsets, f.order, f.posmap, als);
+              f.offsets, f.order, als);
 }
 
 // ---------------------------------------------------------------------------
@@ -469,10 +456,13 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
 }
 
 // down: workgroup (unit d, expert e) owns output columns [256d, 256d+256);
-// y[pos] fp32 rows of the expert's pairs.
+// y fp32 rows of the expert's pairs, at each pair's index.
 template <int GSH>
 __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
   __shared__ uint4 aring[2 * kPChunk * kPRT * 64];
+  // the pair of each row of a pass, in the chunk buffers once the products
+  // are done (no LDS beyond theirs: the 160 KB limit check counts them only)
+  int* prow = reinterpret_cast<int*>(aring);
   extern __shared__ uint2 dsc[];  // [Gd][64]: 4 scales of each column quad
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid >> 6;
   const int lq = lane >> 4, lr = lane & 15;
@@ -490,38 +480,45 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
   const uint32_t wbase = ((uint32_t)lq * a.H + col) * 4u;
   const uint32_t wstep = (uint32_t)a.H * 16u;
   for (int base = 0; base < n_e; base += 16 * kPRT) {
+    // each row's pair index (its result row): loaded here, written to LDS
+    // after the products (the load must not hold the products' first loads)
+    const int pr = tid < 16 * kPRT && base + tid < n_e ? a.order[off_e + base + tid] : 0;
     const int jo = base + 16 * wave + lr;
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(off_e + jo) * (uint32_t)a.I * 2u : kOob;
     f32x4_t y[kPRT][4];
     grouped_products<kPRingDn, GSH>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, a.I >> 5,
                                              a.Gd, dsc, aring, y);
+    lds_barrier();  // every wave's last reads of the chunk buffers are done
+    if (tid < 16 * kPRT) prow[tid] = pr;
+    lds_barrier();  // (the next pass's products start with a barrier before they write the buffers)
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
         const int j = base + 16 * rt + 4 * lq + jj;
         if (live && j < n_e)
-          *(float4*)(a.y + (size_t)(off_e + j) * a.H + col) =
+          *(float4*)(a.y + (size_t)prow[16 * rt + 4 * lq + jj] * a.H + col) =
               make_float4(y[rt][0][jj], y[rt][1][jj], y[rt][2][jj], y[rt][3][jj]);
       }
   }
 }
 
 // ---------------------------------------------------------------------------
-// combine: out[t] (+)= sum over slots, in slot order, of w * y[pos]
+// combine: out[t] (+)= sum over slots, in slot order, of w * y[pair]
 // ---------------------------------------------------------------------------
-// A pair's routing as the combine reads it: the position of its result row
-// (-1: its id is outside [0, E), skipped as at marlin.cu:288-289) and its
-// weight rounded to bf16 (marlin.cu:631-636), read from the caller's (or the
-// routed) weights.
+// A pair's routing as the combine reads it: whether its id is in [0, E)
+// (other ids are skipped, marlin.cu:288-289) and its weight rounded to bf16
+// (marlin.cu:631-636), from the caller's (or the routed) ids and weights.
+// Its result row is the pair index itself.
 struct PfSlots {
-  const int* posmap;
+  const void* idx;
   const void* w;
-  int w_dtype;
+  int idx_is64, w_dtype, E;
 };
-__device__ __forceinline__ void slot_of(const PfSlots& s, int p, int& pos, float& wv) {
-  pos = s.posmap[p];
+__device__ __forceinline__ void slot_of(const PfSlots& s, int p, int& ok, float& wv) {
+  const int id = load_expert_id(s.idx, s.idx_is64, p);
   wv = load_weight_as_bf16(s.w, s.w_dtype, p);
+  ok = id >= 0 && id < s.E;
 }
 
 __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, PfSlots sl, uint16_t* out, int H,
@@ -533,11 +530,11 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, Pf
                                        bf16_to_f32(out[(size_t)t * H + c + 2]), bf16_to_f32(out[(size_t)t * H + c + 3]));
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < top_k; ++k) {
-      int pos;
+      int ok;
       float wv;
-      slot_of(sl, t * top_k + k, pos, wv);
-      if (pos < 0) continue;
-      const float4 v = *(const float4*)(y + (size_t)pos * H + c);
+      slot_of(sl, t * top_k + k, ok, wv);
+      const float4 v = *(const float4*)(y + (size_t)(t * top_k + k) * H + c);
+      if (!ok) continue;
       acc.x += wv * v.x;
       acc.y += wv * v.y;
       acc.z += wv * v.z;
@@ -554,41 +551,35 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const float* y, Pf
 }
 
 // The same for top_k <= 8 with every load of the workgroup issued before any
-// use: the token's slot positions and weights are read once, then the three
-// column chunks of each thread (H <= 3072 per pass) over all slots, and the
-// previous output, go out together (one memory round trip instead of one per
-// chunk).  Same arithmetic and order as prefill_combine_kernel.
+// use: a slot's result row is its pair index, so the three column chunks of
+// each thread (H <= 3072 per pass) over all slots and the previous output go
+// out together with the slots' ids and weights (one memory round trip).  A
+// skipped slot's row is read and not used.  Same arithmetic and order as
+// prefill_combine_kernel.
 constexpr int kCombineSlots = 8;
 constexpr int kCombineChunks = 3;
 __global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, PfSlots sl, uint16_t* out, int H,
                                                                int top_k, int overwrite) {
   const int t = blockIdx.x;
-  __shared__ int spos[kCombineSlots];
+  __shared__ int sok[kCombineSlots];
   __shared__ float swt[kCombineSlots];
-  if (threadIdx.x < kCombineSlots) {
-    int pos = -1;
-    float wv = 0.f;
-    if ((int)threadIdx.x < top_k) slot_of(sl, t * top_k + threadIdx.x, pos, wv);
-    spos[threadIdx.x] = pos;
-    swt[threadIdx.x] = wv;
-  }
-  __syncthreads();
-  int pos[kCombineSlots];
-  float wv[kCombineSlots];
-#pragma unroll
-  for (int k = 0; k < kCombineSlots; ++k) {
-    pos[k] = __builtin_amdgcn_readfirstlane(spos[k]);
-    wv[k] = swt[k];
-  }
+  int okv = 0;
+  float wvv = 0.f;
+  if ((int)threadIdx.x < top_k) slot_of(sl, t * top_k + threadIdx.x, okv, wvv);
   const __amdgpu_buffer_rsrc_t ro = buffer_rsrc(out + (size_t)t * H, overwrite ? 0u : (uint32_t)H * 2u);
-  for (int c0 = threadIdx.x * 4; c0 < H; c0 += 256 * 4 * kCombineChunks) {
+  constexpr int kStep = 256 * 4 * kCombineChunks;
+  const int nit = (H + kStep - 1) / kStep;  // the same for every thread (the barrier below)
+  int ok[kCombineSlots];
+  float wv[kCombineSlots];
+  for (int it = 0; it < nit; ++it) {
+    const int c0 = threadIdx.x * 4 + it * kStep;
     u32x4_t v[kCombineChunks][kCombineSlots];
     u32x2_t o[kCombineChunks];
 #pragma unroll
     for (int k = 0; k < kCombineSlots; ++k) {
       // a row's resource (its offsets stay below 2^32 whatever the row count)
       const __amdgpu_buffer_rsrc_t ry =
-          buffer_rsrc(y + (size_t)max(pos[k], 0) * H, pos[k] >= 0 ? (uint32_t)H * 4u : 0u);
+          buffer_rsrc(y + (size_t)(t * top_k + (k < top_k ? k : 0)) * H, k < top_k ? (uint32_t)H * 4u : 0u);
 #pragma unroll
       for (int i = 0; i < kCombineChunks; ++i) {
         const int c = c0 + i * 1024;
@@ -600,6 +591,18 @@ __global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, P
       const int c = c0 + i * 1024;
       o[i] = __builtin_amdgcn_raw_buffer_load_b64(ro, c < H ? (uint32_t)c * 2u : kOob, 0, 0);
     }
+    if (it == 0) {
+      if (threadIdx.x < kCombineSlots) {
+        sok[threadIdx.x] = okv;
+        swt[threadIdx.x] = wvv;
+      }
+      lds_barrier();  // LDS only: the row loads stay in flight
+#pragma unroll
+      for (int k = 0; k < kCombineSlots; ++k) {
+        ok[k] = __builtin_amdgcn_readfirstlane(sok[k]);
+        wv[k] = swt[k];
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kCombineChunks; ++i) {
       const int c = c0 + i * 1024;
@@ -609,7 +612,7 @@ __global__ __launch_bounds__(256) void prefill_combine8_kernel(const float* y, P
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
       for (int k = 0; k < kCombineSlots; ++k) {
-        if (pos[k] < 0) continue;
+        if (!ok[k]) continue;
         acc.x += wv[k] * __uint_as_float(v[i][k].x);
         acc.y += wv[k] * __uint_as_float(v[i][k].y);
         acc.z += wv[k] * __uint_as_float(v[i][k].z);
@@ -630,7 +633,7 @@ constexpr size_t kPAlign = 256;
 inline size_t pround(size_t v) { return (v + kPAlign - 1) / kPAlign * kPAlign; }
 
 struct PfLayout {
-  size_t idx, w, offsets, order, posmap, xk, act, y, total;
+  size_t idx, w, offsets, order, xk, act, y, total;
 };
 PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   const size_t P = (size_t)M * top_k;
@@ -639,8 +642,7 @@ PfLayout pf_layout(int M, int top_k, int H, int I, int E) {
   l.w = pround(l.idx + P * 4);
   l.offsets = pround(l.w + P * 2);
   l.order = pround(l.offsets + (size_t)(E + 1) * 4);
-  l.posmap = pround(l.order + P * 4);
-  l.xk = pround(l.posmap + P * 4);
+  l.xk = pround(l.order + P * 4);
   l.act = pround(l.xk + (size_t)M * H * 2);
   l.y = pround(l.act + P * I * 2);
   l.total = pround(l.y + P * H * 4);
@@ -713,10 +715,8 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes, i
   f.P = P;
   int* offsets = (int*)(ws + L.offsets);
   int* order = (int*)(ws + L.order);
-  int* posmap = (int*)(ws + L.posmap);
   f.offsets = offsets;
   f.order = order;
-  f.posmap = posmap;
   f.arrive = arrive;
   f.x = (const uint4*)h.x;
   f.xk = (uint4*)(ws + L.xk);
@@ -771,7 +771,7 @@ int launch_moe_prefill(const MoeHostArgs& h, void* workspace, size_t ws_bytes, i
   }
   e = hipGetLastError();
   if (e != hipSuccess) return hip_fail(e, "prefill down launch");
-  const PfSlots sl{posmap, w, w_dtype};
+  const PfSlots sl{f.idx, w, f.idx_is64, w_dtype, h.E};
   if (h.top_k <= kCombineSlots)
     hipLaunchKernelGGL(prefill_combine8_kernel, dim3(h.M), dim3(256), 0, h.stream, k.y, sl, (uint16_t*)h.out, h.H,
                        h.top_k, h.overwrite);

@@ -217,11 +217,13 @@ def test_prefill_duplicates_invalid_skewed(small):
 
 
 @pytest.mark.parametrize("m,top_k,idx_dtype", [(1024, 8, torch.int32), (1025, 8, torch.int64),
-                                               (1100, 4, torch.int32), (64, 1, torch.int64)])
+                                               (1100, 4, torch.int32), (64, 1, torch.int64),
+                                               (96, 16, torch.int32)])
 def test_prefill_many_pairs_and_heavy_expert(small, m, top_k, idx_dtype):
     """The front launch's align sorts up to 8192 (token, slot) pairs from
     registers (1024 x 8 is the largest such call, 64 x 1 the smallest prefill
-    call) and more in a loop (1025 x 8).  Eight experts take ~500-1000 pairs
+    call) and more in a loop (1025 x 8); top_k 16 takes the combine's general
+    form.  Eight experts take ~500-1000 pairs
     each, i.e. 11-22 passes of 48 pairs per workgroup, and one expert takes
     most of them; ids outside [0, E) are skipped, duplicate ids within a
     token each count, and the output is the same on a second call."""
