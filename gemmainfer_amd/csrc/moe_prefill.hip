@@ -311,6 +311,24 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
 #pragma unroll
     for (int j = 0; j < kPChunk; ++j) abuf(0, j, wave) = a0[j];
   }
+  if (!wlive) {
+    // a wave with no columns (the last column tile when I is not a multiple
+    // of 128): its share of the A staging and the barriers, no products
+    // (the issue slots go to the other waves of its SIMD); y stays zero
+#pragma unroll 1
+    for (int c = 0; c < nch; ++c) {
+      lds_barrier();
+      if (loader) {
+        const int kn = (c + 2) * kPChunk;
+#pragma unroll
+        for (int j = 0; j < kPChunk; ++j) {
+          abuf(c + 1, j, wave) = ar[j];
+          ar[j] = row_operand(ra, own(kn + j), kn + j, lq);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll 1
   for (int c = 0; c < nch; ++c) {
     lds_barrier();  // chunk c is in its buffer; every reader of chunk c - 1 is done
@@ -427,14 +445,17 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
   const int col = quad_col(16 * wave + lr);
   const uint32_t wbase = ((uint32_t)lq * twoI + col) * 4u;
   const uint32_t wstep = (uint32_t)twoI * 16u;  // 4 packed rows
+  // a wave whose 64 gate (or up) columns all lie past I (the last tile when
+  // I is not a multiple of 128) has no products to run
+  const bool glive = 128 * tile + 64 * (wave & 1) < a.I;
   for (int base = 0; base < n_e; base += 16 * kPRT) {
     // this wave's row tile (waves < kPRT load the A operands for all)
     const int jo = base + 16 * wave + lr;
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(a.order[off_e + jo] / a.top_k) * (uint32_t)a.H * 2u
                                                  : kOob;
     f32x4_t y[kPRT][4];
-    grouped_products<kPRingGu, GSH>(rw, wbase, wstep, e * a.gu_bytes, rx, roff, a.H >> 5, a.Ggu, gsc,
-                                            aring, y);
+    grouped_products<kPRingGu, GSH>(rw, glive ? wbase : kOob, wstep, e * a.gu_bytes, rx, roff, a.H >> 5,
+                                            a.Ggu, gsc, aring, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       __syncthreads();
