@@ -245,9 +245,10 @@ __device__ __forceinline__ uint4 row_operand(__amdgpu_buffer_rsrc_t r, uint32_t 
 // two chunk buffers [2][kPChunk][kPRT][64] uint4.  The group size (32 <<
 // GSH) is a compile-time value, so every group end inside a chunk is known to
 // the compiler (a chunk holds whole groups); a last partial group is finished
-// at K.  Every row tile is multiplied (rows past the expert's pairs
-// are zeros): no branch on the tile count.
-template <int kPRing, int GSH>
+// at K.  The first RT row tiles are multiplied (rows past the expert's pairs
+// are zeros): RT is a compile-time value, so the loop has no branch on the
+// tile count (a branch inside it split the scheduling region: slower).
+template <int kPRing, int GSH, int RT>
 __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint32_t wbase, uint32_t wstep,
                                                  uint32_t wsoff, __amdgpu_buffer_rsrc_t ra, uint32_t roff_own,
                                                  int KB, int G, const uint2* sc_lds, uint4* aring,
@@ -255,7 +256,7 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
   constexpr int kKbpg = 1 << GSH;
   const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x >> 6;
   const int lq = lane >> 4, lr = lane & 15;
-  const bool loader = wave < kPRT;
+  const bool loader = wave < RT;
   const uint32_t mq = q4_magic();
   const f32x4_t zf = {0.f, 0.f, 0.f, 0.f};
   const uint4 bc = make_uint4(moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair, moe::kQ4BiasPair);
@@ -275,7 +276,7 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
     const uint2 sv = g < G ? sc_lds[g * 64 + 16 * wave + lr] : make_uint2(0u, 0u);
     const float sc[4] = {bf16lo(sv.x), bf16hi(sv.x), bf16lo(sv.y), bf16hi(sv.y)};
 #pragma unroll
-    for (int rt = 0; rt < kPRT; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -348,7 +349,7 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
       const uint4 q2 = moe::q4_operand(w.z, mq), q3 = moe::q4_operand(w.w, mq);
       const bool gstart = j % kKbpg == 0;  // compile-time: a group's first product starts from zero
 #pragma unroll
-      for (int rt = 0; rt < kPRT; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         const uint4 A = abuf(c, j, rt);
         D[rt][0] = moe::mfma_bf16(A, q0, gstart ? zf : D[rt][0]);
         D[rt][1] = moe::mfma_bf16(A, q1, gstart ? zf : D[rt][1]);
@@ -362,7 +363,7 @@ __device__ __forceinline__ void grouped_products(__amdgpu_buffer_rsrc_t rw, uint
       // unpack first: gate/up 111-113 -> 108 us at M=512)
       __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);  // LDS reads
 #pragma unroll
-      for (int p = 0; p < 5 * kPRT; ++p) {
+      for (int p = 0; p < 5 * RT; ++p) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one matrix-core product
         __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
       }
@@ -454,8 +455,10 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_gu_kernel(PfArgs a) {
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(a.order[off_e + jo] / a.top_k) * (uint32_t)a.H * 2u
                                                  : kOob;
     f32x4_t y[kPRT][4];
-    grouped_products<kPRingGu, GSH>(rw, glive ? wbase : kOob, wstep, e * a.gu_bytes, rx, roff, a.H >> 5,
-                                            a.Ggu, gsc, aring, y);
+    // (all three row tiles: a second instantiation for passes of at most 32
+    // pairs, as in down, made this kernel spill and measured slower)
+    grouped_products<kPRingGu, GSH, kPRT>(rw, glive ? wbase : kOob, wstep, e * a.gu_bytes, rx, roff, a.H >> 5,
+                                          a.Ggu, gsc, aring, y);
 #pragma unroll
     for (int rt = 0; rt < kPRT; ++rt) {
       __syncthreads();
@@ -507,8 +510,14 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_down_kernel(PfArgs a) {
     const int jo = base + 16 * wave + lr;
     const uint32_t roff = wave < kPRT && jo < n_e ? (uint32_t)(off_e + jo) * (uint32_t)a.I * 2u : kOob;
     f32x4_t y[kPRT][4];
-    grouped_products<kPRingDn, GSH>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, a.I >> 5,
-                                             a.Gd, dsc, aring, y);
+    // two row tiles when the pass has at most 32 pairs (half the experts at
+    // M = 512): a third fewer products and epilogue operations
+    if (n_e - base <= 32)
+      grouped_products<kPRingDn, GSH, 2>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, a.I >> 5,
+                                         a.Gd, dsc, aring, y);
+    else
+      grouped_products<kPRingDn, GSH, kPRT>(rw, live ? wbase : kOob, wstep, e * a.dn_bytes, ra, roff, a.I >> 5,
+                                            a.Gd, dsc, aring, y);
     lds_barrier();  // every wave's last reads of the chunk buffers are done
     if (tid < 16 * kPRT) prow[tid] = pr;
     lds_barrier();  // (the next pass's products start with a barrier before they write the buffers)
